@@ -1,0 +1,684 @@
+// C ABI of libbarq_rocm (include/barq_rocm.h): argument checking, memory
+// staging for host buffers, workspace management and kernel dispatch.
+#include "../../include/barq_rocm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "launch.hpp"
+
+struct barq_rocm_handle {
+    int device = 0;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;        // device workspace, grown on demand
+    size_t ws_size = 0;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() { return BARQ_OK; }
+
+#define BARQ_HIP(expr)                                                                          \
+    do {                                                                                        \
+        hipError_t e_ = (expr);                                                                 \
+        if (e_ != hipSuccess) return fail(BARQ_E_BACKEND, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define BARQ_CHECK(rc_expr)          \
+    do {                             \
+        int rc_ = (rc_expr);         \
+        if (rc_ != BARQ_OK) return rc_; \
+    } while (0)
+
+// Make the handle's device current for the duration of a call.
+struct DeviceGuard {
+    int prev = -1;
+    bool changed = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+            changed = hipSetDevice(dev) == hipSuccess;
+        }
+    }
+    ~DeviceGuard() {
+        if (changed) (void)hipSetDevice(prev);
+    }
+};
+
+bool is_weight_type(int t) {
+    return t == BARQ_TYPE_Q4_0 || t == BARQ_TYPE_Q8_0 || t == BARQ_TYPE_Q4_K || t == BARQ_TYPE_Q6_K ||
+           t == BARQ_TYPE_Q4_0_BARQ;
+}
+
+int q8_partner(int w_type) {
+    return (w_type == BARQ_TYPE_Q4_K || w_type == BARQ_TYPE_Q6_K) ? BARQ_TYPE_Q8_K : BARQ_TYPE_Q8_0;
+}
+
+size_t blk_elems(int t) {
+    switch (t) {
+    case BARQ_TYPE_F32: case BARQ_TYPE_F16: return 1;
+    case BARQ_TYPE_Q4_0: case BARQ_TYPE_Q8_0: case BARQ_TYPE_Q4_0_BARQ: return 32;
+    case BARQ_TYPE_Q4_K: case BARQ_TYPE_Q6_K: case BARQ_TYPE_Q8_K: return 256;
+    default: return 0;
+    }
+}
+
+size_t blk_bytes(int t) {
+    switch (t) {
+    case BARQ_TYPE_F32: return 4;
+    case BARQ_TYPE_F16: return 2;
+    case BARQ_TYPE_Q4_0: return 18;
+    case BARQ_TYPE_Q4_0_BARQ: return 20;
+    case BARQ_TYPE_Q8_0: return 34;
+    case BARQ_TYPE_Q4_K: return 144;
+    case BARQ_TYPE_Q6_K: return 210;
+    case BARQ_TYPE_Q8_K: return 292;
+    default: return 0;
+    }
+}
+
+size_t row_bytes_of(int t, size_t k) {
+    const size_t be = blk_elems(t);
+    if (!be || k % be) return 0;
+    return k / be * blk_bytes(t);
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// alignment the kernels need for a packed weight / activation buffer
+size_t weight_align(int t) {
+    switch (t) {
+    case BARQ_TYPE_Q4_K: return 16;
+    case BARQ_TYPE_Q4_0_BARQ: case BARQ_TYPE_Q8_K: case BARQ_TYPE_F32: return 4;
+    default: return 2;
+    }
+}
+
+int ensure_ws(barq_rocm_handle* h, size_t bytes) {
+    if (bytes <= h->ws_size) return ok();
+    if (h->ws) {
+        BARQ_HIP(hipStreamSynchronize(h->stream));
+        BARQ_HIP(hipFree(h->ws));
+        h->ws = nullptr;
+        h->ws_size = 0;
+    }
+    size_t want = bytes < 16 * 1024 * 1024 ? 16 * 1024 * 1024 : bytes;
+    hipError_t e = hipMalloc(&h->ws, want);
+    if (e != hipSuccess) {
+        h->ws = nullptr;
+        return fail(BARQ_E_ALLOC, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
+    }
+    h->ws_size = want;
+    return ok();
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves 256-byte aligned slices out of the workspace.
+struct Arena {
+    size_t used = 0;
+    std::vector<std::pair<size_t, size_t>> parts;  // offset, size
+    size_t add(size_t bytes) {
+        size_t off = used;
+        used = round_up(used + bytes, 256);
+        parts.push_back({off, bytes});
+        return off;
+    }
+};
+
+template <class T>
+T* at(barq_rocm_handle* h, size_t off) {
+    return reinterpret_cast<T*>(static_cast<uint8_t*>(h->ws) + off);
+}
+
+int check_handle(barq_rocm_handle* h) {
+    if (!h) return fail(BARQ_E_INVALID, "null handle");
+    return ok();
+}
+
+int check_mem(int mem) {
+    if (mem != BARQ_MEM_HOST && mem != BARQ_MEM_DEVICE) return fail(BARQ_E_INVALID, "mem must be BARQ_MEM_HOST or BARQ_MEM_DEVICE");
+    return ok();
+}
+
+int launched(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(BARQ_E_BACKEND, "%s launch: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+constexpr size_t LDS_LIMIT = 64 * 1024;
+
+}  // namespace
+
+extern "C" {
+
+int barq_rocm_abi_version(void) { return BARQ_ROCM_ABI_VERSION; }
+
+const char* barq_rocm_last_error(void) { return g_last_error.c_str(); }
+
+size_t barq_rocm_block_elems(int type) { return blk_elems(type); }
+size_t barq_rocm_block_bytes(int type) { return blk_bytes(type); }
+size_t barq_rocm_row_bytes(int type, size_t k) { return row_bytes_of(type, k); }
+
+int barq_rocm_create(int device, barq_rocm_handle** out) {
+    if (!out) return fail(BARQ_E_INVALID, "null output pointer");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) return fail(BARQ_E_UNSUPPORTED, "ROCm runtime not available: no HIP device");
+    if (device < 0 || device >= n) return fail(BARQ_E_UNSUPPORTED, "device %d out of range (%d devices)", device, n);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(BARQ_E_BACKEND, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(BARQ_E_UNSUPPORTED, "device %d is %s; libbarq_rocm is built for gfx950 only", device, prop.gcnArchName);
+    DeviceGuard g(device);
+    if (hipSetDevice(device) != hipSuccess) return fail(BARQ_E_BACKEND, "hipSetDevice(%d) failed", device);
+    auto* h = new barq_rocm_handle();
+    h->device = device;
+    e = hipStreamCreateWithFlags(&h->own, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete h;
+        return fail(BARQ_E_BACKEND, "hipStreamCreate: %s", hipGetErrorString(e));
+    }
+    h->stream = h->own;
+    *out = h;
+    return ok();
+}
+
+int barq_rocm_destroy(barq_rocm_handle* h) {
+    if (!h) return ok();
+    DeviceGuard g(h->device);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->ws) (void)hipFree(h->ws);
+    if (h->own) (void)hipStreamDestroy(h->own);
+    delete h;
+    return ok();
+}
+
+int barq_rocm_set_stream(barq_rocm_handle* h, void* stream) {
+    BARQ_CHECK(check_handle(h));
+    h->stream = stream ? static_cast<hipStream_t>(stream) : h->own;
+    return ok();
+}
+
+void* barq_rocm_get_stream(barq_rocm_handle* h) { return h ? static_cast<void*>(h->stream) : nullptr; }
+
+int barq_rocm_synchronize(barq_rocm_handle* h) {
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+int barq_rocm_dequantize(barq_rocm_handle* h, int type, const void* blocks, size_t n_elems, float* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    const size_t be = blk_elems(type);
+    if (!be || type == BARQ_TYPE_F32) return fail(BARQ_E_UNSUPPORTED, "dequantize: unsupported type %d", type);
+    if (n_elems % be || n_elems % 4) return fail(BARQ_E_QUANT, "dequantize: %zu elements is not a whole number of %zu-element blocks", n_elems, be);
+    if (n_elems == 0) return ok();
+    if (!blocks || !out) return fail(BARQ_E_INVALID, "dequantize: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const size_t in_bytes = n_elems / be * blk_bytes(type);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(blocks, type == BARQ_TYPE_F16 ? 8 : weight_align(type)) || !aligned(out, 16))
+            return fail(BARQ_E_INVALID, "dequantize: misaligned buffer (blocks %zu-byte, out 16-byte)", weight_align(type));
+        return launched(barq::dequant_launch(type, blocks, n_elems, out, h->stream), "dequantize");
+    }
+    Arena a;
+    size_t oi = a.add(in_bytes), oo = a.add(n_elems * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, oi), blocks, in_bytes, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::dequant_launch(type, at<uint8_t>(h, oi), n_elems, at<float>(h, oo), h->stream), "dequantize"));
+    BARQ_HIP(hipMemcpyAsync(out, at<float>(h, oo), n_elems * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+static hipError_t quantize_act_dev(int act_type, const float* x, size_t n_rows, size_t k, void* out, hipStream_t s) {
+    return act_type == BARQ_TYPE_Q8_0 ? barq::quantize_q8_0_launch(x, n_rows, k, out, s)
+                                      : barq::quantize_q8_k_launch(x, n_rows, k, out, s);
+}
+
+int barq_rocm_quantize_act(barq_rocm_handle* h, int act_type, const float* x, size_t n_rows, size_t k, void* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (act_type != BARQ_TYPE_Q8_0 && act_type != BARQ_TYPE_Q8_K)
+        return fail(BARQ_E_UNSUPPORTED, "quantize_act: act_type must be Q8_0 or Q8_K, got %d", act_type);
+    const size_t be = blk_elems(act_type);
+    if (k % be) return fail(BARQ_E_QUANT, "quantize_act: k=%zu is not a multiple of %zu", k, be);
+    if (n_rows == 0 || k == 0) return ok();
+    if (!x || !out) return fail(BARQ_E_INVALID, "quantize_act: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const size_t out_bytes = n_rows * row_bytes_of(act_type, k);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(x, 16) || !aligned(out, act_type == BARQ_TYPE_Q8_K ? 4 : 2))
+            return fail(BARQ_E_INVALID, "quantize_act: misaligned buffer (x 16-byte, out %d-byte)", act_type == BARQ_TYPE_Q8_K ? 4 : 2);
+        return launched(quantize_act_dev(act_type, x, n_rows, k, out, h->stream), "quantize_act");
+    }
+    Arena a;
+    size_t ox = a.add(n_rows * k * 4), oo = a.add(out_bytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, n_rows * k * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(quantize_act_dev(act_type, at<float>(h, ox), n_rows, k, at<uint8_t>(h, oo), h->stream), "quantize_act"));
+    BARQ_HIP(hipMemcpyAsync(out, at<uint8_t>(h, oo), out_bytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// matvec / matmul
+
+namespace {
+
+int check_linear(int w_type, size_t k, int act_type, const char* what) {
+    if (!is_weight_type(w_type)) return fail(BARQ_E_UNSUPPORTED, "%s: unsupported weight type %d", what, w_type);
+    if (row_bytes_of(w_type, k) == 0) return fail(BARQ_E_QUANT, "%s: k=%zu is not a multiple of the %zu-element block", what, k, blk_elems(w_type));
+    if (act_type == BARQ_ACT_F32 || act_type == BARQ_ACT_F32_Q8) return ok();
+    if (act_type != BARQ_TYPE_Q8_0 && act_type != BARQ_TYPE_Q8_K)
+        return fail(BARQ_E_UNSUPPORTED, "%s: unsupported activation type %d", what, act_type);
+    if (act_type != q8_partner(w_type))
+        return fail(BARQ_E_UNSUPPORTED, "%s: weight type %d pairs with activation type %d, got %d", what, w_type, q8_partner(w_type), act_type);
+    return ok();
+}
+
+size_t act_row_bytes(int act_type, int w_type, size_t k) {
+    if (act_type == BARQ_ACT_F32 || act_type == BARQ_ACT_F32_Q8) return k * 4;
+    return row_bytes_of(act_type, k);
+}
+
+// Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).
+int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
+               const void* x, size_t m, float* y) {
+    hipStream_t s = h->stream;
+    if (!aligned(w, weight_align(w_type))) return fail(BARQ_E_INVALID, "weights must be %zu-byte aligned", weight_align(w_type));
+    if (!aligned(y, 4)) return fail(BARQ_E_INVALID, "output must be 4-byte aligned");
+    if (act_type == BARQ_ACT_F32) {
+        if (!aligned(x, 16)) return fail(BARQ_E_INVALID, "f32 activations must be 16-byte aligned");
+        if (m == 1) {
+            if (k * 4 > LDS_LIMIT) return fail(BARQ_E_UNSUPPORTED, "f32-activation matvec supports k <= %zu", LDS_LIMIT / 4);
+            return launched(barq::gemv_f32_launch(w_type, w, n_rows, k, static_cast<const float*>(x), y, s), "gemv_f32");
+        }
+        // literal matmul: dequantize W (bit-exact) then the sequential f32 GEMM
+        BARQ_CHECK(ensure_ws(h, n_rows * k * 4));
+        float* wf = at<float>(h, 0);
+        BARQ_CHECK(launched(barq::dequant_launch(w_type, w, n_rows * k, wf, s), "dequantize"));
+        return launched(barq::gemm_f32_nt_launch(static_cast<const float*>(x), wf, m, k, n_rows, y, s), "gemm_f32_nt");
+    }
+    const int aq = q8_partner(w_type);
+    const uint8_t* xq = static_cast<const uint8_t*>(x);
+    if (act_type == BARQ_ACT_F32_Q8) {
+        if (!aligned(x, 16)) return fail(BARQ_E_INVALID, "f32 activations must be 16-byte aligned");
+        const size_t qbytes = m * row_bytes_of(aq, k);
+        BARQ_CHECK(ensure_ws(h, qbytes));
+        BARQ_CHECK(launched(quantize_act_dev(aq, static_cast<const float*>(x), m, k, h->ws, s), "quantize_act"));
+        xq = static_cast<const uint8_t*>(h->ws);
+    } else if (!aligned(x, aq == BARQ_TYPE_Q8_K ? 4 : 2)) {
+        return fail(BARQ_E_INVALID, "activation blocks misaligned");
+    }
+    if (barq::gemv_q8_lds_bytes(w_type, k) > LDS_LIMIT) return fail(BARQ_E_UNSUPPORTED, "k=%zu too large for the LDS-staged kernel", k);
+    if (m >= 16 && barq::gemm_mfma_supported(w_type, n_rows, k))
+        return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, y, s), "gemm_mfma");
+    const size_t xrb = row_bytes_of(aq, k);
+    for (size_t r = 0; r < m; r++)
+        BARQ_CHECK(launched(barq::gemv_q8_launch(w_type, w, n_rows, k, xq + r * xrb, y + r * n_rows, s), "gemv_q8"));
+    return ok();
+}
+
+int matmul_any(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
+               const void* x, size_t m, float* y, int mem, const char* what) {
+    BARQ_CHECK(check_mem(mem));
+    BARQ_CHECK(check_linear(w_type, k, act_type, what));
+    if (n_rows == 0 || m == 0) return ok();
+    if (!w || !x || !y) return fail(BARQ_E_INVALID, "%s: null buffer", what);
+    if (n_rows > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "%s: dimensions exceed 2^31", what);
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    if (mem == BARQ_MEM_DEVICE) return matmul_dev(h, w_type, w, n_rows, k, act_type, x, m, y);
+    // host buffers: stage W, x, y after the region matmul_dev itself may use
+    const size_t wbytes = n_rows * row_bytes_of(w_type, k);
+    const size_t xbytes = m * act_row_bytes(act_type, w_type, k);
+    const size_t ybytes = m * n_rows * 4;
+    const size_t scratch = act_type == BARQ_ACT_F32 && m > 1 ? n_rows * k * 4
+                           : act_type == BARQ_ACT_F32_Q8        ? m * row_bytes_of(q8_partner(w_type), k)
+                                                                : 0;
+    Arena a;
+    a.add(scratch);
+    size_t ow = a.add(wbytes), ox = a.add(xbytes), oy = a.add(ybytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ow), w, wbytes, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ox), x, xbytes, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(matmul_dev(h, w_type, at<uint8_t>(h, ow), n_rows, k, act_type, at<uint8_t>(h, ox), m, at<float>(h, oy)));
+    BARQ_HIP(hipMemcpyAsync(y, at<float>(h, oy), ybytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+}  // namespace
+
+int barq_rocm_matvec(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
+                     const void* x, float* y, int mem) {
+    return matmul_any(h, w_type, w, n_rows, k, act_type, x, 1, y, mem, "matvec");
+}
+
+int barq_rocm_matmul(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
+                     const void* x, size_t m, float* y, int mem) {
+    return matmul_any(h, w_type, w, n_rows, k, act_type, x, m, y, mem, "matmul");
+}
+
+// ---------------------------------------------------------------------------
+// f32 BLAS
+
+int barq_rocm_gemm_f32(barq_rocm_handle* h, const float* a, const float* b, size_t m, size_t k, size_t n, float* c, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (m == 0 || n == 0) return ok();
+    if (!a || !b || !c) return fail(BARQ_E_INVALID, "gemm_f32: null buffer");
+    if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "gemm_f32: dimensions exceed 2^31");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    if (mem == BARQ_MEM_DEVICE) return launched(barq::gemm_f32_launch(a, b, m, k, n, c, h->stream), "gemm_f32");
+    Arena ar;
+    size_t oa = ar.add(m * k * 4), ob = ar.add(k * n * 4), oc = ar.add(m * n * 4);
+    BARQ_CHECK(ensure_ws(h, ar.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, oa), a, m * k * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ob), b, k * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::gemm_f32_launch(at<float>(h, oa), at<float>(h, ob), m, k, n, at<float>(h, oc), h->stream), "gemm_f32"));
+    BARQ_HIP(hipMemcpyAsync(c, at<float>(h, oc), m * n * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+int barq_rocm_gemv_f32(barq_rocm_handle* h, const float* a, const float* x, size_t m, size_t n, float* y, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (m == 0) return ok();
+    if (!a || !x || !y) return fail(BARQ_E_INVALID, "gemv_f32: null buffer");
+    if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "gemv_f32: dimensions exceed 2^31");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    if (mem == BARQ_MEM_DEVICE) return launched(barq::gemv_f32_plain_launch(a, x, m, n, y, h->stream), "gemv_f32");
+    Arena ar;
+    size_t oa = ar.add(m * n * 4), ox = ar.add(n * 4), oy = ar.add(m * 4);
+    BARQ_CHECK(ensure_ws(h, ar.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, oa), a, m * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::gemv_f32_plain_launch(at<float>(h, oa), at<float>(h, ox), m, n, at<float>(h, oy), h->stream), "gemv_f32"));
+    BARQ_HIP(hipMemcpyAsync(y, at<float>(h, oy), m * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// split-scale operator API (QuantizedCudaOps)
+
+int barq_rocm_dequantize_split(barq_rocm_handle* h, int kind, const uint8_t* quants, size_t n_quants,
+                               const float* scales, size_t n_scales, size_t block_size, float* out,
+                               size_t n_out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (block_size == 0) return fail(BARQ_E_INVALID, "dequantize_split: block_size must be > 0");
+    if (n_out == 0) return ok();
+    if (!out || (n_quants && !quants) || (n_scales && !scales)) return fail(BARQ_E_INVALID, "dequantize_split: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const int q8 = kind == BARQ_TYPE_Q8_0;
+    if (mem == BARQ_MEM_DEVICE)
+        return launched(barq::dequant_split_launch(q8, quants, n_quants, scales, n_scales, block_size, out, n_out, h->stream), "dequantize_split");
+    Arena a;
+    size_t oq = a.add(n_quants), os = a.add(n_scales * 4), oo = a.add(n_out * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    if (n_quants) BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, oq), quants, n_quants, hipMemcpyHostToDevice, h->stream));
+    if (n_scales) BARQ_HIP(hipMemcpyAsync(at<float>(h, os), scales, n_scales * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::dequant_split_launch(q8, at<uint8_t>(h, oq), n_quants, at<float>(h, os), n_scales, block_size,
+                                                   at<float>(h, oo), n_out, h->stream), "dequantize_split"));
+    BARQ_HIP(hipMemcpyAsync(out, at<float>(h, oo), n_out * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+int barq_rocm_quantized_matmul_split(barq_rocm_handle* h, const float* a, const uint8_t* bq, size_t n_bq,
+                                     const float* bs, size_t n_bs, float* c, size_t m, size_t n, size_t k,
+                                     int kind, size_t block_size, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (block_size == 0) return fail(BARQ_E_INVALID, "quantized_matmul: block_size must be > 0");
+    if (m == 0 || n == 0) return ok();
+    if (!a || !c || (n_bq && !bq) || (n_bs && !bs)) return fail(BARQ_E_INVALID, "quantized_matmul: null buffer");
+    if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "quantized_matmul: dimensions exceed 2^31");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const int q8 = kind == BARQ_TYPE_Q8_0;
+    Arena ar;
+    size_t ob = ar.add(k * n * 4);
+    size_t oa = 0, oq = 0, os = 0, oc = 0;
+    if (mem == BARQ_MEM_HOST) {
+        oa = ar.add(m * k * 4); oq = ar.add(n_bq); os = ar.add(n_bs * 4); oc = ar.add(m * n * 4);
+    }
+    BARQ_CHECK(ensure_ws(h, ar.used));
+    const float* da = a;
+    const uint8_t* dq = bq;
+    const float* ds = bs;
+    float* dc = c;
+    if (mem == BARQ_MEM_HOST) {
+        BARQ_HIP(hipMemcpyAsync(at<float>(h, oa), a, m * k * 4, hipMemcpyHostToDevice, h->stream));
+        if (n_bq) BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, oq), bq, n_bq, hipMemcpyHostToDevice, h->stream));
+        if (n_bs) BARQ_HIP(hipMemcpyAsync(at<float>(h, os), bs, n_bs * 4, hipMemcpyHostToDevice, h->stream));
+        da = at<float>(h, oa); dq = at<uint8_t>(h, oq); ds = at<float>(h, os); dc = at<float>(h, oc);
+    }
+    float* b = at<float>(h, ob);
+    BARQ_CHECK(launched(barq::dequant_split_launch(q8, dq, n_bq, ds, n_bs, block_size, b, k * n, h->stream), "dequantize_split"));
+    BARQ_CHECK(launched(barq::gemm_f32_launch(da, b, m, k, n, dc, h->stream), "gemm_f32"));
+    if (mem == BARQ_MEM_HOST) {
+        BARQ_HIP(hipMemcpyAsync(c, dc, m * n * 4, hipMemcpyDeviceToHost, h->stream));
+        BARQ_HIP(hipStreamSynchronize(h->stream));
+    }
+    return ok();
+}
+
+int barq_rocm_quantize_q4_0_barq(barq_rocm_handle* h, const float* x, size_t n, uint8_t* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (n % 32) return fail(BARQ_E_QUANT, "quantize_q4_0_barq: n=%zu is not a multiple of 32", n);
+    if (n == 0) return ok();
+    if (!x || !out) return fail(BARQ_E_INVALID, "quantize_q4_0_barq: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const size_t ob_bytes = n / 32 * 20;
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(out, 4)) return fail(BARQ_E_INVALID, "quantize_q4_0_barq: out must be 4-byte aligned");
+        return launched(barq::quantize_q4_0_barq_launch(x, n, out, h->stream), "quantize_q4_0_barq");
+    }
+    Arena a;
+    size_t ox = a.add(n * 4), oo = a.add(ob_bytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::quantize_q4_0_barq_launch(at<float>(h, ox), n, at<uint8_t>(h, oo), h->stream), "quantize_q4_0_barq"));
+    BARQ_HIP(hipMemcpyAsync(out, at<uint8_t>(h, oo), ob_bytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// MoE
+
+int barq_rocm_moe_route(barq_rocm_handle* h, const float* logits, size_t rows, size_t n_experts, size_t top_k,
+                        int32_t* ids, float* weights, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (n_experts == 0) return fail(BARQ_E_INVALID, "Routing logits must contain at least one expert");
+    if (n_experts > 256) return fail(BARQ_E_UNSUPPORTED, "moe_route: at most 256 experts");
+    size_t k = top_k < 1 ? 1 : (top_k > n_experts ? n_experts : top_k);
+    if (k > 64) return fail(BARQ_E_UNSUPPORTED, "moe_route: top_k at most 64");
+    if (rows == 0) return ok();
+    if (!logits || !ids || !weights) return fail(BARQ_E_INVALID, "moe_route: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    if (mem == BARQ_MEM_DEVICE)
+        return launched(barq::moe_route_launch(logits, rows, n_experts, k, ids, weights, h->stream), "moe_route");
+    Arena a;
+    size_t ol = a.add(rows * n_experts * 4), oi = a.add(rows * k * 4), ow = a.add(rows * k * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ol), logits, rows * n_experts * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::moe_route_launch(at<float>(h, ol), rows, n_experts, k, at<int32_t>(h, oi), at<float>(h, ow), h->stream), "moe_route"));
+    BARQ_HIP(hipMemcpyAsync(ids, at<int32_t>(h, oi), rows * k * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipMemcpyAsync(weights, at<float>(h, ow), rows * k * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+namespace {
+
+// Device-pointer MoE FFN.  Work buffers come from one workspace arena that
+// is sized up front (ensure_ws may reallocate and so runs before any use).
+struct MoeArena {
+    size_t off, tok, wts, pos, xg, g, u, yg, q, wf, end;
+};
+
+MoeArena moe_arena(size_t base, size_t ne, size_t hidden, size_t n_ff, size_t na, bool q8) {
+    Arena a;
+    a.used = base;
+    MoeArena m;
+    m.off = a.add((ne + 1) * 4);
+    m.tok = a.add(na * 4);
+    m.wts = a.add(na * 4);
+    m.pos = a.add(na * 4);
+    m.xg = a.add(na * hidden * 4);
+    m.g = a.add(na * n_ff * 4);
+    m.u = a.add(na * n_ff * 4);
+    m.yg = a.add(na * hidden * 4);
+    const size_t qrow = (hidden > n_ff ? hidden : n_ff) / 256 * 292;
+    m.q = a.add(q8 ? na * qrow : 0);
+    // the literal path dequantizes one expert matrix at a time
+    m.wf = a.add(q8 ? 0 : n_ff * hidden * 4);
+    m.end = a.used;
+    return m;
+}
+
+int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate, int ut, const void* const* up, int dt,
+                const void* const* down, size_t hidden, size_t n_ff, const float* x, size_t rows, const int32_t* ids,
+                const float* weights, size_t k, int act, float* out, size_t base) {
+    hipStream_t s = h->stream;
+    const size_t na = rows * k;
+    const bool q8 = act == BARQ_ACT_F32_Q8;
+    const MoeArena L = moe_arena(base, ne, hidden, n_ff, na, q8);
+    const size_t o_off = L.off, o_tok = L.tok, o_wts = L.wts, o_pos = L.pos, o_xg = L.xg, o_g = L.g, o_u = L.u,
+                 o_yg = L.yg, o_q = L.q, o_wf = L.wf;
+    BARQ_CHECK(ensure_ws(h, L.end));
+    int32_t* offsets = at<int32_t>(h, o_off);
+    int32_t* tokens = at<int32_t>(h, o_tok);
+    float* wts = at<float>(h, o_wts);
+    int32_t* rowpos = at<int32_t>(h, o_pos);
+    float* xg = at<float>(h, o_xg);
+    float* gb = at<float>(h, o_g);
+    float* ub = at<float>(h, o_u);
+    float* yg = at<float>(h, o_yg);
+    uint8_t* qb = at<uint8_t>(h, o_q);
+
+    BARQ_CHECK(launched(barq::moe_group_launch(ids, weights, rows, k, ne, offsets, tokens, wts, rowpos, s), "moe_group"));
+    std::vector<int32_t> off(ne + 1);
+    BARQ_HIP(hipMemcpyAsync(off.data(), offsets, (ne + 1) * 4, hipMemcpyDeviceToHost, s));
+    BARQ_HIP(hipStreamSynchronize(s));
+    const size_t n_assign = (size_t)off[ne];
+    BARQ_CHECK(launched(barq::moe_gather_launch(x, tokens, n_assign, hidden, xg, s), "moe_gather"));
+    const int in_act = q8 ? q8_partner(gt) : BARQ_ACT_F32;
+    if (q8) {
+        if (q8_partner(gt) != BARQ_TYPE_Q8_K || q8_partner(ut) != BARQ_TYPE_Q8_K || q8_partner(dt) != BARQ_TYPE_Q8_K)
+            return fail(BARQ_E_UNSUPPORTED, "moe_ffn: the Q8 path needs K-quant (Q4_K/Q6_K) expert weights");
+        BARQ_CHECK(launched(barq::quantize_q8_k_launch(xg, n_assign, hidden, qb, s), "quantize_act"));
+    }
+    const size_t xq_row = q8 ? row_bytes_of(BARQ_TYPE_Q8_K, hidden) : hidden * 4;
+    const uint8_t* xin = q8 ? qb : reinterpret_cast<const uint8_t*>(xg);
+    for (size_t e = 0; e < ne; e++) {
+        const size_t r0 = (size_t)off[e], c = (size_t)off[e + 1] - r0;
+        if (!c) continue;
+        if (q8) {
+            BARQ_CHECK(matmul_dev(h, gt, gate[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, gb + r0 * n_ff));
+            BARQ_CHECK(matmul_dev(h, ut, up[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, ub + r0 * n_ff));
+        } else {
+            float* wf = at<float>(h, o_wf);
+            BARQ_CHECK(launched(barq::dequant_launch(gt, gate[e], n_ff * hidden, wf, s), "dequantize"));
+            BARQ_CHECK(launched(barq::gemm_f32_nt_launch(xg + r0 * hidden, wf, c, hidden, n_ff, gb + r0 * n_ff, s), "gemm_f32_nt"));
+            BARQ_CHECK(launched(barq::dequant_launch(ut, up[e], n_ff * hidden, wf, s), "dequantize"));
+            BARQ_CHECK(launched(barq::gemm_f32_nt_launch(xg + r0 * hidden, wf, c, hidden, n_ff, ub + r0 * n_ff, s), "gemm_f32_nt"));
+        }
+    }
+    BARQ_CHECK(launched(barq::swiglu_launch(gb, ub, n_assign * n_ff, gb, s), "swiglu"));
+    const size_t hq_row = q8 ? row_bytes_of(BARQ_TYPE_Q8_K, n_ff) : n_ff * 4;
+    if (q8) BARQ_CHECK(launched(barq::quantize_q8_k_launch(gb, n_assign, n_ff, qb, s), "quantize_act"));
+    const uint8_t* hin = q8 ? qb : reinterpret_cast<const uint8_t*>(gb);
+    for (size_t e = 0; e < ne; e++) {
+        const size_t r0 = (size_t)off[e], c = (size_t)off[e + 1] - r0;
+        if (!c) continue;
+        if (q8) {
+            BARQ_CHECK(matmul_dev(h, dt, down[e], hidden, n_ff, in_act, hin + r0 * hq_row, c, yg + r0 * hidden));
+        } else {
+            float* wf = at<float>(h, o_wf);
+            BARQ_CHECK(launched(barq::dequant_launch(dt, down[e], hidden * n_ff, wf, s), "dequantize"));
+            BARQ_CHECK(launched(barq::gemm_f32_nt_launch(gb + r0 * n_ff, wf, c, n_ff, hidden, yg + r0 * hidden, s), "gemm_f32_nt"));
+        }
+    }
+    return launched(barq::moe_scatter_launch(yg, ids, weights, rowpos, rows, k, hidden, out, s), "moe_scatter");
+}
+
+}  // namespace
+
+int barq_rocm_moe_ffn(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate, int ut, const void* const* up,
+                      int dt, const void* const* down, size_t hidden, size_t n_ff, const float* x, size_t rows,
+                      const int32_t* ids, const float* weights, size_t k, int act, float* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (ne == 0) return fail(BARQ_E_INVALID, "At least one expert function is required");
+    if (ne > 256) return fail(BARQ_E_UNSUPPORTED, "moe_ffn: at most 256 experts");
+    if (act != BARQ_ACT_F32 && act != BARQ_ACT_F32_Q8) return fail(BARQ_E_UNSUPPORTED, "moe_ffn: act must be BARQ_ACT_F32 or BARQ_ACT_F32_Q8");
+    BARQ_CHECK(check_linear(gt, hidden, BARQ_ACT_F32, "moe_ffn gate"));
+    BARQ_CHECK(check_linear(ut, hidden, BARQ_ACT_F32, "moe_ffn up"));
+    BARQ_CHECK(check_linear(dt, n_ff, BARQ_ACT_F32, "moe_ffn down"));
+    if (hidden % 4) return fail(BARQ_E_DIM, "moe_ffn: hidden must be a multiple of 4");
+    if (rows == 0) return ok();
+    if (k == 0) return fail(BARQ_E_INVALID, "moe_ffn: top_k must be > 0");
+    if (!gate || !up || !down || !x || !ids || !weights || !out) return fail(BARQ_E_INVALID, "moe_ffn: null buffer");
+    for (size_t e = 0; e < ne; e++)
+        if (!gate[e] || !up[e] || !down[e]) return fail(BARQ_E_INVALID, "moe_ffn: null expert weight %zu", e);
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    if (mem == BARQ_MEM_DEVICE) return moe_ffn_dev(h, ne, gt, gate, ut, up, dt, down, hidden, n_ff, x, rows, ids, weights, k, act, out, 0);
+    // host buffers: stage everything into the front of the workspace
+    const size_t gb = n_ff * row_bytes_of(gt, hidden), ub = n_ff * row_bytes_of(ut, hidden), db = hidden * row_bytes_of(dt, n_ff);
+    Arena a;
+    std::vector<size_t> og(ne), ou(ne), od(ne);
+    for (size_t e = 0; e < ne; e++) { og[e] = a.add(gb); ou[e] = a.add(ub); od[e] = a.add(db); }
+    const size_t ox = a.add(rows * hidden * 4), oi = a.add(rows * k * 4), ow = a.add(rows * k * 4), oo = a.add(rows * hidden * 4);
+    // staging region first, then the compute region moe_ffn_dev lays out
+    const MoeArena L = moe_arena(a.used, ne, hidden, n_ff, rows * k, act == BARQ_ACT_F32_Q8);
+    BARQ_CHECK(ensure_ws(h, L.end));
+    for (size_t e = 0; e < ne; e++) {
+        BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, og[e]), gate[e], gb, hipMemcpyHostToDevice, h->stream));
+        BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ou[e]), up[e], ub, hipMemcpyHostToDevice, h->stream));
+        BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, od[e]), down[e], db, hipMemcpyHostToDevice, h->stream));
+    }
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, rows * hidden * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<int32_t>(h, oi), ids, rows * k * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ow), weights, rows * k * 4, hipMemcpyHostToDevice, h->stream));
+    std::vector<const void*> dg(ne), du(ne), dd(ne);
+    for (size_t e = 0; e < ne; e++) { dg[e] = at<uint8_t>(h, og[e]); du[e] = at<uint8_t>(h, ou[e]); dd[e] = at<uint8_t>(h, od[e]); }
+    BARQ_CHECK(moe_ffn_dev(h, ne, gt, dg.data(), ut, du.data(), dt, dd.data(), hidden, n_ff, at<float>(h, ox), rows,
+                           at<int32_t>(h, oi), at<float>(h, ow), k, act, at<float>(h, oo), a.used));
+    BARQ_HIP(hipMemcpyAsync(out, at<float>(h, oo), rows * hidden * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+}  // extern "C"

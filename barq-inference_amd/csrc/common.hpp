@@ -1,0 +1,117 @@
+// Device-side helpers shared by the gfx950 kernels: block geometry, byte
+// loads that tolerate the 2-byte alignment of GGUF blocks, f16 conversion
+// and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace barq {
+
+// GGUF block geometry (barq_core/src/gguf.rs:168-186 block sizes; bytes
+// from gguf.rs:529-530,645,747,854 and llama.cpp block_q4_0/block_q8_K).
+constexpr int QK4_0 = 32, Q4_0_BYTES = 18;
+constexpr int Q4_0_BARQ_BYTES = 20;
+constexpr int QK8_0 = 32, Q8_0_BYTES = 34;
+constexpr int QK_K = 256, Q4_K_BYTES = 144, Q6_K_BYTES = 210, Q8_K_BYTES = 292;
+
+constexpr int TYPE_F32 = 0, TYPE_F16 = 1, TYPE_Q4_0 = 2, TYPE_Q8_0 = 8,
+              TYPE_Q4_K = 12, TYPE_Q6_K = 14, TYPE_Q8_K = 15,
+              TYPE_Q4_0_BARQ = 0x10002;
+
+constexpr int WAVE = 64;
+
+// IEEE binary16 -> binary32 (v_cvt_f32_f16: exact widening, as
+// half::f16::to_f32 used at gguf.rs:661,763,768,869).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits);
+    return (float)h;
+}
+
+// binary32 -> binary16, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// 16-byte vector with 4-byte alignment: global_load_dwordx4 needs only
+// dword alignment on gfx9 family hardware.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ uint4 ld16_a4(const uint8_t* p) {
+    u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16 bytes starting at a 2-byte aligned address p.  Reads only bytes in
+// [floor4(p), p + 16): a dword-aligned 16-byte load plus, when p is not
+// dword aligned, the 2 bytes at p+14, then a funnel shift.  Safe at the end
+// of a block or buffer.
+__device__ __forceinline__ uint4 ld16_a2(const uint8_t* p) {
+    uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;
+    const uint8_t* q = p - sh;
+    uint4 a = ld16_a4(q);
+    uint32_t e = *reinterpret_cast<const uint16_t*>(q + (sh ? 16 : 12));
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(a.y, a.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(a.z, a.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(a.w, a.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(e, a.w, sh);
+    return r;
+}
+
+// 8 bytes at a 2-byte aligned address p, reading only [floor4(p), p + 8).
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
+    uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;
+    const uint8_t* qb = p - sh;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(qb);
+    uint32_t a0 = q[0], a1 = q[1];
+    uint32_t e = *reinterpret_cast<const uint16_t*>(qb + (sh ? 8 : 4));
+    uint2 r;
+    r.x = __builtin_amdgcn_alignbyte(a1, a0, sh);
+    r.y = __builtin_amdgcn_alignbyte(e, a1, sh);
+    return r;
+}
+
+// sdot4: 4 x (i8 * i8) + acc  (v_dot4_i32_i8)
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int acc) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, acc, false);
+}
+
+// ---- wave64 reductions ----------------------------------------------------
+// Sum over a row of 16 lanes with DPP (quad_perm, half-mirror, mirror); every
+// lane of the row ends with the row's total.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+    return v;
+}
+
+// Full wave sum; the result is wave-uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ int wave_isum(int v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+}  // namespace barq

@@ -1,0 +1,62 @@
+// Host-side launchers of the gfx950 kernels (internal to libbarq_rocm).
+// Every launcher enqueues on `s` and returns hipGetLastError().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace barq {
+
+// dequant.hip
+hipError_t dequant_launch(int type, const void* blocks, size_t n_elems, float* out, hipStream_t s);
+hipError_t dequant_split_launch(int kind_q8_0, const uint8_t* quants, size_t n_quants,
+                                const float* scales, size_t n_scales, size_t block_size,
+                                float* out, size_t n_out, hipStream_t s);
+
+// quantize.hip
+hipError_t quantize_q8_0_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s);
+hipError_t quantize_q8_k_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s);
+hipError_t quantize_q4_0_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s);
+
+// gemv.hip
+hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,
+                          float* y, hipStream_t s);
+hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
+                           float* y, hipStream_t s);
+size_t gemv_q8_lds_bytes(int w_type, size_t k);
+void gemv_set_config(int rows_per_wave, int waves);
+
+// gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows)
+hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k,
+                                const void* xq, size_t m, float* y, hipStream_t s);
+bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k);
+
+// f32blas.hip
+hipError_t gemm_f32_launch(const float* a, const float* b, size_t m, size_t k, size_t n, float* c,
+                           hipStream_t s);
+hipError_t gemv_f32_plain_launch(const float* a, const float* x, size_t m, size_t n, float* y,
+                                 hipStream_t s);
+// C[m x n] = A[m x k] B^T with B stored [n x k] (dequantized GGUF rows)
+hipError_t gemm_f32_nt_launch(const float* a, const float* b_nk, size_t m, size_t k, size_t n, float* c,
+                              hipStream_t s);
+
+// moe.hip
+hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, size_t top_k,
+                            int32_t* ids, float* weights, hipStream_t s);
+// CSR grouping of routing assignments (batch_by_expert): offsets[n_experts+1],
+// tokens/wts[rows*top_k] in expert-major, ascending-token order.
+hipError_t moe_group_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
+                            size_t n_experts, int32_t* offsets, int32_t* tokens, float* wts,
+                            int32_t* rowpos, hipStream_t s);
+// xg[i] = x[tokens[i]] for i < n_assign
+hipError_t moe_gather_launch(const float* x, const int32_t* tokens, size_t n_assign, size_t hidden,
+                             float* xg, hipStream_t s);
+// h = silu(g) * u elementwise (ops.rs:191-211 and moe_fused.rs:61-66)
+hipError_t swiglu_launch(const float* g, const float* u, size_t n, float* h, hipStream_t s);
+// out[t] = sum over t's assignments in ascending expert id of w * yg[row]
+// rowpos[t*top_k+i] is the grouped row of assignment (t, i) or -1
+hipError_t moe_scatter_launch(const float* yg, const int32_t* ids, const float* weights,
+                              const int32_t* rowpos, size_t rows, size_t top_k, size_t hidden,
+                              float* out, hipStream_t s);
+
+}  // namespace barq

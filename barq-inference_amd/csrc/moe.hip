@@ -1,0 +1,179 @@
+// Device side of the fused MoE helpers (models/src/moe_fused.rs): top-k
+// routing, grouping of assignments by expert, row gather, SwiGLU and the
+// weighted scatter-add.  The expert contractions themselves run on the GEMV /
+// MFMA kernels.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace barq {
+
+constexpr int MOE_MAX_EXPERTS = 256;
+constexpr int MOE_MAX_TOPK = 64;
+constexpr float F32_EPSILON = 1.1920929e-7f;
+
+// select_top_k_experts (moe_fused.rs:95-144), one thread per row: a stable
+// descending sort keeps equal logits in index order, so the first k picks
+// are the largest values with the lowest index winning ties; softmax over
+// the kept k with the max subtracted and the denominator floored at
+// f32::EPSILON.  k = clamp(top_k, 1, n_experts) (:121).
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int rows, int ne,
+                                                       int k, int32_t* __restrict__ ids,
+                                                       float* __restrict__ weights) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const float* row = logits + (size_t)r * ne;
+    uint64_t taken[MOE_MAX_EXPERTS / 64] = {0, 0, 0, 0};
+    int sel[MOE_MAX_TOPK];
+    for (int i = 0; i < k; i++) {
+        int best = -1;
+        float bv = 0.0f;
+        for (int e = 0; e < ne; e++) {
+            if ((taken[e >> 6] >> (e & 63)) & 1u) continue;
+            const float v = row[e];
+            if (best < 0 || v > bv) { best = e; bv = v; }
+        }
+        taken[best >> 6] |= (uint64_t)1 << (best & 63);
+        sel[i] = best;
+    }
+    float mx = -INFINITY;
+    for (int i = 0; i < k; i++) mx = fmaxf(mx, row[sel[i]]);
+    float denom = 0.0f;
+    for (int i = 0; i < k; i++) denom += expf(row[sel[i]] - mx);
+    denom = fmaxf(denom, F32_EPSILON);
+    for (int i = 0; i < k; i++) {
+        ids[(size_t)r * k + i] = sel[i];
+        weights[(size_t)r * k + i] = expf(row[sel[i]] - mx) / denom;
+    }
+}
+
+hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, size_t top_k,
+                            int32_t* ids, float* weights, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, logits,
+                       (int)rows, (int)n_experts, (int)top_k, ids, weights);
+    return hipGetLastError();
+}
+
+// batch_by_expert (moe_fused.rs:196-223): one wave builds the CSR grouping.
+// Tokens are visited in ascending order and each token's ids in routing
+// order; ids outside [0, n_experts) are skipped (batches.get_mut -> None).
+// rowpos[t*k+i] is the grouped row of assignment (t, i), or -1.
+__global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict__ ids,
+                                                       const float* __restrict__ weights, int rows, int k,
+                                                       int ne, int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ tokens, float* __restrict__ wts,
+                                                       int32_t* __restrict__ rowpos) {
+    __shared__ int cnt[MOE_MAX_EXPERTS + 1];
+    const int lane = threadIdx.x;
+    for (int e = lane; e <= ne; e += 64) cnt[e] = 0;
+    __syncthreads();
+    const int n = rows * k;
+    for (int a = lane; a < n; a += 64) {
+        const int e = ids[a];
+        if (e >= 0 && e < ne) atomicAdd(&cnt[e + 1], 1);
+    }
+    __syncthreads();
+    if (lane == 0) {
+        for (int e = 0; e < ne; e++) cnt[e + 1] += cnt[e];
+        for (int e = 0; e <= ne; e++) offsets[e] = cnt[e];
+        // fill in ascending (token, routing slot) order: deterministic
+        for (int a = 0; a < n; a++) {
+            const int e = ids[a];
+            if (e < 0 || e >= ne) { rowpos[a] = -1; continue; }
+            const int pos = cnt[e]++;
+            tokens[pos] = a / k;
+            wts[pos] = weights[a];
+            rowpos[a] = pos;
+        }
+    }
+}
+
+hipError_t moe_group_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
+                            size_t n_experts, int32_t* offsets, int32_t* tokens, float* wts,
+                            int32_t* rowpos, hipStream_t s) {
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64), 0, s, ids, weights, (int)rows, (int)top_k,
+                       (int)n_experts, offsets, tokens, wts, rowpos);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void moe_gather_kernel(const float4* __restrict__ x, const int32_t* __restrict__ tokens,
+                                                         int n_assign, int h4, float4* __restrict__ xg) {
+    const int i = blockIdx.y;
+    const int t = tokens[i];
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < h4; c += gridDim.x * blockDim.x)
+        xg[(size_t)i * h4 + c] = x[(size_t)t * h4 + c];
+}
+
+hipError_t moe_gather_launch(const float* x, const int32_t* tokens, size_t n_assign, size_t hidden,
+                             float* xg, hipStream_t s) {
+    if (n_assign == 0) return hipSuccess;
+    const int h4 = (int)(hidden / 4);
+    const unsigned gx = (unsigned)((h4 + 255) / 256 < 64 ? (h4 + 255) / 256 : 64);
+    hipLaunchKernelGGL(moe_gather_kernel, dim3(gx, (unsigned)n_assign), dim3(256), 0, s,
+                       reinterpret_cast<const float4*>(x), tokens, (int)n_assign, h4,
+                       reinterpret_cast<float4*>(xg));
+    return hipGetLastError();
+}
+
+// Silu x / (1 + exp(-x)) (ops.rs:191-211), then the gate*up product
+// (moe_fused.rs:61-66).
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     size_t n, float* __restrict__ h) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float gv = g[i];
+        const float a = gv / (1.0f + expf(-gv));
+        h[i] = a * u[i];
+    }
+}
+
+hipError_t swiglu_launch(const float* g, const float* u, size_t n, float* h, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    size_t grid = (n + 255) / 256;
+    if (grid > 16384) grid = 16384;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)grid), dim3(256), 0, s, g, u, n, h);
+    return hipGetLastError();
+}
+
+// dispatch_experts accumulation (moe_fused.rs:292-299): per token, expert
+// contributions are added in ascending expert id order (the order batches
+// are processed), each as out += y * w with the product rounded first.
+__global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restrict__ yg,
+                                                          const int32_t* __restrict__ ids,
+                                                          const float* __restrict__ weights,
+                                                          const int32_t* __restrict__ rowpos, int k,
+                                                          int hidden, float* __restrict__ out) {
+    const int t = blockIdx.y;
+    const int32_t* tid = ids + (size_t)t * k;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < hidden; c += gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+        // ascending expert id; equal ids keep routing order (stable)
+        int last_e = -1, last_i = -1;
+        for (int n = 0; n < k; n++) {
+            int be = 0x7fffffff, bi = -1;
+            for (int i = 0; i < k; i++) {
+                const int e = tid[i];
+                if (rowpos[(size_t)t * k + i] < 0) continue;
+                const bool after = e > last_e || (e == last_e && i > last_i);
+                if (after && (e < be || (e == be && i < bi))) { be = e; bi = i; }
+            }
+            if (bi < 0) break;
+            const float p = yg[(size_t)rowpos[(size_t)t * k + bi] * hidden + c] * weights[(size_t)t * k + bi];
+            acc = acc + p;
+            last_e = be; last_i = bi;
+        }
+        out[(size_t)t * hidden + c] = acc;
+    }
+}
+
+hipError_t moe_scatter_launch(const float* yg, const int32_t* ids, const float* weights,
+                              const int32_t* rowpos, size_t rows, size_t top_k, size_t hidden,
+                              float* out, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const unsigned gx = (unsigned)((hidden + 255) / 256 < 64 ? (hidden + 255) / 256 : 64);
+    hipLaunchKernelGGL(moe_scatter_kernel, dim3(gx, (unsigned)rows), dim3(256), 0, s, yg, ids, weights,
+                       rowpos, (int)top_k, (int)hidden, out);
+    return hipGetLastError();
+}
+
+}  // namespace barq

@@ -1,0 +1,135 @@
+// Activation quantizers (llama.cpp block_q8_0 / block_q8_K; the reference has
+// no implementation — Q8_K is only a type id, gguf.rs:132) and the
+// reference's own Q4_0 encoder (quant/src/q4_0.rs:23-67).
+//
+// All arithmetic is single IEEE operations (division is correctly rounded in
+// HIP by default), so results are bit-identical to the CPU restatement.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace barq {
+
+// Q8_0: one lane per element, 32 lanes per block.
+// d = amax/127 (stored f16), id = d ? 1/d : 0, q = roundf(x*id).
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ x,
+                                                            uint8_t* __restrict__ out, size_t nb) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nb * 32) return;  // whole 32-lane groups exit together
+    const size_t b = e / 32;
+    const int l = (int)(e % 32);
+    const float v = x[e];
+    float a = fabsf(v);
+    #pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float d = a / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q = (int)roundf(v * id);
+    uint8_t* blk = out + b * 34;
+    blk[2 + l] = (uint8_t)(int8_t)q;
+    if (l == 0) *reinterpret_cast<uint16_t*>(blk) = f32_to_f16_bits(d);
+}
+
+// Q8_K: one wave per 256-element block, 4 elements per lane.
+// max = the signed value of the first element with the largest |x|;
+// iscale = -127/max; q = min(127, rint(iscale*x)); d = 1/iscale;
+// bsums[g] = sum of q[16g .. 16g+16).  An all-zero block stores zeros.
+__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x,
+                                                            uint8_t* __restrict__ out, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;  // whole waves exit together
+    const int lane = threadIdx.x & 63;
+    const float4 v = reinterpret_cast<const float4*>(x + b * 256)[lane];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    float ba = 0.0f, bv = 0.0f;
+    int bi = 0x7fffffff;
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float ax = fabsf(vv[j]);
+        if (ax > ba) { ba = ax; bv = vv[j]; bi = 4 * lane + j; }
+    }
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(ba, off);
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
+    }
+    uint8_t* blk = out + b * 292;
+    if (ba == 0.0f) {
+        reinterpret_cast<uint32_t*>(blk + 4)[lane] = 0u;
+        if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = 0;
+        if (lane == 0) *reinterpret_cast<float*>(blk) = 0.0f;
+        return;
+    }
+    const float iscale = -127.0f / bv;
+    int q[4];
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int t = (int)rintf(iscale * vv[j]);
+        q[j] = t < 127 ? t : 127;
+    }
+    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                            ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    reinterpret_cast<uint32_t*>(blk + 4)[lane] = packed;
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
+    if (lane == 0) *reinterpret_cast<float*>(blk) = 1.0f / iscale;
+}
+
+// quant::Q4_0::quantize (quant/src/q4_0.rs:23-67): scale = max_abs/8 (0 for an
+// all-zero block), q = clamp(round(x/scale) as i8, -8, 7) with Rust's
+// half-away-from-zero round and saturating cast; element i goes to the low
+// (even i) or high (odd i) nibble of byte i/2.  20-byte blocks.
+__global__ __launch_bounds__(256) void quantize_q4_0_barq_kernel(const float* __restrict__ x,
+                                                                 uint8_t* __restrict__ out, size_t nb) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nb * 32) return;
+    const size_t b = e / 32;
+    const int l = (int)(e % 32);
+    const float v = x[e];
+    float a = fabsf(v);
+    #pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float scale = a == 0.0f ? 0.0f : a / 8.0f;
+    int q = 0;
+    if (scale != 0.0f) {
+        const float r = roundf(v / scale);
+        q = (r != r) ? 0 : (r > 127.0f ? 127 : (r < -128.0f ? -128 : (int)r));
+    }
+    q = q < -8 ? -8 : (q > 7 ? 7 : q);
+    const uint32_t nib = (uint32_t)q & 0x0Fu;
+    const uint32_t other = __shfl_xor(nib, 1);
+    uint8_t* blk = out + b * 20;
+    if ((l & 1) == 0) blk[4 + l / 2] = (uint8_t)(nib | (other << 4));
+    if (l == 0) *reinterpret_cast<float*>(blk) = scale;
+}
+
+hipError_t quantize_q8_0_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s) {
+    const size_t nb = n_rows * (k / 32);
+    if (nb == 0) return hipSuccess;
+    const size_t threads = nb * 32;
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       x, static_cast<uint8_t*>(out), nb);
+    return hipGetLastError();
+}
+
+hipError_t quantize_q8_k_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s) {
+    const size_t nb = n_rows * (k / 256);
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8_k_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x,
+                       static_cast<uint8_t*>(out), nb);
+    return hipGetLastError();
+}
+
+hipError_t quantize_q4_0_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s) {
+    const size_t nb = n / 32;
+    if (nb == 0) return hipSuccess;
+    const size_t threads = nb * 32;
+    hipLaunchKernelGGL(quantize_q4_0_barq_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       x, out, nb);
+    return hipGetLastError();
+}
+
+}  // namespace barq

@@ -1,0 +1,201 @@
+/*
+ * barq_rocm.h — C ABI of the MI355X (gfx950) quantized-linear backend.
+ *
+ * This is the drop-in boundary for barq-inference's quantized-linear hot
+ * path: GGUF block-quant dequantize-and-dot for Q4_0, Q8_0, Q4_K and Q6_K
+ * (batch-1 GEMV, batched int8-MFMA GEMM, ragged MoE expert GEMM).  The
+ * reference is Rust and has no FFI on this path; every entry point below
+ * names the Rust interface it replaces, so a `backend` crate arm (or a
+ * `BackendPreference::Rocm` in barq_core/src/blas.rs:20-42) can bind it with
+ * an `extern "C"` block and a build.rs that runs hipcc.
+ *
+ * Conventions
+ *  - Every function returns a barq_status; 0 is success.  The message of the
+ *    last failure on the calling thread is barq_rocm_last_error().
+ *  - Buffers are owned by the caller.  `mem` says where they live:
+ *      BARQ_MEM_DEVICE — device pointers; the call is enqueued on the
+ *        handle's stream and returns without waiting (stream order).
+ *      BARQ_MEM_HOST   — host pointers; the call copies in, computes, copies
+ *        out and waits (the reference's QuantizedCudaOps round trip,
+ *        backend/src/cuda_quant.rs:311-338, but with the compute on device).
+ *  - A handle is used by one thread at a time; distinct handles may be used
+ *    concurrently (blas::gemm_f32 is called from rayon workers,
+ *    models/src/transformer.rs:315-331).
+ *  - Weights are GGUF row-major: n_rows rows of k elements, blocks along k
+ *    (gguf.rs:415-519 element order).  y = W x, i.e. y[n] = sum_k W[n,k] x[k],
+ *    which is blas::gemv_f32(dequant(W), x) (blas.rs:229-304) and the rows of
+ *    blas::gemm_f32(x, W^T) (blas.rs:103-213, W^T built by
+ *    models/src/weight_cache.rs:172-210).
+ */
+#ifndef BARQ_ROCM_H
+#define BARQ_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BARQ_ROCM_ABI_VERSION 1
+
+/* Status codes: barq_core::error::Error variants (barq_core/src/error.rs:9-57) */
+typedef enum {
+    BARQ_OK = 0,
+    BARQ_E_BACKEND = 1,      /* Error::Backend (error.rs:48): HIP runtime failure */
+    BARQ_E_UNSUPPORTED = 2,  /* Error::Unsupported (error.rs:55): no device, type or shape not supported */
+    BARQ_E_DIM = 3,          /* Error::DimensionMismatch (error.rs:27) */
+    BARQ_E_QUANT = 4,        /* Error::Quantization (error.rs:44): k not a whole number of blocks */
+    BARQ_E_INVALID = 5,      /* Error::Tensor (error.rs:11): null pointer or bad argument */
+    BARQ_E_ALLOC = 6         /* Error::Allocation (error.rs:15) */
+} barq_status;
+
+/* Type ids: the GgufTensorType discriminants (barq_core/src/gguf.rs:117-137),
+   plus the reference's own 20-byte Q4_0 layout (gguf.rs:521-578,
+   quant/src/q4_0.rs:23-115), which differs from GGUF's 18-byte block_q4_0. */
+typedef enum {
+    BARQ_TYPE_F32 = 0,
+    BARQ_TYPE_F16 = 1,
+    BARQ_TYPE_Q4_0 = 2,        /* f16 d + 16 B; elem i<16 low nibble of byte i, else high of byte i-16; (nib-8)*d */
+    BARQ_TYPE_Q8_0 = 8,        /* f16 d + 32 x i8 */
+    BARQ_TYPE_Q4_K = 12,       /* f16 d, f16 dmin, 12 B 6-bit scales/mins, 128 B nibbles; 256 elems */
+    BARQ_TYPE_Q6_K = 14,       /* 128 B ql, 64 B qh, 16 x i8 scales, f16 d; 256 elems */
+    BARQ_TYPE_Q8_K = 15,       /* f32 d, 256 x i8, 16 x i16 bsums (activations) */
+    BARQ_TYPE_Q4_0_BARQ = 0x10002 /* f32 scale + 16 B; elem i in byte i/2 (low if even), sign-extended */
+} barq_type;
+
+/* Activation mode for matvec/matmul.  BARQ_ACT_F32 keeps x in f32 and
+   dequantizes W in registers: the literal reference arithmetic.  Passing
+   BARQ_TYPE_Q8_0 / BARQ_TYPE_Q8_K means x is already-quantized blocks (from
+   barq_rocm_quantize_act) and the product runs on integer dot/MFMA units.
+   BARQ_ACT_F32_Q8 means x is f32 and the library quantizes it to the
+   weight type's Q8 partner (Q8_0 for Q4_0/Q8_0/Q4_0_BARQ, Q8_K for
+   Q4_K/Q6_K) in its workspace first. */
+#define BARQ_ACT_F32 0
+#define BARQ_ACT_F32_Q8 0x20000
+
+typedef enum { BARQ_MEM_HOST = 0, BARQ_MEM_DEVICE = 1 } barq_mem;
+
+typedef struct barq_rocm_handle barq_rocm_handle;
+
+/* ---- lifecycle ---------------------------------------------------------
+ * Replaces CudaBackend::new(device_id) (backend/src/cuda.rs:60-155) and
+ * QuantizedCudaOps::new (backend/src/cuda_quant.rs:217-238).  A missing or
+ * unusable device returns BARQ_E_UNSUPPORTED, as cuda.rs:64-77 maps a failed
+ * CudaDevice::new to Error::Unsupported, so callers fall back to the CPU
+ * chain of blas.rs:134-212.  The handle owns a HIP stream and a workspace. */
+int barq_rocm_create(int device, barq_rocm_handle** out);
+int barq_rocm_destroy(barq_rocm_handle* h);
+/* Message of the last failure on this thread ("" if none). */
+const char* barq_rocm_last_error(void);
+/* Use an external hipStream_t for subsequent calls (NULL: the handle's own). */
+int barq_rocm_set_stream(barq_rocm_handle* h, void* hip_stream);
+void* barq_rocm_get_stream(barq_rocm_handle* h);
+int barq_rocm_synchronize(barq_rocm_handle* h);
+/* ABI version of the loaded library (BARQ_ROCM_ABI_VERSION). */
+int barq_rocm_abi_version(void);
+
+/* ---- block geometry ----------------------------------------------------
+ * GgufTensorType::block_size (gguf.rs:168-186) and the per-type block byte
+ * sizes of gguf.rs:529-530,645,747,854.  0 for an unknown type. */
+size_t barq_rocm_block_elems(int type);
+size_t barq_rocm_block_bytes(int type);
+/* Bytes of one row of k elements (0 if k is not a whole number of blocks). */
+size_t barq_rocm_row_bytes(int type, size_t k);
+
+/* ---- dequantize --------------------------------------------------------
+ * Replaces the per-type decoders behind GgufReader::load_tensor
+ * (gguf.rs:437-519): load_q4_0 :521-578 (BARQ_TYPE_Q4_0_BARQ; GGUF Q4_0 is
+ * BARQ_TYPE_Q4_0), load_q8_0 :634-681, load_q4_k :730-837, load_q6_k
+ * :839-914, plus F16 :456-469 and the Q8_K activation blocks.  Output is
+ * bit-identical to those decoders.  n_elems must be a whole number of blocks. */
+int barq_rocm_dequantize(barq_rocm_handle* h, int type, const void* blocks,
+                         size_t n_elems, float* out, int mem);
+
+/* ---- activation quantize -----------------------------------------------
+ * No reference counterpart: Q8_K is only an id (gguf.rs:132, quant.rs:29).
+ * Implements llama.cpp's block_q8_0 (d = amax/127 stored f16,
+ * q = roundf(x/d)) and block_q8_K (iscale = -127/max, q = min(127,
+ * rint(iscale*x)), d = 1/iscale, bsums of 16) for n_rows rows of k. */
+int barq_rocm_quantize_act(barq_rocm_handle* h, int act_type, const float* x,
+                           size_t n_rows, size_t k, void* out_blocks, int mem);
+
+/* ---- matvec / matmul ---------------------------------------------------
+ * Replace blas::gemv_f32 (blas.rs:229-304; the output head,
+ * transformer.rs:486) and blas::gemm_f32 (blas.rs:103-213; every
+ * projection, transformer.rs:274,423) when the weight is kept packed instead
+ * of dequantized at load (gguf.rs:437-475) and transposed
+ * (weight_cache.rs:172-210).
+ *   matvec: y[n_rows] = W x.
+ *   matmul: Y[m x n_rows] (row-major) = X W^T, X is m rows of k (f32 or Q8
+ *           blocks per row) — gemm_f32(X, W^T, m, k, n_rows).
+ * For m >= 16 matmul runs the LDS-staged int8-MFMA kernel. */
+int barq_rocm_matvec(barq_rocm_handle* h, int w_type, const void* w,
+                     size_t n_rows, size_t k, int act_type, const void* x,
+                     float* y, int mem);
+int barq_rocm_matmul(barq_rocm_handle* h, int w_type, const void* w,
+                     size_t n_rows, size_t k, int act_type, const void* x,
+                     size_t m, float* y, int mem);
+
+/* ---- f32 BLAS ----------------------------------------------------------
+ * Device arms of blas::gemm_f32 (blas.rs:103-213: C[m x n] = A[m x k]
+ * B[k x n], row-major) and blas::gemv_f32 (blas.rs:229-304: y = A[m x n] x),
+ * for callers that keep f32 weights. */
+int barq_rocm_gemm_f32(barq_rocm_handle* h, const float* a, const float* b,
+                       size_t m, size_t k, size_t n, float* c, int mem);
+int barq_rocm_gemv_f32(barq_rocm_handle* h, const float* a, const float* x,
+                       size_t m, size_t n, float* y, int mem);
+
+/* ---- the reference's split-scale quantized operator API ----------------
+ * QuantizedCudaOps (backend/src/cuda_quant.rs:192-338) keeps quants and f32
+ * scales in separate buffers.  kind == BARQ_TYPE_Q8_0 decodes signed bytes
+ * (dequantize_signed_8bit_host :77-102); any other kind decodes packed
+ * sign-extended nibbles (dequantize_packed_4bit_host :44-75), which is what
+ * the reference's dequantize_q4k/q5k do.  block_size is elements per scale
+ * (the reference passes recommended_block_size(), cuda.rs:228-230, for
+ * dequantize_* and QuantizedGemmConfig::block_size, :128-150, for matmul).
+ * quantized_matmul: C[m x n] = A[m x k] B, B = [k x n] decoded along its
+ * flat row-major index (quantized_matmul_host :104-126). */
+int barq_rocm_dequantize_split(barq_rocm_handle* h, int kind,
+                               const uint8_t* quants, size_t n_quants,
+                               const float* scales, size_t n_scales,
+                               size_t block_size, float* out, size_t n_out,
+                               int mem);
+int barq_rocm_quantized_matmul_split(barq_rocm_handle* h, const float* a,
+                                     const uint8_t* b_quantized, size_t n_bq,
+                                     const float* b_scales, size_t n_bscales,
+                                     float* c, size_t m, size_t n, size_t k,
+                                     int kind, size_t block_size, int mem);
+
+/* quant::Q4_0::quantize (quant/src/q4_0.rs:23-67): f32 -> 20-byte
+ * BARQ_TYPE_Q4_0_BARQ blocks, bit-identical.  n must be a multiple of 32. */
+int barq_rocm_quantize_q4_0_barq(barq_rocm_handle* h, const float* x, size_t n,
+                                 uint8_t* out, int mem);
+
+/* ---- fused MoE ---------------------------------------------------------
+ * MoEFusedOps (models/src/moe_fused.rs:41-309).
+ * route: select_top_k_experts (:95-144) — per row, the top_k logits
+ *   (descending, stable), softmax over the kept k; ids/weights are
+ *   rows x top_k.
+ * ffn: dispatch_experts (:226-308) with fused_ffn (:84-92) as every expert:
+ *   out[t] = sum over t's experts e, ascending e, of
+ *   w[t,e] * ( (silu(x_t G_e^T) * (x_t U_e^T)) D_e^T ).
+ *   gate/up are [n_ff x hidden], down is [hidden x n_ff] GGUF weights; the
+ *   three arrays hold n_experts pointers (host arrays of `mem` pointers).
+ *   act = BARQ_ACT_F32_Q8 runs the integer path (rows and the gated hidden
+ *   quantized to Q8_K); act = BARQ_ACT_F32 keeps f32 activations. */
+int barq_rocm_moe_route(barq_rocm_handle* h, const float* logits, size_t rows,
+                        size_t n_experts, size_t top_k, int32_t* ids,
+                        float* weights, int mem);
+int barq_rocm_moe_ffn(barq_rocm_handle* h, size_t n_experts,
+                      int gate_type, const void* const* gate,
+                      int up_type, const void* const* up,
+                      int down_type, const void* const* down,
+                      size_t hidden, size_t n_ff, const float* x, size_t rows,
+                      const int32_t* ids, const float* weights, size_t top_k,
+                      int act, float* out, int mem);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BARQ_ROCM_H */

@@ -1,0 +1,279 @@
+"""ctypes binding of the CPU oracle (oracle/_build/libbarq_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for libbarq_rocm and the timed
+CPU baseline.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module.  Every function restates the
+reference (see the citations in barq_oracle.c).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libbarq_oracle.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, Q4_0_BARQ = 0, 1, 2, 8, 12, 14, 15, 0x10002
+
+_lib = None
+_vp, _sz, _i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        l = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_block_elems": (_sz, [_i]),
+            "orc_block_bytes": (_sz, [_i]),
+            "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_dequantize": (_sz, [_i, _vp, _sz, _vp]),
+            "orc_get_scale_min_k4": (None, [_i, _vp, _vp, _vp]),
+            "orc_pack_scale_min_k4": (None, [_vp, _vp, _vp]),
+            "orc_q4_0_gguf_to_barq": (None, [_vp, _sz, _vp]),
+            "orc_quantize_q8_0": (None, [_vp, _sz, _vp]),
+            "orc_quantize_q8_k": (None, [_vp, _sz, _vp]),
+            "orc_gemv_f32": (None, [_vp, _vp, _sz, _sz, _vp]),
+            "orc_gemm_f32": (None, [_vp, _vp, _sz, _sz, _sz, _vp]),
+            "orc_matvec": (_i, [_i, _vp, _sz, _sz, _i, _vp, _vp]),
+            "orc_matmul": (_i, [_i, _vp, _sz, _sz, _i, _vp, _sz, _vp]),
+            "orc_q4_0_quantize_barq": (_sz, [_vp, _sz, _vp]),
+            "orc_dequantize_packed_4bit_split": (None, [_vp, _sz, _vp, _sz, _sz, _vp, _sz]),
+            "orc_dequantize_signed_8bit_split": (None, [_vp, _sz, _vp, _sz, _sz, _vp, _sz]),
+            "orc_quantized_matmul_split": (None, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _i, _sz, _vp]),
+            "orc_moe_select_top_k": (_sz, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "orc_moe_batch_by_expert": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
+            "orc_moe_dispatch": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
+            "orc_moe_ffn": (_i, [_i, _vp, _i, _vp, _i, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp]),
+            "cpub_gemm_literal_m1": (None, [_vp, _vp, _sz, _sz, _sz, _sz, _vp]),
+            "cpub_gemv_simd": (None, [_vp, _vp, _sz, _sz, _sz, _vp]),
+            "cpub_gemv_simd_threaded": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _i]),
+            "cpub_simd_level": (_i, []),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def block_elems(t):
+    return lib().orc_block_elems(t)
+
+
+def block_bytes(t):
+    return lib().orc_block_bytes(t)
+
+
+def row_bytes(t, k):
+    return k // block_elems(t) * block_bytes(t)
+
+
+def f16_to_f32(bits: int) -> float:
+    return lib().orc_f16_to_f32(bits)
+
+
+def f32_to_f16(v: float) -> int:
+    return lib().orc_f32_to_f16(v)
+
+
+def dequantize(t: int, blocks: np.ndarray, n: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    r = lib().orc_dequantize(t, _p(blocks), n, _p(out))
+    if r == ctypes.c_size_t(-1).value:
+        raise ValueError(f"unsupported type {t}")
+    return out
+
+
+def get_scale_min_k4(j: int, q: np.ndarray):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    sc, m = ctypes.c_uint8(), ctypes.c_uint8()
+    lib().orc_get_scale_min_k4(j, _p(q), ctypes.addressof(sc), ctypes.addressof(m))
+    return sc.value, m.value
+
+
+def pack_scale_min_k4(ls, lm) -> np.ndarray:
+    ls = np.ascontiguousarray(ls, dtype=np.uint8)
+    lm = np.ascontiguousarray(lm, dtype=np.uint8)
+    out = np.empty(12, dtype=np.uint8)
+    lib().orc_pack_scale_min_k4(_p(ls), _p(lm), _p(out))
+    return out
+
+
+def q4_0_gguf_to_barq(gguf: np.ndarray) -> np.ndarray:
+    gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
+    nb = gguf.size // 18
+    out = np.empty(nb * 20, dtype=np.uint8)
+    lib().orc_q4_0_gguf_to_barq(_p(gguf), nb, _p(out))
+    return out
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+    lib().orc_quantize_q8_0(_p(x), x.size, _p(out))
+    return out
+
+
+def quantize_q8_k(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // 256 * 292, dtype=np.uint8)
+    lib().orc_quantize_q8_k(_p(x), x.size, _p(out))
+    return out
+
+
+def quantize_act(act_type: int, x: np.ndarray) -> np.ndarray:
+    return quantize_q8_0(x) if act_type == Q8_0 else quantize_q8_k(x)
+
+
+def gemv_f32(a: np.ndarray, x: np.ndarray, m: int, n: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(m, dtype=np.float32)
+    lib().orc_gemv_f32(_p(a), _p(x), m, n, _p(y))
+    return y
+
+
+def gemm_f32(a: np.ndarray, b: np.ndarray, m: int, k: int, n: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_gemm_f32(_p(a), _p(b), m, k, n, _p(c))
+    return c
+
+
+def matmul(w_type: int, w: np.ndarray, n_rows: int, k: int, act_type: int, x: np.ndarray, m: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x)
+    y = np.empty((m, n_rows), dtype=np.float32)
+    rc = lib().orc_matmul(w_type, _p(w), n_rows, k, act_type, _p(x), m, _p(y))
+    if rc:
+        raise ValueError("orc_matmul: bad type or shape")
+    return y
+
+
+def matvec(w_type, w, n_rows, k, act_type, x) -> np.ndarray:
+    return matmul(w_type, w, n_rows, k, act_type, x, 1)[0]
+
+
+def q4_0_quantize_barq(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nb = (x.size + 31) // 32
+    out = np.zeros(nb * 20, dtype=np.uint8)
+    n = lib().orc_q4_0_quantize_barq(_p(x), x.size, _p(out))
+    return out[:n]
+
+
+def dequantize_split(kind_q8_0: bool, quants, scales, block_size, n_out) -> np.ndarray:
+    quants = np.ascontiguousarray(quants, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    out = np.zeros(n_out, dtype=np.float32)
+    f = lib().orc_dequantize_signed_8bit_split if kind_q8_0 else lib().orc_dequantize_packed_4bit_split
+    f(_p(quants), quants.size, _p(scales), scales.size, block_size, _p(out), n_out)
+    return out
+
+
+def quantized_matmul_split(a, bq, bs, m, n, k, kind_q8_0: bool, block_size) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    bq = np.ascontiguousarray(bq, dtype=np.uint8)
+    bs = np.ascontiguousarray(bs, dtype=np.float32)
+    c = np.empty((m, n), dtype=np.float32)
+    lib().orc_quantized_matmul_split(_p(a), _p(bq), bq.size, _p(bs), bs.size, m, n, k, int(kind_q8_0), block_size, _p(c))
+    return c
+
+
+def moe_select_top_k(logits: np.ndarray, k: int):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, cols = logits.shape
+    kk = max(1, min(k, cols))
+    ids = np.empty((rows, kk), dtype=np.int32)
+    w = np.empty((rows, kk), dtype=np.float32)
+    got = lib().orc_moe_select_top_k(_p(logits), rows, cols, k, _p(ids), _p(w))
+    assert got == kk
+    return ids, w
+
+
+def moe_batch_by_expert(ids: np.ndarray, weights: np.ndarray, n_experts: int):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    rows, k = ids.shape
+    off = np.empty(n_experts + 1, dtype=np.int32)
+    tok = np.full(rows * k, -1, dtype=np.int32)
+    wts = np.zeros(rows * k, dtype=np.float32)
+    lib().orc_moe_batch_by_expert(_p(ids), _p(weights), rows, k, n_experts, _p(off), _p(tok), _p(wts))
+    return off, tok[: off[-1]], wts[: off[-1]]
+
+
+EXPERT_FN = ctypes.CFUNCTYPE(_i, _i, ctypes.POINTER(ctypes.c_float), _sz, _sz, ctypes.POINTER(ctypes.c_float), _vp)
+
+
+def moe_dispatch(x: np.ndarray, n_experts: int, ids: np.ndarray, weights: np.ndarray, expert_fns) -> np.ndarray:
+    """dispatch_experts with Python expert closures f(batch [rows x hidden]) -> [rows x hidden]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    rows, hidden = x.shape
+
+    def tramp(e, inp, r, h, outp, ctx):
+        a = np.ctypeslib.as_array(inp, shape=(r, h)).copy()
+        res = np.asarray(expert_fns[e](a), dtype=np.float32)
+        np.ctypeslib.as_array(outp, shape=(r, h))[:] = res
+        return 0
+
+    cb = EXPERT_FN(tramp)
+    out = np.empty((rows, hidden), dtype=np.float32)
+    rc = lib().orc_moe_dispatch(_p(x), rows, hidden, n_experts, _p(ids), _p(weights), ids.shape[1],
+                                ctypes.cast(cb, _vp), None, _p(out))
+    if rc:
+        raise ValueError("orc_moe_dispatch failed")
+    return out
+
+
+def moe_ffn(gate_type, gates, up_type, ups, down_type, downs, hidden, n_ff, x, ids, weights, act) -> np.ndarray:
+    ne = len(gates)
+    arr = _vp * ne
+    gates = [np.ascontiguousarray(g, dtype=np.uint8) for g in gates]
+    ups = [np.ascontiguousarray(g, dtype=np.uint8) for g in ups]
+    downs = [np.ascontiguousarray(g, dtype=np.uint8) for g in downs]
+    g = arr(*[_p(t) for t in gates])
+    u = arr(*[_p(t) for t in ups])
+    d = arr(*[_p(t) for t in downs])
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    rows = x.shape[0]
+    out = np.empty((rows, hidden), dtype=np.float32)
+    rc = lib().orc_moe_ffn(gate_type, g, up_type, u, down_type, d, ne, hidden, n_ff, _p(x), rows, _p(ids),
+                           _p(weights), ids.shape[1], act, _p(out))
+    if rc:
+        raise ValueError("orc_moe_ffn failed")
+    return out
+
+
+# ---- CPU baseline variants (bench.py's cpu_baseline leg) -----------------
+def cpub_gemm_literal_m1(x, w_t, k, n, j0, j1, y):
+    lib().cpub_gemm_literal_m1(_p(x), _p(w_t), k, n, j0, j1, _p(y))
+
+
+def cpub_gemv_simd(a, x, n, r0, r1, y):
+    lib().cpub_gemv_simd(_p(a), _p(x), n, r0, r1, _p(y))
+
+
+def cpub_gemv_simd_threaded(a, x, n, r0, r1, y, threads) -> int:
+    return lib().cpub_gemv_simd_threaded(_p(a), _p(x), n, r0, r1, _p(y), threads)
+
+
+def cpub_simd_level() -> int:
+    return lib().cpub_simd_level()

@@ -1,0 +1,61 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "barq-inference_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and libbarq_rocm.so")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    from oracle import oracle
+    oracle.lib()
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def be():
+    """libbarq_rocm handle on device 0 (GPU tests only; never falls back)."""
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    from barq_rocm import Backend
+    b = Backend(0)
+    yield b
+    b.close()
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def assert_close_1e3(y, ref, tol=1e-3):
+    """The parity bar for matvec/matmul outputs: relative L2 error <= tol and
+    max |y - ref| <= tol * max |ref|."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert y.shape == ref.shape, (y.shape, ref.shape)
+    r = rel_err(y, ref)
+    m = float(np.max(np.abs(y - ref))) if y.size else 0.0
+    lim = tol * float(np.max(np.abs(ref))) if ref.size else 0.0
+    assert r <= tol, f"relative L2 error {r:.3e} > {tol}"
+    assert m <= lim, f"max abs error {m:.3e} > {lim:.3e}"
+
+
+def assert_bits_equal(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    assert a.shape == b.shape
+    ua, ub = a.view(np.uint32), b.view(np.uint32)
+    bad = np.nonzero(ua != ub)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first at {bad[:5]}: {a[bad[:5]]} vs {b[bad[:5]]}"

@@ -1,0 +1,288 @@
+"""GPU parity: libbarq_rocm (through the C ABI) against the CPU oracle.
+
+Bars: dequantized weights and quantized activations bit-exact; matvec and
+matmul outputs within 1e-3 (relative L2 and max-abs relative to max |y|),
+the tolerance the north star states.  The oracle for the Q8 paths runs on
+the same quantized activations the GPU produced (after checking those are
+bit-exact with the oracle's own quantization)."""
+import numpy as np
+import pytest
+
+import barq_rocm as B
+from barq_rocm import synth
+from conftest import assert_bits_equal, assert_close_1e3
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q4_0": B.Q4_0, "Q4_0_BARQ": B.Q4_0_BARQ, "Q8_0": B.Q8_0, "Q4_K": B.Q4_K, "Q6_K": B.Q6_K}
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def special_blocks(t, nb, seed):
+    """Random blocks with edge values mixed in: f16 subnormal / zero / max
+    scales, all-0x00 and all-0xFF payloads."""
+    bb = B.BLOCK_BYTES[t]
+    w = synth.gen_weights(t, nb, B.BLOCK_ELEMS[t], seed).reshape(nb, bb).copy()
+    rng = np.random.default_rng(seed)
+    f16s = np.float16([0.0, 2.0 ** -24, 6.1e-5, 65504.0, -1.5, 1.0]).view(np.uint8).reshape(-1, 2)
+    for i in range(0, nb, 7):
+        if t in (B.Q4_0, B.Q8_0):
+            w[i, 0:2] = f16s[i % 6]
+        elif t == B.Q4_K:
+            w[i, 0:2] = f16s[i % 6]
+            w[i, 2:4] = f16s[(i + 1) % 6]
+        elif t == B.Q6_K:
+            w[i, 208:210] = f16s[i % 6]
+        elif t == B.Q4_0_BARQ:
+            w[i, 0:4] = np.float32([0.0, 1e-40, 3.4e38, -2.0, 1.0, 0.125])[i % 6:i % 6 + 1].view(np.uint8)
+        if i % 3 == 0:
+            off = 4 if t == B.Q4_0_BARQ else (0 if t == B.Q6_K else 2 if t != B.Q4_K else 16)
+            end = 208 if t == B.Q6_K else bb
+            w[i, off:end] = 0xFF if i % 2 else 0x00
+    return w.reshape(-1)
+
+
+# ---- dequantize: bit-exact -------------------------------------------------
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_dequantize_bit_exact(be, orc, name):
+    t = TYPES[name]
+    nb = 3001
+    w = special_blocks(t, nb, 11)
+    n = nb * B.BLOCK_ELEMS[t]
+    print(f"dequantize {name} n={n}", flush=True)
+    got = host(be.dequantize(t, dev(w), n))
+    ref = orc.dequantize(t, w, n)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin)
+    assert_bits_equal(got[fin], ref[fin])
+
+
+def test_dequantize_f16_all_patterns(be, orc):
+    bits = np.arange(65536, dtype=np.uint16).view(np.uint8)
+    got = host(be.dequantize(B.F16, dev(bits), 65536))
+    ref = orc.dequantize(orc.F16, bits, 65536)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_bits_equal(got[~nan], ref[~nan])
+
+
+def test_dequantize_host_memory(be, orc):
+    w = synth.gen_q4_k(33, 512, 5)
+    out = np.empty(33 * 512, np.float32)
+    be.dequantize_raw(B.Q4_K, w, out.size, out, B.MEM_HOST)
+    assert_bits_equal(out, orc.dequantize(orc.Q4_K, w, out.size))
+
+
+# ---- activation quantizers: bit-exact --------------------------------------
+
+def act_rows(k, rows, seed):
+    x = synth.gen_f32(rows * k, seed).reshape(rows, k)
+    x[1 % rows, :] = 0.0                                   # zero rows / blocks
+    x[2 % rows, 7] = 1e4                                   # one huge value
+    x[3 % rows, :] *= 1e-6                                 # tiny values
+    if rows > 4:
+        x[4, :64] = np.float32(np.arange(64) - 31.5)        # many ties after scaling
+        x[4, 100], x[4, 200] = 9.0, -9.0                    # |max| tie: first wins
+    return x
+
+
+@pytest.mark.parametrize("act", ["Q8_0", "Q8_K"])
+def test_quantize_act_bit_exact(be, orc, act):
+    at = getattr(B, act)
+    for k, rows in [(256, 8), (4096, 5), (14336, 3)]:
+        x = act_rows(k, rows, 21 + k)
+        print(f"quantize {act} k={k} rows={rows}", flush=True)
+        got = host(be.quantize_act(at, dev(x)))
+        ref = np.concatenate([orc.quantize_act(at, x[r]) for r in range(rows)])
+        assert np.array_equal(got, ref)
+
+
+def test_quantize_q4_0_barq_bit_exact(be, orc):
+    x = act_rows(4096, 6, 31).reshape(-1)
+    got = host(be.quantize_q4_0_barq(dev(x)))
+    assert np.array_equal(got, orc.q4_0_quantize_barq(x))
+
+
+# ---- matvec ----------------------------------------------------------------
+
+SHAPES_K = [(1, 256), (5, 512), (67, 4096), (33, 4352), (129, 14336), (1023, 768)]
+SHAPES_32 = [(1, 32), (7, 96), (67, 4096), (33, 4128), (130, 4064)]
+
+
+def shapes_for(t):
+    return SHAPES_K if B.BLOCK_ELEMS[t] == 256 else SHAPES_32
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_matvec_q8_activations(be, orc, name):
+    t = TYPES[name]
+    at = B.Q8_PARTNER[t]
+    for n, k in shapes_for(t):
+        w = synth.gen_weights(t, n, k, 100 + n)
+        x = synth.gen_f32(k, 200 + k)
+        print(f"matvec {name} x {at} n={n} k={k}", flush=True)
+        xq = be.quantize_act(at, dev(x))
+        assert np.array_equal(host(xq), orc.quantize_act(at, x))
+        y = host(be.matvec(t, dev(w), n, k, at, xq))
+        ref = orc.matvec(t, w, n, k, at, host(xq))
+        assert_close_1e3(y, ref)
+        # library-side quantization gives the same result
+        y2 = host(be.matvec(t, dev(w), n, k, B.ACT_F32_Q8, dev(x)))
+        assert np.array_equal(y, y2)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_matvec_f32_activations_literal(be, orc, name):
+    # the literal reference path: gemv_f32(dequant(W), x)
+    t = TYPES[name]
+    for n, k in shapes_for(t):
+        w = synth.gen_weights(t, n, k, 300 + n)
+        x = synth.gen_f32(k, 400 + k)
+        print(f"matvec {name} x f32 n={n} k={k}", flush=True)
+        y = host(be.matvec(t, dev(w), n, k, B.ACT_F32, dev(x)))
+        ref = orc.matvec(t, w, n, k, orc.F32, x)
+        assert_close_1e3(y, ref, tol=1e-5)
+
+
+def test_matvec_host_memory(be, orc):
+    n, k = 100, 4096
+    w = synth.gen_q4_k(n, k, 7)
+    x = synth.gen_f32(k, 8)
+    y = np.empty(n, np.float32)
+    be.matvec_raw(B.Q4_K, w, n, k, B.ACT_F32_Q8, x, y, B.MEM_HOST)
+    ref = orc.matvec(B.Q4_K, w, n, k, B.Q8_K, orc.quantize_q8_k(x))
+    assert_close_1e3(y, ref)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_matvec_full_baseline_configs(be, orc, cfg):
+    """C1 Q4_0 4096x4096, C2 Q4_K 14336x4096, C3 Q6_K 128256x4096 at full size."""
+    t, w, x = synth.linear_inputs(cfg)
+    c = synth.CONFIGS[cfg]
+    n, k = c["n_rows"], c["k"]
+    at = B.Q8_PARTNER[t]
+    print(f"full config C{cfg}", flush=True)
+    xq = be.quantize_act(at, dev(x[0]))
+    assert np.array_equal(host(xq), orc.quantize_act(at, x[0]))
+    y = host(be.matvec(t, dev(w), n, k, at, xq))
+    ref = orc.matvec(t, w, n, k, at, host(xq))
+    assert_close_1e3(y, ref)
+    # gap to the literal f32-activation reference, information only
+    lit = orc.matvec(t, w, n, k, orc.F32, x[0])
+    rel = float(np.linalg.norm(y.astype(np.float64) - lit) / np.linalg.norm(lit))
+    print(f"C{cfg}: Q8-activation gap to literal f32 reference {rel:.2e}")
+    assert rel < 2e-2
+
+
+# ---- matmul ----------------------------------------------------------------
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_matmul_q8(be, orc, name):
+    t = TYPES[name]
+    at = B.Q8_PARTNER[t]
+    k = 512 if B.BLOCK_ELEMS[t] == 256 else 256
+    for n, m in [(40, 3), (96, 17), (257, 33)]:
+        w = synth.gen_weights(t, n, k, 500 + n)
+        x = synth.gen_f32(m * k, 600 + m).reshape(m, k)
+        print(f"matmul {name} n={n} k={k} m={m}", flush=True)
+        xq = be.quantize_act(at, dev(x))
+        y = host(be.matmul(t, dev(w), n, k, at, xq, m))
+        ref = orc.matmul(t, w, n, k, at, host(xq), m)
+        assert_close_1e3(y, ref)
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q4_0"])
+def test_matmul_f32_literal_bit_exact(be, orc, name):
+    # dequantize (bit-exact) + sequential unfused f32 GEMM == the reference's
+    # gemm_f32(X, W^T) bit for bit
+    t = TYPES[name]
+    n, k, m = 70, 512, 5
+    w = synth.gen_weights(t, n, k, 700)
+    x = synth.gen_f32(m * k, 701).reshape(m, k)
+    y = host(be.matmul(t, dev(w), n, k, B.ACT_F32, dev(x), m))
+    assert_bits_equal(y, orc.matmul(t, w, n, k, orc.F32, x, m))
+
+
+# ---- f32 BLAS and the split-scale API: bit-exact ------------------------------
+
+def test_gemm_gemv_f32_reference_known_answers(be):
+    a = np.float32([1, 2, 3, 4]); b = np.float32([5, 6, 7, 8])
+    assert be.gemm_f32(a, b, 2, 2, 2, B.MEM_HOST).reshape(-1).tolist() == [19, 22, 43, 50]
+    a = np.float32([1, 2, 3, 4, 5, 6]); b = np.float32([7, 8, 9, 10, 11, 12])
+    assert be.gemm_f32(a, b, 2, 3, 2, B.MEM_HOST).reshape(-1).tolist() == [58, 64, 139, 154]
+    assert be.gemv_f32(np.float32([1, 2, 3, 4]), np.float32([5, 6]), 2, 2, B.MEM_HOST).tolist() == [17, 39]
+    assert be.gemv_f32(np.float32([1e8, 1, -1e8]), np.float32([1, 1, 1]), 1, 3, B.MEM_HOST)[0] == 0.0
+
+
+def test_gemm_gemv_f32_bit_exact(be, orc):
+    rng = np.random.default_rng(9)
+    for m, k, n in [(1, 4096, 300), (67, 129, 65), (128, 256, 192)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        assert_bits_equal(host(be.gemm_f32(dev(a), dev(b), m, k, n)), orc.gemm_f32(a, b, m, k, n))
+    a = rng.standard_normal((1000, 4099)).astype(np.float32)
+    x = rng.standard_normal(4099).astype(np.float32)
+    assert_bits_equal(host(be.gemv_f32(dev(a), dev(x), 1000, 4099)), orc.gemv_f32(a, x, 1000, 4099))
+
+
+def test_split_api_bit_exact(be, orc):
+    rng = np.random.default_rng(10)
+    for bs in (32, 256, 5):
+        nsc = 40
+        q = rng.integers(0, 256, nsc * ((bs + 1) // 2) - 3).astype(np.uint8)
+        s = rng.standard_normal(nsc).astype(np.float32)
+        for kind_q8 in (False, True):
+            qq = rng.integers(0, 256, nsc * bs - 3).astype(np.uint8) if kind_q8 else q
+            got = be.dequantize_split(B.Q8_0 if kind_q8 else B.Q4_K, qq, s, bs, nsc * bs + 7)
+            assert_bits_equal(got, orc.dequantize_split(kind_q8, qq, s, bs, nsc * bs + 7))
+    # the reference's own tests (cuda_quant.rs:345-373)
+    assert be.dequantize_split(B.Q4_K, np.uint8([0x88, 0x88]), np.float32([1.0]), 4, 4).tolist() == [-8.0] * 4
+    c = be.quantized_matmul_split(np.float32([1, 2, 3, 4]), np.uint8([0x11, 0x11]), np.float32([1.0]), 2, 2, 2, B.Q4_K, 4)
+    assert c.reshape(-1).tolist() == [3.0, 3.0, 7.0, 7.0]
+    m, n, k = 9, 40, 96
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bq = rng.integers(0, 256, k * n // 2).astype(np.uint8)
+    bsc = rng.standard_normal(k * n // 32).astype(np.float32)
+    got = be.quantized_matmul_split(a, bq, bsc, m, n, k, B.Q4_K, 32)
+    assert_bits_equal(got, orc.quantized_matmul_split(a, bq, bsc, m, n, k, False, 32))
+
+
+# ---- MoE -------------------------------------------------------------------
+
+def test_moe_route(be, orc):
+    logits = synth.gen_f32(64 * 8, 5).reshape(64, 8)
+    logits[3, :] = np.float32([1, 3, 3, 0, 0, 0, 0, 0])      # tie: lower index first
+    ids, w = be.moe_route(dev(logits), 64, 8, 2)
+    rid, rw = orc.moe_select_top_k(logits, 2)
+    assert np.array_equal(host(ids), rid)
+    assert np.allclose(host(w), rw, rtol=1e-6, atol=1e-7)
+    ids, _ = be.moe_route(np.float32([[0.1, 2.0, 1.0, -1.0], [3.0, 0.0, 1.5, 1.0]]), 2, 4, 2, B.MEM_HOST)
+    assert ids.tolist() == [[1, 2], [0, 2]]
+
+
+@pytest.mark.parametrize("act", ["q8", "f32"])
+def test_moe_ffn_small(be, orc, act):
+    ne, hid, nff, rows, k = 4, 512, 1024, 24, 2
+    gates = [synth.gen_q4_k(nff, hid, 10 + e) for e in range(ne)]
+    ups = [synth.gen_q4_k(nff, hid, 20 + e) for e in range(ne)]
+    downs = [synth.gen_q6_k(hid, nff, 30 + e) for e in range(ne)]
+    x = synth.gen_f32(rows * hid, 40).reshape(rows, hid)
+    ids, w = orc.moe_select_top_k(synth.gen_f32(rows * ne, 41).reshape(rows, ne), k)
+    a = B.ACT_F32_Q8 if act == "q8" else B.ACT_F32
+    out = be.moe_ffn(B.Q4_K, [dev(g) for g in gates], B.Q4_K, [dev(u) for u in ups], B.Q6_K,
+                     [dev(d) for d in downs], hid, nff, dev(x), rows, dev(ids), dev(w), k, a)
+    ref = orc.moe_ffn(B.Q4_K, gates, B.Q4_K, ups, B.Q6_K, downs, hid, nff, x, ids, w,
+                      orc.Q8_K if act == "q8" else orc.F32)
+    assert_close_1e3(host(out), ref)
+    # host-memory entry point gives the same result
+    out_h = be.moe_ffn(B.Q4_K, gates, B.Q4_K, ups, B.Q6_K, downs, hid, nff, x, rows, ids, w, k, a, mem=B.MEM_HOST)
+    assert np.array_equal(out_h, host(out))
