@@ -104,6 +104,33 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (a + b) + (c + d);
 }
 
+// Sum R per-lane partials (one per row) over the 64 lanes with the gfx950
+// lane-swap instructions: two rows fold into one register per swap, so R rows
+// cost ~R/2 swaps + one 16-lane DPP reduction instead of R full reductions.
+// Afterwards lane row_lane4(r) holds the total of row r.
+__device__ __forceinline__ float swap32_add(float a, float b) {
+    auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), false, false);
+    // s[0] = [a lanes 0-31 | b lanes 0-31], s[1] = [a lanes 32-63 | b lanes 32-63]
+    return __builtin_bit_cast(float, (int)s[0]) + __builtin_bit_cast(float, (int)s[1]);
+}
+
+// rows of 16 lanes: a = [a0 a1 a2 a3], b = [b0 b1 b2 b3] -> [a0+a1, b0+b1, a2+a3, b2+b3]
+__device__ __forceinline__ float swap16_add(float a, float b) {
+    auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), false, false);
+    return __builtin_bit_cast(float, (int)s[0]) + __builtin_bit_cast(float, (int)s[1]);
+}
+
+// r -> lane holding its total after reduce4 (rows a,b,c,d -> 0, 32, 16, 48)
+__host__ __device__ constexpr int row_lane4(int r) { return r == 0 ? 0 : r == 1 ? 32 : r == 2 ? 16 : 48; }
+
+// Reduce up to four rows; unused rows pass 0.
+__device__ __forceinline__ float reduce4(float a, float b, float c, float d) {
+    const float ab = swap32_add(a, b);   // [a 32 | b 32]
+    const float cd = swap32_add(c, d);   // [c 32 | d 32]
+    const float v = swap16_add(ab, cd);     // rows of 16: a, c, b, d
+    return row16_sum(v);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;

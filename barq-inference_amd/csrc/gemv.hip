@@ -13,104 +13,101 @@
 #include "gemv_formats.hpp"
 #include "launch.hpp"
 
+#include <cstdio>
+#include <cstdlib>
+
 namespace barq {
 
-template <class F>
-__device__ __forceinline__ void stage_act(const ActLds& a, const uint8_t* __restrict__ xq, int k) {
-    if constexpr (F::ACT_BLOCK == 256) {
-        stage_q8k(a, xq, k / 256);
-    } else {
-        stage_q8_0_copy(a, xq, k / 32);
-        __syncthreads();
-        stage_sums16(a, k);
-    }
-}
-
+// Integer path.  Per wave: the lane's activation slice is loaded first (it is
+// shared by all rows), then the weight slices of all R rows are issued before
+// any arithmetic (the scheduling barrier keeps the compiler from sinking them
+// next to their uses), so each wave has R rows of HBM traffic in flight.
 template <class F, int R, int WAVES>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
                     float* __restrict__ y, int n_rows, int k) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const ActLds a = act_lds_layout(smem, k, F::ACT_BLOCK);
-    stage_act<F>(a, xq, k);
-    __syncthreads();
-
-    const int lane = threadIdx.x & 63;
+    const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * WAVES + wave) * R;
     if (row0 >= n_rows) return;
+    const typename F::Lane c = F::lane(l);
     const int nblk = k / F::ROW_BLOCK_ELEMS;
     const int n_it = (k + 4095) / 4096;
+    const int last = n_rows - 1 - row0;
+    const uint8_t* wrow = W + (size_t)row0 * row_bytes;
 
     float acc[R];
     #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
 
     for (int it = 0; it < n_it; it++) {
-        const bool act = F::active(it, lane, nblk);
-        typename F::X xs;
-        typename F::Wt w[R];
-        if (act) {
+        if (F::active(it, c, nblk)) {
+            typename F::X xs;
+            F::load_x(xs, xq, it, c, nblk);
+            typename F::Wt w[R];
             #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int row = min(row0 + r, n_rows - 1);
-                if constexpr (F::LANES_PER_BLOCK) F::load_w(w[r], W + (size_t)row * row_bytes, it, lane);
-                else F::load_w(w[r], W + (size_t)row * row_bytes, it, lane, nblk);
-            }
-            if constexpr (F::LANES_PER_BLOCK) F::load_x(xs, a, it, lane);
-            else F::load_x(xs, a, it, lane, nblk);
+            for (int r = 0; r < R; r++) F::load_w(w[r], wrow + (size_t)min(r, last) * row_bytes, it, c, nblk);
+            __builtin_amdgcn_sched_barrier(0);
             #pragma unroll
-            for (int r = 0; r < R; r++) acc[r] += F::dot(w[r], xs, lane);
+            for (int r = 0; r < R; r++) acc[r] += F::dot(w[r], xs, c);
         }
     }
 
     #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const float s = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < n_rows) y[row0 + r] = s;
+    for (int g = 0; g < R; g += 4) {
+        const float v = reduce4(acc[g], g + 1 < R ? acc[g + 1] : 0.0f, g + 2 < R ? acc[g + 2] : 0.0f,
+                                g + 3 < R ? acc[g + 3] : 0.0f);
+        if ((l & 15) == 0) {
+            const int rr = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+            if (rr < R && rr <= last) y[row0 + rr] = v;
+        }
     }
 }
 
+// Literal path: x (f32) staged in LDS, weights dequantized in registers.
 template <class F, int R, int WAVES>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_f32_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const float* __restrict__ x,
                      float* __restrict__ y, int n_rows, int k) {
     extern __shared__ __align__(16) uint8_t smem[];
     float* xs = reinterpret_cast<float*>(smem);
-    stage_f32(xs, x, k);
+    {
+        const float4* src = reinterpret_cast<const float4*>(x);
+        float4* dst = reinterpret_cast<float4*>(xs);
+        for (int t = threadIdx.x; t < k / 4; t += blockDim.x) dst[t] = src[t];
+    }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63;
+    const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * WAVES + wave) * R;
     if (row0 >= n_rows) return;
+    const typename F::Lane c = F::lane(l);
     const int nblk = k / F::ROW_BLOCK_ELEMS;
     const int n_it = (k + 4095) / 4096;
+    const int last = n_rows - 1 - row0;
+    const uint8_t* wrow = W + (size_t)row0 * row_bytes;
 
     float acc[R];
     #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
 
     for (int it = 0; it < n_it; it++) {
-        if (!F::active(it, lane, nblk)) continue;
+        if (!F::active(it, c, nblk)) continue;
         typename F::Wt w[R];
         #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = min(row0 + r, n_rows - 1);
-            if constexpr (F::LANES_PER_BLOCK) F::load_w(w[r], W + (size_t)row * row_bytes, it, lane);
-            else F::load_w(w[r], W + (size_t)row * row_bytes, it, lane, nblk);
-        }
+        for (int r = 0; r < R; r++) F::load_w(w[r], wrow + (size_t)min(r, last) * row_bytes, it, c, nblk);
         // two-block formats: the second block of the last lane may be absent
         const int kbase = it * 4096;
         #pragma unroll
         for (int g = 0; g < 16; g++) {
-            const int off = kbase + F::xoff(lane, g);
+            const int off = kbase + F::xoff(l, g);
             if (off >= k) continue;
             const float4 xv = *reinterpret_cast<const float4*>(xs + off);
             #pragma unroll
             for (int r = 0; r < R; r++) {
                 float v[4];
-                F::deq4(w[r], lane, g, v);
+                F::deq4(w[r], c, g, v);
                 acc[r] = __builtin_fmaf(v[0], xv.x, acc[r]);
                 acc[r] = __builtin_fmaf(v[1], xv.y, acc[r]);
                 acc[r] = __builtin_fmaf(v[2], xv.z, acc[r]);
@@ -120,9 +117,13 @@ void gemv_f32_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const floa
     }
 
     #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const float s = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < n_rows) y[row0 + r] = s;
+    for (int g = 0; g < R; g += 4) {
+        const float v = reduce4(acc[g], g + 1 < R ? acc[g + 1] : 0.0f, g + 2 < R ? acc[g + 2] : 0.0f,
+                                g + 3 < R ? acc[g + 3] : 0.0f);
+        if ((l & 15) == 0) {
+            const int rr = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+            if (rr < R && rr <= last) y[row0 + rr] = v;
+        }
     }
 }
 
@@ -130,7 +131,16 @@ void gemv_f32_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const floa
 // (rows per wave, waves per workgroup) for the integer path.  The default for
 // each format was chosen by sweeping on MI355X; gemv_set_config overrides it.
 struct GemvCfg { int r, waves; };
-static GemvCfg g_cfg_override = {0, 0};
+
+// BARQ_GEMV_CFG="R,W" overrides the launch shape (used for tuning sweeps).
+static GemvCfg read_env_cfg() {
+    GemvCfg c = {0, 0};
+    if (const char* e = getenv("BARQ_GEMV_CFG")) {
+        if (sscanf(e, "%d,%d", &c.r, &c.waves) != 2) c = {0, 0};
+    }
+    return c;
+}
+static GemvCfg g_cfg_override = read_env_cfg();
 
 void gemv_set_config(int rows_per_wave, int waves) { g_cfg_override = {rows_per_wave, waves}; }
 
@@ -139,8 +149,7 @@ static hipError_t launch_q8(const uint8_t* W, size_t row_bytes, const uint8_t* x
                             int n_rows, int k, hipStream_t s) {
     const int rows_per_block = R * WAVES;
     const unsigned grid = (unsigned)((n_rows + rows_per_block - 1) / rows_per_block);
-    const size_t lds = act_lds_bytes(k, F::ACT_BLOCK);
-    hipLaunchKernelGGL((gemv_q8_kernel<F, R, WAVES>), dim3(grid), dim3(WAVES * 64), lds, s,
+    hipLaunchKernelGGL((gemv_q8_kernel<F, R, WAVES>), dim3(grid), dim3(WAVES * 64), 0, s,
                        W, row_bytes, xq, y, n_rows, k);
     return hipGetLastError();
 }
@@ -175,18 +184,15 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     const int n = (int)n_rows, kk = (int)k;
     switch (w_type) {
-    case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, {4, 4});
-    case TYPE_Q6_K: return dispatch_q8<FmtQ6K>(w, k / 256 * 210, x, y, n, kk, s, {2, 4});
-    case TYPE_Q4_0: return dispatch_q8<FmtQ40>(w, k / 32 * 18, x, y, n, kk, s, {2, 4});
-    case TYPE_Q8_0: return dispatch_q8<FmtQ80>(w, k / 32 * 34, x, y, n, kk, s, {2, 4});
-    case TYPE_Q4_0_BARQ: return dispatch_q8<FmtQ40Barq>(w, k / 32 * 20, x, y, n, kk, s, {2, 4});
+    case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, {2, 2});
+    case TYPE_Q6_K: return dispatch_q8<FmtQ6K>(w, k / 256 * 210, x, y, n, kk, s, {1, 8});
+    case TYPE_Q4_0: return dispatch_q8<FmtQ40>(w, k / 32 * 18, x, y, n, kk, s, {1, 4});
+    case TYPE_Q8_0: return dispatch_q8<FmtQ80>(w, k / 32 * 34, x, y, n, kk, s, {1, 4});
+    case TYPE_Q4_0_BARQ: return dispatch_q8<FmtQ40Barq>(w, k / 32 * 20, x, y, n, kk, s, {1, 4});
     default: return hipErrorInvalidValue;
     }
 }
 
-size_t gemv_q8_lds_bytes(int w_type, size_t k) {
-    return act_lds_bytes((int)k, (w_type == TYPE_Q4_K || w_type == TYPE_Q6_K) ? 256 : 32);
-}
 
 hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
                            float* y, hipStream_t s) {

@@ -23,7 +23,6 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
                           float* y, hipStream_t s);
 hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
                            float* y, hipStream_t s);
-size_t gemv_q8_lds_bytes(int w_type, size_t k);
 void gemv_set_config(int rows_per_wave, int waves);
 
 // gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows)
