@@ -47,6 +47,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    p.add_argument("--no-traffic", action="store_true",
+                   help="skip the two rocprofv3 --pmc child runs that measure HBM traffic per launch")
+    p.add_argument("--probe-copy", action="store_true",
+                   help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
 
 
@@ -88,6 +92,52 @@ def time_launches(launch, K, eager):
     return t0.elapsed_time(t1) / K, "eager"
 
 
+KERNEL_OF_CONFIG = {1: "gemv_q8_kernel<barq::FmtQ40", 2: "gemv_q8_kernel<barq::FmtQ4K",
+                    3: "gemv_q8_kernel<barq::FmtQ6K", 4: "gemm_kq_kernel<barq::GQ4K"}
+
+
+def measure_traffic(config):
+    """HBM bytes per launch of the config's dominant kernel: two rocprofv3
+    child runs of this script (FETCH_SIZE, then WRITE_SIZE, in KiB per
+    dispatch), each scaled by what the same counter reads for a 256 MiB
+    device copy (--probe-copy).  Returns (bytes, detail) or (None, reason)."""
+    import csv
+    import shutil
+    import statistics as st
+    import subprocess
+    import tempfile
+
+    if not shutil.which("rocprofv3"):
+        return None, "rocprofv3 not found"
+    name = KERNEL_OF_CONFIG[config]
+    vals = {}
+    tmp = tempfile.mkdtemp(prefix="barq_pmc_")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = os.path.join(tmp, counter)
+        cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "t", "--",
+               sys.executable, os.path.abspath(__file__), "--config", str(config), "--steps", "10", "--warmup", "2",
+               "--no-cpu", "--no-traffic", "--probe-copy"]
+        try:
+            r = subprocess.run(cmd, cwd=tmp, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, timeout=180)
+        except subprocess.TimeoutExpired:
+            return None, f"{counter} run timed out"
+        files = [os.path.join(dp, f) for dp, _, fs in os.walk(out) for f in fs if f.endswith("counter_collection.csv")]
+        if r.returncode != 0 and not files:
+            return None, f"{counter} run failed: {r.stderr.decode(errors='replace')[-300:]}"
+        rows = [row for f in files for row in csv.DictReader(open(f))]
+        kern = [float(row["Counter_Value"]) for row in rows if name in row["Kernel_Name"]]
+        copies = [float(row["Counter_Value"]) for row in rows if "copyBuffer" in row["Kernel_Name"]][-5:]
+        if not kern or len(copies) < 5:
+            return None, f"{counter}: kernel or copy-probe dispatches missing"
+        vals[counter] = (st.median(kern), 262144.0 / st.median(copies))
+    shutil.rmtree(tmp, ignore_errors=True)
+    fk, fs = vals["FETCH_SIZE"]
+    wk, wsc = vals["WRITE_SIZE"]
+    traffic = (fk * fs + wk * wsc) * 1024.0
+    return traffic, dict(fetch_kib=round(fk, 1), fetch_scale=round(fs, 4), write_kib=round(wk, 1),
+                         write_scale=round(wsc, 4))
+
+
 def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
     """The reference's per-call CPU path on a bounded sample (oracle restatement)."""
     import numpy as np
@@ -99,31 +149,34 @@ def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
     # (i) literal: gemm_f32(x[1 x k], W^T[k x n]) column by column (blas.rs:199-210)
     w_t = np.ascontiguousarray(wf.reshape(n, k).T)          # weight_cache.rs:196-201
     y = np.zeros(n, np.float32)
-    j, t_used = 0, 0.0
+    # whole passes over the output columns, repeated until the budget is spent
+    done, t_used = 0, 0.0
     chunk = 256
-    while j < n and t_used < budget_s * 0.5:
+    while t_used < budget_s * 0.5:
+        j = done % n
         j1 = min(n, j + chunk)
         t0 = time.perf_counter()
         orc.cpub_gemm_literal_m1(x, w_t, k, n, j, j1, y)
         t_used += time.perf_counter() - t0
-        j = j1
-    lit_s = t_used * n / j
-    out["literal_1core"] = dict(us_per_call=lit_s * 1e6, cols_sampled=j, sample_s=round(t_used, 3))
+        done += j1 - j
+    lit_s = t_used * n / done
+    out["literal_1core"] = dict(us_per_call=lit_s * 1e6, cols_sampled=done, sample_s=round(t_used, 3))
     del w_t
     # (ii) reference SIMD dot per row (simd.rs:115-138), one thread
     a = wf
-    r, t_used = 0, 0.0
-    while r < n and t_used < budget_s * 0.25:
+    done, t_used = 0, 0.0
+    while t_used < budget_s * 0.25:
+        r = done % n
         r1 = min(n, r + 512)
         t0 = time.perf_counter()
         orc.cpub_gemv_simd(a, x, k, r, r1, y)
         t_used += time.perf_counter() - t0
-        r = r1
-    simd_s = t_used * n / r
-    out["simd_1core"] = dict(us_per_call=simd_s * 1e6, rows_sampled=r, sample_s=round(t_used, 3))
+        done += r1 - r
+    simd_s = t_used * n / done
+    out["simd_1core"] = dict(us_per_call=simd_s * 1e6, rows_sampled=done, sample_s=round(t_used, 3))
     # (iii) the same dot over all host threads, full calls
     reps, t_used = 0, 0.0
-    while t_used < budget_s * 0.25 and reps < 200:
+    while t_used < budget_s * 0.25:
         t0 = time.perf_counter()
         used = orc.cpub_gemv_simd_threaded(a, x, k, 0, n, y, threads)
         t_used += time.perf_counter() - t0
@@ -147,9 +200,10 @@ def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
         "unit": "GB/s (algorithmic Q4_K call bytes / CPU time)",
         "cores": 1,
         "kind": "port",
-        "sample": (f"reference per-call path (blas.rs:199-210 gemm_f32 at M=1 over f32 W^T dequantized at load), "
-                   f"{out['literal_1core']['cols_sampled']} of {n} output columns timed, scaled to the full call; "
-                   f"{cpu_model}, {simd}"),
+        "sample": (f"reference per-call path (blas.rs:199-210 gemm_f32 at M=1 over f32 W^T dequantized at load, "
+                   f"not timed), {out['literal_1core']['cols_sampled']} output columns timed "
+                   f"({out['literal_1core']['cols_sampled'] / n:.1f} calls' worth) in "
+                   f"{out['literal_1core']['sample_s']} s; {cpu_model}, {simd}"),
         "us_per_call": round(out["literal_1core"]["us_per_call"], 1),
         "variants": {k_: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                      for k_, v in out.items()},
@@ -213,8 +267,12 @@ def main():
     ok = None
     try:
         from oracle import oracle as orc
-        ref = orc.matmul(w_type, w, n, k, at, xq.cpu().numpy(), m)
-        yy = y.cpu().numpy().reshape(m, n)
+        rows = np.linspace(0, m - 1, min(m, 16)).astype(int)   # a spread of rows keeps the oracle quick
+        rb = B.row_bytes(at, k)
+        xq_h = xq.cpu().numpy()
+        sub = np.concatenate([xq_h[r * rb:(r + 1) * rb] for r in rows])
+        ref = orc.matmul(w_type, w, n, k, at, sub, len(rows))
+        yy = y.cpu().numpy().reshape(m, n)[rows]
         ok = float(np.linalg.norm(yy - ref) / np.linalg.norm(ref))
     except Exception as e:
         log(f"parity check skipped: {e}")
@@ -243,6 +301,29 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "alg_bytes_per_launch": alg},
     }
+    if m >= 16:
+        # the batched path is bound by int8 MFMA: 2*M*N*K ops per launch
+        ops = 2.0 * m * n * k
+        tops = ops / (ms * 1e-3) / 1e12
+        result["metric"] = "Q4_K batched GEMM int8 TOP/s (% of dense int8 MFMA peak), 1 GPU"
+        result["value"] = round(tops, 2)
+        result["unit"] = "TOP/s"
+        result["roofline"] = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                              "unit": "TOP/s (int8)", "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                              "alg_ops_per_launch": ops, "alg_bytes_per_launch": alg,
+                              "hbm_gbs_alg": round(gbs, 2)}
+    if args.probe_copy:
+        src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy probe: 5 x 256 MiB device copies")
+    if not args.no_traffic:
+        log("measuring HBM traffic per launch (rocprofv3 --pmc child runs)")
+        traffic, detail = measure_traffic(args.config)
+        result["roofline"]["traffic"] = round(traffic) if traffic else None
+        result["roofline"]["traffic_detail"] = detail
     if not args.no_cpu:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(w_type, w, x[0], n, k, args.cpu_seconds, alg)
