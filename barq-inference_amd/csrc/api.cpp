@@ -335,7 +335,7 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     } else if (!aligned(x, aq == BARQ_TYPE_Q8_K ? 4 : 2)) {
         return fail(BARQ_E_INVALID, "activation blocks misaligned");
     }
-    if (m >= 16 && barq::gemm_mfma_supported(w_type, n_rows, k))
+    if (m >= 16 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
         return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, y, s), "gemm_mfma");
     const size_t xrb = row_bytes_of(aq, k);
     for (size_t r = 0; r < m; r++)

@@ -17,10 +17,11 @@
 //         crosses a byte).  C = ((s1*q).x << 3) + (s0*q).x.
 //   Q6_K: w' = s * (q - 32) in [-4064, 4096] is split as 128*h + l with
 //         l in [0, 127] and h in [-32, 32].  C = ((h.x) << 7) + l.x.
-// The Q4_K min term dmin * sum_j m_j * sum_{i in sub-block j} x_i uses the
-// activation's 32-element sums split the same way (s = 128*bh + bl) in a
-// v_mfma_i32_16x16x32_i8 pair.  The integer results are exact; the float
-// epilogue per super-block is y += dx * (d * C - dmin * Cmin).
+// The Q4_K min term dmin * sum_k m_j(k) * x_k is one more int8 pass over the
+// same activation fragments against the 6-bit mins broadcast over their
+// 32-element sub-blocks (MFMA time is cheaper here than the VALU a separate
+// bsum path would need).  The integer results are exact; the float epilogue
+// per super-block is y += dx * (d * C - dmin * Cmin).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -40,6 +41,23 @@ __device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t s) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// Raw buffer access: a 128-bit base/limit descriptor in SGPRs, a per-lane
+// 32-bit offset and a wave-uniform offset.  Reads at or beyond the limit
+// return zero, which pads ragged row tiles without per-row branches.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ brsrc make_brsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld16(brsrc r, uint32_t voff, uint32_t soff) {
+    const u32x4v v = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t bld4(brsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
 // ---------------------------------------------------------------------------
 // Weight formats.  decode() produces, for lane (column n = l%16, k-group
 // g = l/16) and MFMA step p (super-block elements 64p + 16g + [0, 16)), the
@@ -52,14 +70,14 @@ struct GQ4K {
     static constexpr bool HAS_MIN = true;
     static constexpr int SHIFT = 3;
 
-    // global block rows are 16-byte aligned (row bytes = 144 * k/256, base 16-aligned)
-    static __device__ __forceinline__ uint4 chunk(const uint8_t* blk, int c) {
-        return *reinterpret_cast<const uint4*>(blk + 16 * c);
+    // piece c of a block: 16-byte aligned (row bytes = 144 * k/256, base 16-aligned)
+    static __device__ __forceinline__ uint4 chunk(brsrc r, uint32_t off, uint32_t soff, int) {
+        return bld16(r, off, soff);
     }
 
     struct B {
         v4i h[4], l[4];
-        long mn;      // mins m_0..m_7 (lanes of k-group 0), else 0
+        int m[4];     // per step: the lane's sub-block min, broadcast to 4 bytes
         float d, dmin;
     };
 
@@ -84,8 +102,9 @@ struct GQ4K {
             const uint32_t n2 = (qs.z >> nsh) & 0x0F0F0F0Fu, n3 = (qs.w >> nsh) & 0x0F0F0F0Fu;
             b.h[p] = v4i{(int)mul_u16x2(n0, s1), (int)mul_u16x2(n1, s1), (int)mul_u16x2(n2, s1), (int)mul_u16x2(n3, s1)};
             b.l[p] = v4i{(int)mul_u16x2(n0, s0), (int)mul_u16x2(n1, s0), (int)mul_u16x2(n2, s0), (int)mul_u16x2(n3, s0)};
+            const uint32_t mj = ((p < 2 ? mA : mB) >> (8 * ((2 * p + hi) & 3))) & 0xFFu;
+            b.m[p] = (int)(mj * 0x01010101u);
         }
-        b.mn = g == 0 ? (long)(((uint64_t)mB << 32) | mA) : 0;
     }
 };
 
@@ -96,15 +115,23 @@ struct GQ6K {
     static constexpr bool HAS_MIN = false;
     static constexpr int SHIFT = 7;
 
-    // block rows are only 2-byte aligned
-    static __device__ __forceinline__ uint4 chunk(const uint8_t* blk, int c) {
-        if (c < 13) return ld16_a2(blk + 16 * c);
-        return make_uint4(ld_u16(blk + 208), 0u, 0u, 0u);
+    // blocks are only 2-byte aligned: read the dword-aligned 20-byte window
+    // and funnel-shift (pieces 0-12); piece 13 is the f16 d
+    static __device__ __forceinline__ uint4 chunk(brsrc r, uint32_t off, uint32_t soff, int c) {
+        const uint32_t o = off + soff, sh = o & 3u, a = o - sh;
+        if (c == 13) {
+            const uint32_t v = bld4(r, a, 0);
+            return make_uint4(sh ? v >> 16 : v & 0xFFFFu, 0u, 0u, 0u);
+        }
+        const uint4 v = bld16(r, a, 0);
+        const uint32_t e = bld4(r, a + 16u, 0);
+        return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+                          __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh));
     }
 
     struct B {
         v4i h[4], l[4];
-        long mn;
+        int m[4];
         float d, dmin;
     };
 
@@ -123,7 +150,6 @@ struct GQ6K {
     static __device__ __forceinline__ void decode(const uint8_t* wr, int g, B& b) {
         b.d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(wr + 208));
         b.dmin = 0.0f;
-        b.mn = 0;
         const int g1 = g & 1;
         #pragma unroll
         for (int p = 0; p < 4; p++) {
@@ -150,15 +176,148 @@ struct GQ6K {
 };
 
 // ---------------------------------------------------------------------------
+// One LDS stage holds super-block b of the tile: the int8 activation rows,
+// their block scales, their split 32-element sums and the packed weight
+// blocks.  Two stages alternate: while the waves run the MFMAs of stage b,
+// the global loads of stage b+1 are in flight into registers; they are
+// stored to the other stage afterwards, so one barrier per super-block
+// separates the producers and consumers.
 template <class F, int BM>
-__global__ __launch_bounds__(256, 2)
+struct Stage {
+    uint8_t xq[BM * XQ_STRIDE];
+    float xd[BM];
+    uint8_t w[GM_BN * F::STRIDE];
+};
+
+template <class F, int BM>
+struct StageRegs {
+    static constexpr int XQ_PER_T = BM / 16;                         // 16-byte activation pieces per thread
+    static constexpr int W_PER_T = (GM_BN * F::CHUNKS + 255) / 256;  // 16-byte weight pieces per thread
+    uint4 xq[XQ_PER_T];
+    uint4 w[W_PER_T];
+    float dx;         // block scale of the thread's row (threads < BM)
+};
+
+// Per-thread constant offsets of the stage loads (computed once per kernel).
+template <class F, int BM>
+struct StageAddr {
+    uint32_t xq;                                  // activation piece (row t/16, 16 bytes at 16*(t%16))
+    uint32_t xm;                                  // row t's block scale
+    uint32_t w[StageRegs<F, BM>::W_PER_T];        // weight piece t + 256 i
+};
+
+template <class F, int BM>
+__device__ __forceinline__ void stage_addr(StageAddr<F, BM>& a, size_t w_row_bytes, size_t x_row_bytes, int t) {
+    a.xq = (uint32_t)(t >> 4) * (uint32_t)x_row_bytes + 4u + 16u * (uint32_t)(t & 15);
+    a.xm = (uint32_t)t * (uint32_t)x_row_bytes;
+    #pragma unroll
+    for (int i = 0; i < StageRegs<F, BM>::W_PER_T; i++) {
+        const int c = t + 256 * i, rr = c / F::CHUNKS, piece = c - rr * F::CHUNKS;
+        a.w[i] = (uint32_t)rr * (uint32_t)w_row_bytes + 16u * (uint32_t)piece;
+    }
+}
+
+// xr covers activation rows [m0, M) and wr weight rows [n0, N) of the tile;
+// rows past the end read as zero.
+template <class F, int BM>
+__device__ __forceinline__ void stage_load(StageRegs<F, BM>& r, const StageAddr<F, BM>& a, brsrc wr, brsrc xr,
+                                           uint32_t x_row_bytes, int b, int t) {
+    const uint32_t xs = (uint32_t)b * Q8_K_BYTES;
+    #pragma unroll
+    for (int i = 0; i < StageRegs<F, BM>::XQ_PER_T; i++) r.xq[i] = bld16(xr, a.xq, xs + 16u * (uint32_t)i * x_row_bytes);
+    if (t < BM) r.dx = __builtin_bit_cast(float, bld4(xr, a.xm, xs));
+    const uint32_t ws = (uint32_t)b * F::BB;
+    #pragma unroll
+    for (int i = 0; i < StageRegs<F, BM>::W_PER_T; i++) {
+        const int c = t + 256 * i;
+        if (c < GM_BN * F::CHUNKS) r.w[i] = F::chunk(wr, a.w[i], ws, c % F::CHUNKS);
+    }
+}
+
+template <class F, int BM>
+__device__ __forceinline__ void stage_store(Stage<F, BM>& st, const StageRegs<F, BM>& r, int t) {
+    #pragma unroll
+    for (int i = 0; i < StageRegs<F, BM>::XQ_PER_T; i++)
+        *reinterpret_cast<uint4*>(st.xq + ((t >> 4) + 16 * i) * XQ_STRIDE + 16 * (t & 15)) = r.xq[i];
+    if (t < BM) st.xd[t] = r.dx;
+    #pragma unroll
+    for (int i = 0; i < StageRegs<F, BM>::W_PER_T; i++) {
+        const int c = t + 256 * i;
+        if (c < GM_BN * F::CHUNKS) {
+            const int rr = c / F::CHUNKS, piece = c - rr * F::CHUNKS;
+            *reinterpret_cast<uint4*>(st.w + rr * F::STRIDE + 16 * piece) = r.w[i];
+        }
+    }
+}
+
+// All BM/16 activation tiles' fragments are read first; the MFMAs then run
+// step-major across tiles, so consecutive MFMAs are independent and the
+// accumulation chains of different tiles hide each other's latency.
+template <class F, int BM>
+__device__ __forceinline__ void stage_compute(const Stage<F, BM>& st, float (&acc)[BM / 16][4], int wave, int g,
+                                              int li) {
+    constexpr int MT = BM / 16;
+    typename F::B bw;
+    F::decode(st.w + (16 * wave + li) * F::STRIDE, g, bw);
+    v4i a[MT][4];
+    #pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const uint8_t* xr = st.xq + (16 * i + li) * XQ_STRIDE + 16 * g;
+        #pragma unroll
+        for (int p = 0; p < 4; p++) a[i][p] = *reinterpret_cast<const v4i*>(xr + 64 * p);
+    }
+    v4i c[MT];
+    #pragma unroll
+    for (int i = 0; i < MT; i++) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][0], bw.h[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+    #pragma unroll
+    for (int p = 1; p < 4; p++) {
+        #pragma unroll
+        for (int i = 0; i < MT; i++) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][p], bw.h[p], c[i], 0, 0, 0);
+    }
+    #pragma unroll
+    for (int i = 0; i < MT; i++) c[i] = c[i] << F::SHIFT;
+    #pragma unroll
+    for (int p = 0; p < 4; p++) {
+        #pragma unroll
+        for (int i = 0; i < MT; i++) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][p], bw.l[p], c[i], 0, 0, 0);
+    }
+    if (F::HAS_MIN) {
+        v4i cm[MT];
+        #pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const v4i bm = {bw.m[p], bw.m[p], bw.m[p], bw.m[p]};
+            #pragma unroll
+            for (int i = 0; i < MT; i++)
+                cm[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][p], bm, p ? cm[i] : v4i{0, 0, 0, 0}, 0, 0, 0);
+        }
+        #pragma unroll
+        for (int i = 0; i < MT; i++) {
+            const float4 dx = *reinterpret_cast<const float4*>(st.xd + 16 * i + 4 * g);
+            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+            #pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = __builtin_fmaf(-bw.dmin, (float)cm[i][r], bw.d * (float)c[i][r]);
+                acc[i][r] = __builtin_fmaf(dxv[r], v, acc[i][r]);
+            }
+        }
+    } else {
+        #pragma unroll
+        for (int i = 0; i < MT; i++) {
+            const float4 dx = *reinterpret_cast<const float4*>(st.xd + 16 * i + 4 * g);
+            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+            #pragma unroll
+            for (int r = 0; r < 4; r++) acc[i][r] = __builtin_fmaf(dxv[r], bw.d * (float)c[i][r], acc[i][r]);
+        }
+    }
+}
+
+template <class F, int BM>
+__global__ __launch_bounds__(256, 1)
 void gemm_kq_kernel(const uint8_t* __restrict__ W, size_t w_row_bytes, const uint8_t* __restrict__ X,
                     size_t x_row_bytes, float* __restrict__ Y, int M, int N, int nsb, int tiles_m, int n_tiles) {
     constexpr int MT = BM / 16;
-    __shared__ __align__(16) uint8_t s_xq[BM * XQ_STRIDE];
-    __shared__ __align__(16) uint8_t s_xmin[BM * 16];
-    __shared__ __align__(16) float s_xd[BM];
-    __shared__ __align__(16) uint8_t s_w[GM_BN * F::STRIDE];
+    extern __shared__ __align__(16) uint8_t smem[];
+    Stage<F, BM>* st = reinterpret_cast<Stage<F, BM>*>(smem);
 
     // XCD-aware order: workgroup i runs on XCD i % 8; give each XCD a
     // contiguous run of tiles so the activation rows of a weight tile's
@@ -174,83 +333,33 @@ void gemm_kq_kernel(const uint8_t* __restrict__ W, size_t w_row_bytes, const uin
     #pragma unroll
     for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = acc[i][2] = acc[i][3] = 0.0f;
 
-    for (int b = 0; b < nsb; b++) {
-        if (b) __syncthreads();
-        // ---- stage super-block b: activation rows ----
-        #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            const int r = (t >> 4) + 16 * i, row = m0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row < M) v = ld16_a4(X + (size_t)row * x_row_bytes + (size_t)b * Q8_K_BYTES + 4 + 16 * (t & 15));
-            *reinterpret_cast<uint4*>(s_xq + r * XQ_STRIDE + 16 * (t & 15)) = v;
-        }
-        for (int r = t; r < BM; r += 256) {
-            const int row = m0 + r;
-            float dx = 0.0f;
-            uint4 mm = make_uint4(0, 0, 0, 0);
-            if (row < M) {
-                const uint8_t* blk = X + (size_t)row * x_row_bytes + (size_t)b * Q8_K_BYTES;
-                dx = *reinterpret_cast<const float*>(blk);
-                if (F::HAS_MIN) {
-                    const uint4 s0 = ld16_a4(blk + 260), s1 = ld16_a4(blk + 276);
-                    const uint32_t w[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-                    uint32_t bh[2] = {0, 0}, bl[2] = {0, 0};
-                    #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const int s = __builtin_amdgcn_sbfe((int)w[j], 0, 16) + __builtin_amdgcn_sbfe((int)w[j], 16, 16);
-                        bh[j >> 2] |= ((uint32_t)(s >> 7) & 0xFFu) << (8 * (j & 3));
-                        bl[j >> 2] |= ((uint32_t)s & 0x7Fu) << (8 * (j & 3));
-                    }
-                    mm = make_uint4(bh[0], bh[1], bl[0], bl[1]);
-                }
-            }
-            s_xd[r] = dx;
-            *reinterpret_cast<uint4*>(s_xmin + 16 * r) = mm;
-        }
-        // ---- weight rows ----
-        for (int c = t; c < GM_BN * F::CHUNKS; c += 256) {
-            const int r = c / F::CHUNKS, piece = c - r * F::CHUNKS, row = n0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row < N) v = F::chunk(W + (size_t)row * w_row_bytes + (size_t)b * F::BB, piece);
-            *reinterpret_cast<uint4*>(s_w + r * F::STRIDE + 16 * piece) = v;
-        }
-        __syncthreads();
+    // the tile's rows as buffers (the launcher keeps both limits below 2^32)
+    const brsrc xr = make_brsrc(X + (size_t)m0 * x_row_bytes, (uint32_t)((size_t)(M - m0) * x_row_bytes));
+    const brsrc wr = make_brsrc(W + (size_t)n0 * w_row_bytes, (uint32_t)((size_t)(N - n0) * w_row_bytes));
+    StageAddr<F, BM> addr;
+    stage_addr<F, BM>(addr, w_row_bytes, x_row_bytes, t);
+    const uint32_t xrb = (uint32_t)x_row_bytes;
 
-        // ---- compute ----
-        typename F::B bw;
-        F::decode(s_w + (16 * wave + li) * F::STRIDE, g, bw);
-        #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            const uint8_t* xr = s_xq + (16 * i + li) * XQ_STRIDE + 16 * g;
-            v4i a[4];
-            #pragma unroll
-            for (int p = 0; p < 4; p++) a[p] = *reinterpret_cast<const v4i*>(xr + 64 * p);
-            v4i c = {0, 0, 0, 0};
-            #pragma unroll
-            for (int p = 0; p < 4; p++) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[p], bw.h[p], c, 0, 0, 0);
-            c = c << F::SHIFT;
-            #pragma unroll
-            for (int p = 0; p < 4; p++) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[p], bw.l[p], c, 0, 0, 0);
-            const float4 dx = *reinterpret_cast<const float4*>(s_xd + 16 * i + 4 * g);
-            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
-            if (F::HAS_MIN) {
-                const uint4 mm = *reinterpret_cast<const uint4*>(s_xmin + 16 * (16 * i + li));
-                const long ah = (long)(((uint64_t)mm.y << 32) | mm.x);
-                const long al = (long)(((uint64_t)mm.w << 32) | mm.z);
-                v4i cm = {0, 0, 0, 0};
-                cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bw.mn, cm, 0, 0, 0);
-                cm = cm << 7;
-                cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bw.mn, cm, 0, 0, 0);
-                #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float v = __builtin_fmaf(-bw.dmin, (float)cm[r], bw.d * (float)c[r]);
-                    acc[i][r] = __builtin_fmaf(dxv[r], v, acc[i][r]);
-                }
-            } else {
-                #pragma unroll
-                for (int r = 0; r < 4; r++) acc[i][r] = __builtin_fmaf(dxv[r], bw.d * (float)c[r], acc[i][r]);
-            }
-        }
+    // Super-block b+2's loads are issued while b is computed and b+1 waits
+    // in the other register set, so each load has two iterations to land.
+    StageRegs<F, BM> ra, rb;
+    ra.dx = rb.dx = 0.0f;
+    stage_load<F, BM>(ra, addr, wr, xr, xrb, 0, t);
+    if (nsb > 1) stage_load<F, BM>(rb, addr, wr, xr, xrb, 1, t);
+    stage_store<F, BM>(st[0], ra, t);
+    __syncthreads();
+    for (int b = 0; b < nsb; b += 2) {
+        // even b: compute st[0]; rb holds b+1; reload ra with b+2
+        if (b + 2 < nsb) stage_load<F, BM>(ra, addr, wr, xr, xrb, b + 2, t);
+        stage_compute<F, BM>(st[0], acc, wave, g, li);
+        if (b + 1 < nsb) stage_store<F, BM>(st[1], rb, t);
+        __syncthreads();
+        if (b + 1 >= nsb) break;
+        // odd b+1: compute st[1]; ra holds b+2; reload rb with b+3
+        if (b + 3 < nsb) stage_load<F, BM>(rb, addr, wr, xr, xrb, b + 3, t);
+        stage_compute<F, BM>(st[1], acc, wave, g, li);
+        if (b + 2 < nsb) stage_store<F, BM>(st[0], ra, t);
+        __syncthreads();
     }
 
     // C layout of the 16x16 MFMA: lane (li, g) holds rows 4g + r of column li
@@ -267,6 +376,267 @@ void gemm_kq_kernel(const uint8_t* __restrict__ W, size_t w_row_bytes, const uin
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K x Q8_K, v_mfma_i32_32x32x32_i8 (K = 32 = one Q4_K sub-block per MFMA).
+//
+// Workgroup tile BM activation rows x 128 weight rows; wave w owns weight
+// rows [32w, 32w+32) and all BM activation rows (BM/32 MFMA tiles), so every
+// weight sub-block is unpacked exactly once per workgroup.  NS LDS stages are
+// filled by buffer->LDS direct loads (no VGPR staging), NS-1 super-blocks
+// ahead of the MFMAs, with one barrier per super-block; rows past M or N read
+// as zero from the range-checked buffers.  The activation tile is stored with
+// its 16-byte chunks XOR-swizzled by row (chunk c of row r at c ^ (r & 15))
+// so the fragment reads of 32 rows hit distinct banks.
+//
+// Per sub-block j and tile: Ch += x.(s1*q), Cl += x.(s0*q), Cm += x.m_j (three
+// independent accumulation chains); per super-block C = 8*Ch + Cl and
+// y += dx * (d*C - dmin*Cm).
+// ---------------------------------------------------------------------------
+typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int G3_BN = 128;
+
+// Buffer -> LDS direct loads (lane i's bytes land at the wave's LDS base + i * size).
+// Issued as inline asm so the compiler's wait-count insertion does not treat
+// every in-flight stage as a pending write to the stage being read (it drains
+// all of them otherwise); the kernel waits on its own loads with wait_vmcnt
+// before each barrier.  The descriptor is passed as four SGPRs.
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+#ifdef BARQ_DMA_BUILTIN
+typedef brsrc dma_rsrc;
+__device__ __forceinline__ dma_rsrc make_dma_rsrc(const void* base, uint32_t bytes) { return make_brsrc(base, bytes); }
+__device__ __forceinline__ void lds_load16(dma_rsrc r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(dma_rsrc r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 4, voff, soff, 0, 0);
+}
+#else
+typedef i32x4v dma_rsrc;
+__device__ __forceinline__ i32x4v make_rsrc4(const void* base, uint32_t bytes);
+__device__ __forceinline__ dma_rsrc make_dma_rsrc(const void* base, uint32_t bytes) { return make_rsrc4(base, bytes); }
+__device__ __forceinline__ void lds_load16(i32x4v r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(i32x4v r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+#endif
+__device__ __forceinline__ i32x4v make_rsrc4(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return i32x4v{(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xFFFF, (int)bytes, 0x00020000};
+}
+
+template <int BM, int NW = 4>
+struct G3 {
+    static constexpr int XQ = 0;                              // BM rows x 272 B: 256 int8 + a 16-byte pad chunk
+    static constexpr int W = (BM * 17 + 63) / 64 * 1024;      // 128 x 144 packed Q4_K blocks (after the padded activation rows)
+    static constexpr int XD = W + G3_BN * Q4_K_BYTES;         // BM f32 block scales (room for one 64-lane load)
+    static constexpr int XD_LOADS = BM < 64 ? 1 : BM / 64;
+    static constexpr int STAGE = XD + XD_LOADS * 256;
+    static constexpr int X_CHUNKS = BM * 17;                  // activation tile in 16-byte chunks, pads included
+    static constexpr int X_INSTR_ALL = (X_CHUNKS + 63) / 64;  // 64-chunk load instructions for the whole tile
+    static constexpr int X_INSTR = (X_INSTR_ALL + NW - 1) / NW;   // per wave (the last one may be partial or absent)
+    static constexpr int W_INSTR_ALL = G3_BN * 9 / 64;        // 18 for the weight tile
+    static constexpr int LOADS_MIN = X_INSTR_ALL / NW + W_INSTR_ALL / NW;   // load instructions every wave issues per stage (at least)
+    static constexpr int W_INSTR = (W_INSTR_ALL + NW - 1) / NW;
+    static constexpr int MTW = BM / 32 / (NW / 4);             // 32x32 MFMA tiles per wave
+};
+
+// Per-thread offsets of the stage loads (independent of the super-block).
+template <int BM, int NW>
+struct G3Off {
+    uint32_t x[G3<BM, NW>::X_INSTR];
+    uint32_t w[G3<BM, NW>::W_INSTR];
+    uint32_t xd;
+};
+
+template <int BM, int NW>
+__device__ __forceinline__ void g3_offsets(G3Off<BM, NW>& o, uint32_t xrb, uint32_t wrb, int wave, int l) {
+    using L = G3<BM, NW>;
+    #pragma unroll
+    for (int q = 0; q < L::X_INSTR; q++) {
+        const int p = (q * NW + wave) * 64 + l, r = p / 17, c = p - r * 17;
+        // the pad chunk (c == 16) and chunks past the tile reload a valid chunk of the row
+        o.x[q] = (uint32_t)r * xrb + 4u + 16u * (uint32_t)(c < 16 ? c : 0);
+    }
+    #pragma unroll
+    for (int q = 0; q < L::W_INSTR; q++) {
+        const int p = (q * NW + wave) * 64 + l, row = p / 9, piece = p - row * 9;
+        o.w[q] = (uint32_t)row * wrb + 16u * (uint32_t)piece;
+    }
+    o.xd = (uint32_t)(64 * wave + l) * xrb;
+}
+
+template <int BM, int NW>
+__device__ __forceinline__ void g3_issue(uint8_t* stage, dma_rsrc xr, dma_rsrc wr, const G3Off<BM, NW>& o, int b, int wave) {
+    using L = G3<BM, NW>;
+    const uint32_t xs = (uint32_t)b * Q8_K_BYTES, ws = (uint32_t)b * Q4_K_BYTES;
+    #pragma unroll
+    for (int q = 0; q < L::X_INSTR; q++) {
+        const int idx = q * NW + wave;
+        if (idx < L::X_INSTR_ALL) lds_load16(xr, stage + L::XQ + 1024 * idx, o.x[q], xs);
+    }
+    #pragma unroll
+    for (int q = 0; q < L::W_INSTR; q++) {
+        const int idx = q * NW + wave;
+        if (idx < L::W_INSTR_ALL) lds_load16(wr, stage + L::W + 1024 * idx, o.w[q], ws);
+    }
+    if (wave < L::XD_LOADS) lds_load4(xr, stage + L::XD + 256 * wave, o.xd, xs);
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BM, int NW>
+__device__ __forceinline__ void g3_compute(const uint8_t* stage, float (&acc)[G3<BM, NW>::MTW][16], int wave, int l) {
+    using L = G3<BM, NW>;
+    constexpr int MT = L::MTW;
+    const int n = l & 31, g2 = l >> 5;
+    const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // 8 waves: two per 32-column slice, one per half of the rows
+    const uint8_t* wrow = stage + L::W + (32 * slice + n) * Q4_K_BYTES;
+    const uint4 hdr = *reinterpret_cast<const uint4*>(wrow);
+    const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
+    // get_scale_min_k4 (gguf.rs:825-837) for the eight sub-blocks, bytewise
+    const uint32_t scA = hdr.y & 0x3F3F3F3Fu;
+    const uint32_t scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    const uint32_t mA = hdr.z & 0x3F3F3F3Fu;
+    const uint32_t mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    // s = 8*s1 + s0 for four sub-blocks at a time
+    const uint32_t s1A = (scA >> 3) & 0x07070707u, s0A = scA & 0x07070707u;
+    const uint32_t s1B = (scB >> 3) & 0x07070707u, s0B = scB & 0x07070707u;
+    // this lane's activation row (tile 0) and k-group: chunk 2j + g2 of a 272-byte row
+    const uint8_t* xrow = stage + L::XQ + (mbase + n) * 272 + 16 * g2;
+    v16i ch[MT], cl[MT], cm[MT];
+    #pragma unroll
+    for (int pr = 0; pr < 4; pr++) {
+        // sub-blocks 2pr (low nibbles) and 2pr+1 (high nibbles) share qs[32pr + 16g2 .. +16)
+        const uint4 qs = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * pr + 16 * g2);
+        #pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int j = 2 * pr + h;
+            // byte j&3 of the packed scales / mins, broadcast with one v_perm each
+            const uint32_t bsel = (uint32_t)(j & 3);
+            const uint32_t s1 = __builtin_amdgcn_perm(0u, j < 4 ? s1A : s1B, 0x0c000c00u | (bsel << 16) | bsel);
+            const uint32_t s0 = __builtin_amdgcn_perm(0u, j < 4 ? s0A : s0B, 0x0c000c00u | (bsel << 16) | bsel);
+            const int mb = (int)__builtin_amdgcn_perm(0u, j < 4 ? mA : mB, bsel * 0x01010101u);
+            const uint32_t n0 = (qs.x >> (4 * h)) & 0x0F0F0F0Fu, n1 = (qs.y >> (4 * h)) & 0x0F0F0F0Fu;
+            const uint32_t n2 = (qs.z >> (4 * h)) & 0x0F0F0F0Fu, n3 = (qs.w >> (4 * h)) & 0x0F0F0F0Fu;
+            const v4i bh = {(int)mul_u16x2(n0, s1), (int)mul_u16x2(n1, s1), (int)mul_u16x2(n2, s1), (int)mul_u16x2(n3, s1)};
+            const v4i bl = {(int)mul_u16x2(n0, s0), (int)mul_u16x2(n1, s0), (int)mul_u16x2(n2, s0), (int)mul_u16x2(n3, s0)};
+            const v4i bm = {mb, mb, mb, mb};
+            #pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * 272 + 32 * j);
+                const v16i z = {};
+                ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
+                cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
+                cm[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bm, j ? cm[t] : z, 0, 0, 0);
+            }
+        }
+    }
+    // C layout of the 32x32 MFMA: lane (n, g2), register r -> row 8*(r/4) + 4*g2 + r%4, column n
+    #pragma unroll
+    for (int t = 0; t < MT; t++) {
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 dx = *reinterpret_cast<const float4*>(stage + L::XD + 4 * (mbase + 32 * t + 8 * q + 4 * g2));
+            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = 4 * q + i;
+                const int c = (ch[t][r] << 3) + cl[t][r];
+                const float v = __builtin_fmaf(-dmin, (float)cm[t][r], d * (float)c);
+                acc[t][r] = __builtin_fmaf(dxv[i], v, acc[t][r]);
+            }
+        }
+    }
+}
+
+// One pipeline step: super-block b computed from stage S (= b % NS) while the
+// loads of b+NS-1 go to stage (S-1) % NS.  Each stage is its own LDS array,
+// so the compiler's wait counting separates the in-flight stages; the raw
+// s_barrier (no memory fence) does not drain them.
+template <int BM, int NW, int NS, int S>
+__device__ __forceinline__ void g3_step(uint8_t* const (&stages)[4], int b, int nsb, dma_rsrc xr, dma_rsrc wr,
+                                        const G3Off<BM, NW>& off, int wave, int l, float (&acc)[G3<BM, NW>::MTW][16]) {
+    using L = G3<BM, NW>;
+    if (b >= nsb) return;
+    // this thread's loads of super-block b are done once at most the later
+    // stages' loads are still outstanding; then every thread's are after the barrier
+    if (b + NS - 2 < nsb) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (b + NS - 1 < nsb) g3_issue<BM, NW>(stages[(S + NS - 1) % NS], xr, wr, off, b + NS - 1, wave);
+    g3_compute<BM, NW>(stages[S], acc, wave, l);
+}
+
+template <int BM, int NS, int NW>
+__global__ __launch_bounds__(64 * NW, (BM <= 32 ? 2 : 1))
+void gemm_q4k_v3_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb,
+                        float* __restrict__ Y, int M, int N, int nsb, int tiles_m, int n_tiles, int xcd_order) {
+    using L = G3<BM, NW>;
+    constexpr int MT = L::MTW;
+    static_assert(NS == 3 || NS == 4, "stage count");
+    __shared__ __align__(16) uint8_t st0[L::STAGE];
+    __shared__ __align__(16) uint8_t st1[L::STAGE];
+    __shared__ __align__(16) uint8_t st2[L::STAGE];
+    __shared__ __align__(16) uint8_t st3[NS == 4 ? L::STAGE : 16];
+    uint8_t* const stages[4] = {st0, st1, st2, st3};   // with NS == 3 the fourth is never used
+
+    int tile = blockIdx.x;
+    if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
+    const int mt = tile % tiles_m, ntile = tile / tiles_m;
+    const int m0 = mt * BM, n0 = ntile * G3_BN;
+    const int l = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    const dma_rsrc xr = make_dma_rsrc(X + (size_t)m0 * xrb, (uint32_t)((size_t)(M - m0) * xrb));
+    const dma_rsrc wr = make_dma_rsrc(W + (size_t)n0 * wrb, (uint32_t)((size_t)(N - n0) * wrb));
+
+    float acc[MT][16];
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+
+    G3Off<BM, NW> off;
+    g3_offsets<BM, NW>(off, xrb, wrb, wave, l);
+    #pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nsb) g3_issue<BM, NW>(stages[s], xr, wr, off, s, wave);
+    for (int b = 0; b < nsb; b += NS) {
+        g3_step<BM, NW, NS, 0>(stages, b, nsb, xr, wr, off, wave, l, acc);
+        g3_step<BM, NW, NS, 1>(stages, b + 1, nsb, xr, wr, off, wave, l, acc);
+        g3_step<BM, NW, NS, 2>(stages, b + 2, nsb, xr, wr, off, wave, l, acc);
+        if constexpr (NS == 4) g3_step<BM, NW, NS, 3>(stages, b + 3, nsb, xr, wr, off, wave, l, acc);
+    }
+
+    const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
+    if (col < N) {
+        #pragma unroll
+        for (int t = 0; t < MT; t++)
+            #pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + mb + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                if (row < M) Y[(size_t)row * N + col] = acc[t][r];
+            }
+    }
+}
+
 // ---- launch ---------------------------------------------------------------
 static int read_env_bm() {
     if (const char* e = getenv("BARQ_GEMM_BM")) return atoi(e);
@@ -279,7 +649,15 @@ static hipError_t launch_kq(const uint8_t* W, size_t wrb, const uint8_t* X, size
                             int nsb, hipStream_t s) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + GM_BN - 1) / GM_BN;
     const int n_tiles = tiles_m * tiles_n;
-    hipLaunchKernelGGL((gemm_kq_kernel<F, BM>), dim3(n_tiles), dim3(256), 0, s, W, wrb, X, xrb, Y, M, N, nsb,
+    constexpr size_t lds = 2 * sizeof(Stage<F, BM>);
+    static bool attr_set = false;   // per template instance; the attribute is per device function
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kq_kernel<F, BM>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((gemm_kq_kernel<F, BM>), dim3(n_tiles), dim3(256), lds, s, W, wrb, X, xrb, Y, M, N, nsb,
                        tiles_m, n_tiles);
     return hipGetLastError();
 }
@@ -292,6 +670,46 @@ static int pick_bm(int M, int N) {
     int bm = 128;
     while (bm > 16 && (bm >= 2 * ((M + 15) / 16 * 16) || (long)tiles_n * ((M + bm - 1) / bm) < 512)) bm >>= 1;
     return bm;
+}
+
+static int read_env_v3() {
+    if (const char* e = getenv("BARQ_GEMM_V3")) return atoi(e);
+    return 1;
+}
+static int g_use_v3 = read_env_v3();
+// BARQ_GEMM_XCD=0 turns off the XCD-aware tile order (tuning experiments)
+static int read_env_xcd() {
+    if (const char* e = getenv("BARQ_GEMM_XCD")) return atoi(e);
+    return 1;
+}
+static int g_xcd_order = read_env_xcd();
+
+template <int BM, int NS, int NW = 4>
+static hipError_t launch_q4k_v3(const uint8_t* W, uint32_t wrb, const uint8_t* X, uint32_t xrb, float* Y, int M,
+                                int N, int nsb, hipStream_t s) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + G3_BN - 1) / G3_BN;
+    const int n_tiles = tiles_m * tiles_n;
+    hipLaunchKernelGGL((gemm_q4k_v3_kernel<BM, NS, NW>), dim3(n_tiles), dim3(64 * NW), 0, s, W, wrb, X, xrb, Y, M, N, nsb,
+                       tiles_m, n_tiles, g_xcd_order);
+    return hipGetLastError();
+}
+
+static hipError_t dispatch_q4k_v3(const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
+                                  hipStream_t s) {
+    const int nsb = (int)(k / 256);
+    const uint32_t wrb = (uint32_t)(nsb * Q4_K_BYTES), xrb = (uint32_t)(nsb * Q8_K_BYTES);
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+    const int M = (int)m, N = (int)n_rows;
+    const int tiles_n = (N + G3_BN - 1) / G3_BN;
+    // Tile choice (measured on MI355X): 64x128 workgroup tiles with eight
+    // waves (two per SIMD, each a 32x32 MFMA tile) for M > 32; 32-row tiles
+    // with four waves for the small expert groups of a MoE step.
+    const int bm = g_bm_override ? g_bm_override : (M > 32 ? 65 : 32);
+    (void)tiles_n;
+    if (bm == 65) return launch_q4k_v3<64, 4, 8>(w, wrb, x, xrb, y, M, N, nsb, s);
+    if (bm == 64) return launch_q4k_v3<64, 4>(w, wrb, x, xrb, y, M, N, nsb, s);
+    return launch_q4k_v3<32, 3>(w, wrb, x, xrb, y, M, N, nsb, s);
 }
 
 template <class F>
@@ -310,16 +728,21 @@ static hipError_t dispatch_kq(const void* W, size_t n_rows, size_t k, const void
     }
 }
 
-bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k) {
-    return (w_type == TYPE_Q4_K || w_type == TYPE_Q6_K) && k % 256 == 0 && n_rows > 0 &&
-           n_rows <= (size_t)INT32_MAX;
+// The tile loads are raw buffer loads with 32-bit offsets: the weight matrix
+// and the activation rows must each be below 2 GiB.
+bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m) {
+    if ((w_type != TYPE_Q4_K && w_type != TYPE_Q6_K) || k % 256 != 0 || n_rows == 0) return false;
+    const size_t wbytes = n_rows * (k / 256) * (w_type == TYPE_Q4_K ? Q4_K_BYTES : Q6_K_BYTES);
+    const size_t xbytes = m * (k / 256) * Q8_K_BYTES;
+    return wbytes < (1ull << 31) && xbytes < (1ull << 31);
 }
 
 hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,
                                 float* y, hipStream_t s) {
     if (m == 0 || n_rows == 0) return hipSuccess;
+    if (!gemm_mfma_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
     switch (w_type) {
-    case TYPE_Q4_K: return dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
+    case TYPE_Q4_K: return g_use_v3 ? dispatch_q4k_v3(W, n_rows, k, xq, m, y, s) : dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
     case TYPE_Q6_K: return dispatch_kq<GQ6K>(W, n_rows, k, xq, m, y, s);
     default: return hipErrorInvalidValue;
     }

@@ -18,6 +18,25 @@
 
 namespace barq {
 
+// Workgroup -> rows.  Workgroup i runs on XCD i % 8.  A workgroup covers
+// RW = R * WAVES rows; LW = 32 / RW workgroups fill one 128-byte line of y.
+// Workgroups on one XCD take whole lines of y and consecutive lines go to
+// consecutive XCDs, so each output line is written from one L2 (no partial
+// lines written back from several XCDs) while the weight reads still
+// interleave across all XCDs at a 32-row granularity.
+template <int RW>
+__device__ __forceinline__ int wg_rows_remap(int id, int G) {
+    if constexpr (RW >= 32 || (32 % RW) != 0) {
+        return id;
+    } else {
+        constexpr int LW = 32 / RW;
+        const int full = G / (8 * LW) * (8 * LW);
+        if (id >= full) return id;
+        const int x = id & 7, j = id >> 3;
+        return ((j / LW) * 8 + x) * LW + (j % LW);
+    }
+}
+
 // Integer path.  Per wave: the lane's activation slice is loaded first (it is
 // shared by all rows), then the weight slices of all R rows are issued before
 // any arithmetic (the scheduling barrier keeps the compiler from sinking them
@@ -28,7 +47,7 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
                     float* __restrict__ y, int n_rows, int k) {
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * WAVES + wave) * R;
+    const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
     if (row0 >= n_rows) return;
     const typename F::Lane c = F::lane(l);
     const int nblk = k / F::ROW_BLOCK_ELEMS;

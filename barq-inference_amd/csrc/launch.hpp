@@ -28,7 +28,7 @@ void gemv_set_config(int rows_per_wave, int waves);
 // gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows)
 hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k,
                                 const void* xq, size_t m, float* y, hipStream_t s);
-bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k);
+bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m);
 
 // f32blas.hip
 hipError_t gemm_f32_launch(const float* a, const float* b, size_t m, size_t k, size_t n, float* c,
