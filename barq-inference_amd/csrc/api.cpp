@@ -556,8 +556,9 @@ MoeArena moe_arena(size_t base, size_t ne, size_t hidden, size_t n_ff, size_t na
     m.wts = a.add(na * 4);
     m.pos = a.add(na * 4);
     m.xg = a.add(na * hidden * 4);
-    m.g = a.add(na * n_ff * 4);
-    m.u = a.add(na * n_ff * 4);
+    // gate and up results are adjacent (one grouped launch writes both)
+    m.g = a.add(2 * na * n_ff * 4);
+    m.u = m.g + na * n_ff * 4;
     m.yg = a.add(na * hidden * 4);
     const size_t qrow = (hidden > n_ff ? hidden : n_ff) / 256 * 292;
     m.q = a.add(q8 ? na * qrow : 0);
@@ -588,6 +589,37 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
     uint8_t* qb = at<uint8_t>(h, o_q);
 
     BARQ_CHECK(launched(barq::moe_group_launch(ids, weights, rows, k, ne, offsets, tokens, wts, rowpos, s), "moe_group"));
+    if (q8 && q8_partner(gt) == BARQ_TYPE_Q8_K && q8_partner(ut) == BARQ_TYPE_Q8_K && q8_partner(dt) == BARQ_TYPE_Q8_K &&
+        barq::kq_supported(gt, n_ff, hidden, na) && barq::kq_supported(ut, n_ff, hidden, na) &&
+        barq::kq_supported(dt, hidden, n_ff, na)) {
+        // Device-only schedule: every kernel reads the expert row ranges from
+        // `offsets`, so nothing waits for the host.  Rows past the last
+        // assignment are gathered from token 0 and never read back.
+        BARQ_CHECK(launched(barq::quantize_q8_k_gather_launch(x, tokens, na, hidden, qb, s), "quantize_act"));
+        const size_t chunk = gt == ut ? 32 : 64;   // expert weight pointers per grouped launch
+        std::vector<const void*> wp;
+        for (size_t e0 = 0; e0 < ne; e0 += chunk) {
+            const size_t c = ne - e0 < chunk ? ne - e0 : chunk;
+            if (gt == ut) {
+                wp.assign(gate + e0, gate + e0 + c);
+                wp.insert(wp.end(), up + e0, up + e0 + c);
+                BARQ_CHECK(launched(barq::kq_grouped_launch(gt, wp.data(), c, 2, offsets + e0, na, n_ff, hidden, qb, gb,
+                                                            na * n_ff, s), "moe gate/up"));
+            } else {
+                BARQ_CHECK(launched(barq::kq_grouped_launch(gt, gate + e0, c, 1, offsets + e0, na, n_ff, hidden, qb, gb,
+                                                            0, s), "moe gate"));
+                BARQ_CHECK(launched(barq::kq_grouped_launch(ut, up + e0, c, 1, offsets + e0, na, n_ff, hidden, qb, ub,
+                                                            0, s), "moe up"));
+            }
+        }
+        BARQ_CHECK(launched(barq::swiglu_q8_k_launch(gb, ub, na, n_ff, qb, s), "swiglu"));
+        for (size_t e0 = 0; e0 < ne; e0 += 64) {
+            const size_t c = ne - e0 < 64 ? ne - e0 : 64;
+            BARQ_CHECK(launched(barq::kq_grouped_launch(dt, down + e0, c, 1, offsets + e0, na, hidden, n_ff, qb, yg, 0, s),
+                                "moe down"));
+        }
+        return launched(barq::moe_scatter_launch(yg, ids, weights, rowpos, rows, k, hidden, out, s), "moe_scatter");
+    }
     std::vector<int32_t> off(ne + 1);
     BARQ_HIP(hipMemcpyAsync(off.data(), offsets, (ne + 1) * 4, hipMemcpyDeviceToHost, s));
     BARQ_HIP(hipStreamSynchronize(s));

@@ -1,0 +1,497 @@
+// Batched K-quant x Q8_K GEMM on gfx950 int8 MFMA: Y[m, n] = sum_k X[m, k] W[n, k]
+// for Q4_K and Q6_K weights (GGUF rows, blocks along k) and Q8_K activation
+// rows.  This is the prefill path and the MoE expert-group path; a grouped
+// launch covers every expert of a MoE step, reading each expert's row range
+// from device-side offsets (no host round trip).
+//
+// Workgroup tile: BM activation rows x 128 weight rows.  Each wave owns a
+// 32-column slice (and, with eight waves, half of the BM rows) and issues
+// v_mfma_i32_32x32x32_i8, whose K = 32 covers one Q4_K sub-block or two Q6_K
+// sub-blocks; every lane's 16 k-values belong to a single sub-block, so the
+// sub-block scale can be folded into that lane's int8 operand:
+//   Q4_K: s*q with s = 8*s1 + s0 (s1, s0 in [0, 7]): s1*q and s0*q are <= 105
+//         and come from one packed 16-bit multiply per four weights; the mins
+//         are a third pass against m_j broadcast over the sub-block.
+//   Q6_K: w' = s*(q - 32) in [-4064, 4096] = 128*h + l, l in [0, 127].
+// The integer results per super-block are exact; the f32 epilogue is
+//   Q4_K: y += dx * (d * (8*Ch + Cl) - dmin * Cm)
+//   Q6_K: y += dx * d * (128*Ch + Cl)
+//
+// Data movement: NS LDS stages, each one super-block of the tile, filled by
+// buffer->LDS direct loads NS-1 super-blocks ahead of the MFMAs with one
+// barrier per super-block.  Activation rows are stored with a 16-byte pad
+// (272-byte rows: conflict-free fragment reads); Q6_K blocks are copied as the
+// dword-aligned 224-byte window around each 210-byte block (the kernel needs
+// an even number of super-blocks per row so that window offset is uniform).
+#include "launch.hpp"
+#include "mfma_common.hpp"
+
+#include <cstdlib>
+
+namespace barq {
+
+constexpr int KQ_BN = 128;       // weight rows per workgroup
+constexpr int KQ_MAXE = 64;      // expert weight pointers carried by a grouped launch
+
+struct KQWeights {
+    const uint8_t* w[KQ_MAXE];
+};
+
+struct KQ4 {
+    static constexpr int TYPE = TYPE_Q4_K, BB = Q4_K_BYTES, RS = 144, PIECES = 9;
+    static __device__ __forceinline__ uint32_t soff(int b) { return (uint32_t)b * 144u; }
+};
+struct KQ6 {
+    static constexpr int TYPE = TYPE_Q6_K, BB = Q6_K_BYTES, RS = 224, PIECES = 14;
+    // the dword-aligned start of block b's window (row bytes are a multiple of 4)
+    static __device__ __forceinline__ uint32_t soff(int b) { return (uint32_t)b * 210u & ~3u; }
+};
+
+// LDS stage layout and per-wave load counts
+template <class F, int BM, int NW>
+struct KQL {
+    static constexpr int X_CHUNKS = BM * 17;                   // 272-byte rows in 16-byte chunks
+    static constexpr int X_INSTR_ALL = (X_CHUNKS + 63) / 64;
+    static constexpr int XQ = 0;
+    static constexpr int W = X_INSTR_ALL * 1024;
+    static constexpr int W_INSTR_ALL = KQ_BN * F::PIECES / 64;
+    static constexpr int XD = W + KQ_BN * F::RS;
+    static constexpr int XD_LOADS = BM < 64 ? 1 : BM / 64;
+    static constexpr int STAGE = XD + XD_LOADS * 256;
+    static constexpr int X_INSTR = (X_INSTR_ALL + NW - 1) / NW;
+    static constexpr int W_INSTR = (W_INSTR_ALL + NW - 1) / NW;
+    static constexpr int LOADS_MIN = X_INSTR_ALL / NW + W_INSTR_ALL / NW;
+    static constexpr int MTW = BM / 32 / (NW / 4);              // 32x32 MFMA tiles per wave
+    static_assert(KQ_BN * F::PIECES % 64 == 0, "weight tile is whole load instructions");
+};
+
+template <class F, int BM, int NW>
+struct KQOff {
+    uint32_t x[KQL<F, BM, NW>::X_INSTR];
+    uint32_t w[KQL<F, BM, NW>::W_INSTR];
+    uint32_t xd;
+};
+
+template <class F, int BM, int NW>
+__device__ __forceinline__ void kq_offsets(KQOff<F, BM, NW>& o, uint32_t xrb, uint32_t wrb, int wave, int l) {
+    using L = KQL<F, BM, NW>;
+    #pragma unroll
+    for (int q = 0; q < L::X_INSTR; q++) {
+        const int p = (q * NW + wave) * 64 + l, r = p / 17, c = p - r * 17;
+        // the pad chunk (c == 16) reloads the row's first chunk
+        o.x[q] = (uint32_t)r * xrb + 4u + 16u * (uint32_t)(c < 16 ? c : 0);
+    }
+    #pragma unroll
+    for (int q = 0; q < L::W_INSTR; q++) {
+        const int p = (q * NW + wave) * 64 + l, row = p / F::PIECES, piece = p - row * F::PIECES;
+        o.w[q] = (uint32_t)row * wrb + 16u * (uint32_t)piece;
+    }
+    o.xd = (uint32_t)(64 * wave + l) * xrb;
+}
+
+template <class F, int BM, int NW>
+__device__ __forceinline__ void kq_issue(uint8_t* stage, i32x4v xr, i32x4v wr, const KQOff<F, BM, NW>& o, int b,
+                                         int wave) {
+    using L = KQL<F, BM, NW>;
+    const uint32_t xs = (uint32_t)b * Q8_K_BYTES, ws = F::soff(b);
+    #pragma unroll
+    for (int q = 0; q < L::X_INSTR; q++) {
+        const int idx = q * NW + wave;
+        if (idx < L::X_INSTR_ALL) lds_load16(xr, stage + L::XQ + 1024 * idx, o.x[q], xs);
+    }
+    #pragma unroll
+    for (int q = 0; q < L::W_INSTR; q++) {
+        const int idx = q * NW + wave;
+        if (idx < L::W_INSTR_ALL) lds_load16(wr, stage + L::W + 1024 * idx, o.w[q], ws);
+    }
+    if (wave < L::XD_LOADS) lds_load4(xr, stage + L::XD + 256 * wave, o.xd, xs);
+}
+
+// dx of the lane's 16 output rows of tile t (32x32 C layout: lane (n, g2),
+// register r -> row 8*(r/4) + 4*g2 + r%4)
+template <int MT>
+__device__ __forceinline__ void kq_dx(const uint8_t* xd, int mbase, int g2, float (&dx)[MT][16]) {
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        #pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 v = *reinterpret_cast<const float4*>(xd + 4 * (mbase + 32 * t + 8 * q + 4 * g2));
+            dx[t][4 * q] = v.x; dx[t][4 * q + 1] = v.y; dx[t][4 * q + 2] = v.z; dx[t][4 * q + 3] = v.w;
+        }
+}
+
+// ---- Q4_K super-block --------------------------------------------------------
+template <int MT>
+__device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* xrow, const uint8_t* xd, int mbase,
+                                            int g2, float (&acc)[MT][16]) {
+    const uint4 hdr = *reinterpret_cast<const uint4*>(wrow);
+    const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
+    // get_scale_min_k4 (gguf.rs:825-837) for the eight sub-blocks, bytewise
+    const uint32_t scA = hdr.y & 0x3F3F3F3Fu;
+    const uint32_t scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    const uint32_t mA = hdr.z & 0x3F3F3F3Fu;
+    const uint32_t mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    const uint32_t s1A = (scA >> 3) & 0x07070707u, s0A = scA & 0x07070707u;
+    const uint32_t s1B = (scB >> 3) & 0x07070707u, s0B = scB & 0x07070707u;
+    v16i ch[MT], cl[MT], cm[MT];
+    #pragma unroll
+    for (int pr = 0; pr < 4; pr++) {
+        // sub-blocks 2pr (low nibbles) and 2pr+1 (high nibbles) share qs[32pr + 16g2 .. +16)
+        const uint4 qs = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * pr + 16 * g2);
+        #pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int j = 2 * pr + h;
+            const uint32_t bsel = (uint32_t)(j & 3);
+            const uint32_t s1 = __builtin_amdgcn_perm(0u, j < 4 ? s1A : s1B, 0x0c000c00u | (bsel << 16) | bsel);
+            const uint32_t s0 = __builtin_amdgcn_perm(0u, j < 4 ? s0A : s0B, 0x0c000c00u | (bsel << 16) | bsel);
+            const int mb = (int)__builtin_amdgcn_perm(0u, j < 4 ? mA : mB, bsel * 0x01010101u);
+            const uint32_t n0 = (qs.x >> (4 * h)) & 0x0F0F0F0Fu, n1 = (qs.y >> (4 * h)) & 0x0F0F0F0Fu;
+            const uint32_t n2 = (qs.z >> (4 * h)) & 0x0F0F0F0Fu, n3 = (qs.w >> (4 * h)) & 0x0F0F0F0Fu;
+            const v4i bh = {(int)mul_u16x2(n0, s1), (int)mul_u16x2(n1, s1), (int)mul_u16x2(n2, s1), (int)mul_u16x2(n3, s1)};
+            const v4i bl = {(int)mul_u16x2(n0, s0), (int)mul_u16x2(n1, s0), (int)mul_u16x2(n2, s0), (int)mul_u16x2(n3, s0)};
+            const v4i bm = {mb, mb, mb, mb};
+            #pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * 272 + 32 * j);
+                const v16i z = {};
+                ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
+                cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
+                cm[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bm, j ? cm[t] : z, 0, 0, 0);
+            }
+        }
+    }
+    float dx[MT][16];
+    kq_dx<MT>(xd, mbase, g2, dx);
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int c = (ch[t][r] << 3) + cl[t][r];
+            const float v = __builtin_fmaf(-dmin, (float)cm[t][r], d * (float)c);
+            acc[t][r] = __builtin_fmaf(dx[t][r], v, acc[t][r]);
+        }
+}
+
+// ---- Q6_K super-block --------------------------------------------------------
+// 16 bytes at p + sh (p 16-byte aligned, sh in {0, 2}) from an aligned 16-byte
+// read and the following dword
+__device__ __forceinline__ uint4 lds16_sh(const uint8_t* p, uint32_t sh) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t e = *reinterpret_cast<const uint32_t*>(p + 16);
+    return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+                      __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh));
+}
+
+// four 6-bit quants q (bytes of q4) -> bytes of h and l with s*(q-32) = 128*h + l
+__device__ __forceinline__ void q6_split4(uint32_t q4, uint32_t scv, uint32_t off, int& h, int& l) {
+    const uint32_t a = mul_u16x2(__builtin_amdgcn_perm(0u, q4, 0x0c010c00u), scv);
+    const uint32_t c = mul_u16x2(__builtin_amdgcn_perm(0u, q4, 0x0c030c02u), scv);
+    const s16x2 wa = __builtin_bit_cast(s16x2, a) + __builtin_bit_cast(s16x2, off);
+    const s16x2 wc = __builtin_bit_cast(s16x2, c) + __builtin_bit_cast(s16x2, off);
+    const s16x2 ha = wa >> (short)7, hc = wc >> (short)7;
+    const s16x2 la = wa & (short)127, lc = wc & (short)127;
+    h = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hc), __builtin_bit_cast(uint32_t, ha), 0x06040200u);
+    l = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, lc), __builtin_bit_cast(uint32_t, la), 0x06040200u);
+}
+
+template <int MT>
+__device__ __forceinline__ void kq6_compute(const uint8_t* wrow, const uint8_t* xrow, const uint8_t* xd, int mbase,
+                                            int g2, int b, float (&acc)[MT][16]) {
+    // the block starts sh bytes into the copied window (gguf.rs:839-914 layout:
+    // ql[128] @0, qh[64] @128, scales[16] @192, d @208)
+    const uint32_t sh = 2u * (uint32_t)(b & 1);
+    const uint32_t dw = *reinterpret_cast<const uint32_t*>(wrow + 208);
+    const float d = f16_bits_to_f32(sh ? dw >> 16 : dw & 0xFFFFu);
+    v16i ch[MT], cl[MT];
+    #pragma unroll
+    for (int half = 0; half < 2; half++) {
+        // element 32j + 16g2 + i: half = j/4, quarter qd = j%4, position l = 16g2 + i
+        const uint4 qh = lds16_sh(wrow + 128 + 32 * half + 16 * g2, sh);
+        #pragma unroll
+        for (int odd = 0; odd < 2; odd++) {
+            const uint4 ql = lds16_sh(wrow + 64 * half + 32 * odd + 16 * g2, sh);
+            #pragma unroll
+            for (int hi = 0; hi < 2; hi++) {
+                const int qd = 2 * hi + odd, j = 4 * half + qd;
+                const int sc = (int)(int8_t)wrow[sh + 192 + 8 * half + g2 + 2 * qd];
+                const uint32_t scv = ((uint32_t)sc & 0xFFFFu) * 0x00010001u;
+                const uint32_t off = ((uint32_t)(-32 * sc) & 0xFFFFu) * 0x00010001u;
+                const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w}, qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+                int hv[4], lv[4];
+                #pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t q4 = ((qlw[i] >> (4 * hi)) & 0x0F0F0F0Fu) | (((qhw[i] >> (2 * qd)) & 0x03030303u) << 4);
+                    q6_split4(q4, scv, off, hv[i], lv[i]);
+                }
+                const v4i bh = {hv[0], hv[1], hv[2], hv[3]}, bl = {lv[0], lv[1], lv[2], lv[3]};
+                #pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * 272 + 32 * j);
+                    const v16i z = {};
+                    ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
+                    cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
+                }
+            }
+        }
+    }
+    float dx[MT][16];
+    kq_dx<MT>(xd, mbase, g2, dx);
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int c = (ch[t][r] << 7) + cl[t][r];
+            acc[t][r] = __builtin_fmaf(dx[t][r], d * (float)c, acc[t][r]);
+        }
+}
+
+// ---- pipeline ----------------------------------------------------------------
+// One step: super-block b computed from stage S (= b % NS) while the loads of
+// b+NS-1 go to stage (S-1) % NS.  Each stage is its own LDS array; the raw
+// s_barrier (no memory fence) does not drain the in-flight stages.
+template <class F, int BM, int NW, int NS, int S>
+__device__ __forceinline__ void kq_step(uint8_t* const (&stages)[4], int b, int nsb, i32x4v xr, i32x4v wr,
+                                        const KQOff<F, BM, NW>& off, int wave, int l,
+                                        float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    using L = KQL<F, BM, NW>;
+    constexpr int MT = L::MTW;
+    if (b >= nsb) return;
+    // this thread's loads of super-block b are done once at most the later
+    // stages' loads are outstanding; every thread's are after the barrier
+    if (b + NS - 2 < nsb) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (b + NS - 1 < nsb) kq_issue<F, BM, NW>(stages[(S + NS - 1) % NS], xr, wr, off, b + NS - 1, wave);
+    const uint8_t* st = stages[S];
+    const int n = l & 31, g2 = l >> 5;
+    const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
+    const uint8_t* wrow = st + L::W + (32 * slice + n) * F::RS;
+    const uint8_t* xrow = st + L::XQ + (mbase + n) * 272 + 16 * g2;
+    if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, acc);
+    else kq6_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, b, acc);
+}
+
+// One BM x 128 output tile: rows [m0, m0 + BM) of the `count` activation rows
+// at X (row bytes xrb) against weight rows [n0, n0 + 128) of W; results to
+// Y[row * N + col].  All waves of the workgroup call it with the same values.
+template <class F, int BM, int NS, int NW>
+__device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[4], const uint8_t* W, uint32_t wrb, const uint8_t* X,
+                                        uint32_t xrb, float* Y, int count, int N, int nsb, int m0, int n0, int wave,
+                                        int l) {
+    using L = KQL<F, BM, NW>;
+    constexpr int MT = L::MTW;
+    const i32x4v xr = make_rsrc4(X + (size_t)m0 * xrb, (uint32_t)((size_t)(count - m0) * xrb));
+    const i32x4v wr = make_rsrc4(W + (size_t)n0 * wrb, (uint32_t)((size_t)(N - n0) * wrb));
+
+    float acc[MT][16];
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+
+    KQOff<F, BM, NW> off;
+    kq_offsets<F, BM, NW>(off, xrb, wrb, wave, l);
+    #pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nsb) kq_issue<F, BM, NW>(stages[s], xr, wr, off, s, wave);
+    for (int b = 0; b < nsb; b += NS) {
+        kq_step<F, BM, NW, NS, 0>(stages, b, nsb, xr, wr, off, wave, l, acc);
+        kq_step<F, BM, NW, NS, 1>(stages, b + 1, nsb, xr, wr, off, wave, l, acc);
+        kq_step<F, BM, NW, NS, 2>(stages, b + 2, nsb, xr, wr, off, wave, l, acc);
+        if constexpr (NS == 4) kq_step<F, BM, NW, NS, 3>(stages, b + 3, nsb, xr, wr, off, wave, l, acc);
+    }
+
+    const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
+    if (col < N) {
+        #pragma unroll
+        for (int t = 0; t < MT; t++)
+            #pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + mb + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                if (row < count) Y[(size_t)row * N + col] = acc[t][r];
+            }
+    }
+}
+
+// Ungrouped: one tile per workgroup of the M x N product with weights wt.w[0].
+// GROUPED: nmat weight sets of ne experts each; expert e's activation and
+// output rows are [offsets[e], offsets[e+1]) of X and of Y + mat * ymat, and
+// its weights are wt.w[mat * ne + e].  Tiles exist only for rows that are
+// there: every workgroup builds the per-expert tile prefix from the device
+// offsets (lane e holds expert e) and strides over the flattened
+// (expert, m-tile, mat, n-tile) list, so no host round trip is needed.
+template <class F, int BM, int NS, int NW, bool GROUPED>
+__global__ __launch_bounds__(64 * NW, 1)
+void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb, float* __restrict__ Y, int M,
+               int N, int nsb, int tiles_m, int tiles_n, const int32_t* __restrict__ offsets, int ne, int nmat,
+               size_t ymat, int xcd_order) {
+    static_assert(NS == 3 || NS == 4, "stage count");
+    using L = KQL<F, BM, NW>;
+    __shared__ __align__(16) uint8_t st0[L::STAGE];
+    __shared__ __align__(16) uint8_t st1[L::STAGE];
+    __shared__ __align__(16) uint8_t st2[L::STAGE];
+    __shared__ __align__(16) uint8_t st3[NS == 4 ? L::STAGE : 16];
+    uint8_t* const stages[4] = {st0, st1, st2, st3};   // with NS == 3 the fourth is never used
+    const int l = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    if constexpr (!GROUPED) {
+        // workgroup i runs on XCD i % 8: give each XCD a contiguous run of
+        // tiles so neighbouring weight tiles share its L2
+        const int n_tiles = tiles_m * tiles_n;
+        int tile = blockIdx.x;
+        if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
+        const int mt = tile % tiles_m, ntile = tile / tiles_m;
+        kq_tile<F, BM, NS, NW>(stages, wt.w[0], wrb, X, xrb, Y, M, N, nsb, mt * BM, ntile * KQ_BN, wave, l);
+    } else {
+        int r0 = 0, cnt = 0;
+        if (l < ne) {
+            r0 = offsets[l];
+            cnt = offsets[l + 1] - r0;
+        }
+        const int nt = (cnt + BM - 1) / BM;
+        int inc = nt;   // inclusive prefix of m-tiles over experts
+        #pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(inc, o);
+            if (l >= o) inc += v;
+        }
+        const int s_total = __builtin_amdgcn_readfirstlane(__shfl(inc, 63));
+        const int total = s_total * nmat * tiles_n;
+        for (int t = blockIdx.x; t < total; t += gridDim.x) {
+            const int ntile = t % tiles_n, r = t / tiles_n, mat = r % nmat, s = r / nmat;
+            // expert of m-slot s: the number of experts whose tiles all lie before it
+            const int e = __builtin_amdgcn_readfirstlane(__popcll(__ballot(inc <= s)));
+            const int mt = s - __builtin_amdgcn_readfirstlane(__shfl(inc - nt, e));
+            const int row0 = __builtin_amdgcn_readfirstlane(__shfl(r0, e));
+            const int count = __builtin_amdgcn_readfirstlane(__shfl(cnt, e));
+            // the previous tile's last stages have been read by every wave
+            if (t != (int)blockIdx.x) __builtin_amdgcn_s_barrier();
+            kq_tile<F, BM, NS, NW>(stages, wt.w[mat * ne + e], wrb, X + (size_t)row0 * xrb, xrb,
+                                   Y + (size_t)mat * ymat + (size_t)row0 * N, count, N, nsb, mt * BM, ntile * KQ_BN,
+                                   wave, l);
+        }
+    }
+}
+
+// ---- launch ------------------------------------------------------------------
+static int kq_env(const char* name, int def) {
+    if (const char* e = getenv(name)) return atoi(e);
+    return def;
+}
+static const int g_kq_bm = kq_env("BARQ_GEMM_BM", 0);    // tile override for tuning: 32, 64 or 65 (64 rows, 8 waves)
+static const int g_kq_xcd = kq_env("BARQ_GEMM_XCD", 1);  // XCD-aware tile order (ungrouped)
+
+static int cu_count() {
+    static int n[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!n[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        n[dev] = v;
+    }
+    return n[dev];
+}
+
+struct KQArgs {
+    KQWeights wt;
+    uint32_t wrb, xrb;
+    const uint8_t* X;
+    float* Y;
+    int M, N, nsb;
+    const int32_t* offsets;
+    int ne, nmat;        // grouped: experts per weight set, weight sets
+    size_t total_rows;   // grouped: rows over all experts
+    size_t ymat;
+};
+
+template <class F, int BM, int NS, int NW, bool GROUPED>
+static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
+    const int tiles_n = (a.N + KQ_BN - 1) / KQ_BN;
+    int tiles_m = (a.M + BM - 1) / BM;
+    unsigned grid = (unsigned)(tiles_m * tiles_n);
+    if constexpr (GROUPED) {
+        // m-tiles over all experts: sum of ceil(c_e / BM) <= (total + ne (BM - 1)) / BM
+        const size_t slots = (a.total_rows + (size_t)a.ne * (BM - 1)) / BM;
+        const size_t tiles = slots * (size_t)a.nmat * (size_t)tiles_n;
+        const size_t per_cu = 163840 / (NS * (size_t)KQL<F, BM, NW>::STAGE);
+        const size_t cap = (size_t)cu_count() * (per_cu ? per_cu : 1);
+        grid = (unsigned)(tiles < cap ? tiles : cap);
+        tiles_m = 0;
+    }
+    hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, GROUPED>), dim3(grid), dim3(64 * NW), 0, s, a.wt, a.wrb, a.X, a.xrb,
+                       a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, g_kq_xcd);
+    return hipGetLastError();
+}
+
+// rows: M (ungrouped) or the expected rows per expert (grouped)
+template <class F, bool GROUPED>
+static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
+    // measured on MI355X: 64x128 tiles with eight waves (two per SIMD) above
+    // 32 rows, 32-row tiles with four waves for small expert groups
+    const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 65 : 32);
+    if constexpr (F::TYPE == TYPE_Q4_K) {
+        if (bm == 65) return kq_launch_t<F, 64, 4, 8, GROUPED>(a, s);
+        return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+    } else {
+        if (bm == 65) return kq_launch_t<F, 64, 3, 8, GROUPED>(a, s);
+        return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+    }
+}
+
+// Raw buffer loads use 32-bit offsets: each weight matrix and the activation
+// rows must stay below 2 GiB.  Q6_K needs row bytes that are a multiple of 4
+// (an even number of super-blocks).
+bool kq_supported(int w_type, size_t n_rows, size_t k, size_t m) {
+    if ((w_type != TYPE_Q4_K && w_type != TYPE_Q6_K) || k % 256 != 0 || k == 0 || n_rows == 0) return false;
+    const size_t nsb = k / 256;
+    if (w_type == TYPE_Q6_K && (nsb & 1)) return false;
+    const size_t wbytes = n_rows * nsb * (w_type == TYPE_Q4_K ? Q4_K_BYTES : Q6_K_BYTES);
+    const size_t xbytes = m * nsb * Q8_K_BYTES;
+    return wbytes < (1ull << 31) && xbytes < (1ull << 31) && n_rows <= (size_t)INT32_MAX;
+}
+
+static KQArgs kq_args(int w_type, size_t n_rows, size_t k, const void* xq, float* y) {
+    KQArgs a = {};
+    a.nsb = (int)(k / 256);
+    a.wrb = (uint32_t)(a.nsb * (w_type == TYPE_Q4_K ? Q4_K_BYTES : Q6_K_BYTES));
+    a.xrb = (uint32_t)(a.nsb * Q8_K_BYTES);
+    a.X = static_cast<const uint8_t*>(xq);
+    a.Y = y;
+    a.N = (int)n_rows;
+    a.ne = a.nmat = 1;
+    return a;
+}
+
+hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
+                          hipStream_t s) {
+    if (m == 0 || n_rows == 0) return hipSuccess;
+    if (!kq_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
+    KQArgs a = kq_args(w_type, n_rows, k, xq, y);
+    a.wt.w[0] = static_cast<const uint8_t*>(W);
+    a.M = (int)m;
+    return w_type == TYPE_Q4_K ? kq_dispatch<KQ4, false>(a, m, s) : kq_dispatch<KQ6, false>(a, m, s);
+}
+
+hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
+                             size_t total_rows, size_t n_rows, size_t k, const void* xq, float* y, size_t y_mat_stride,
+                             hipStream_t s) {
+    if (n_experts == 0 || n_mats == 0 || total_rows == 0 || n_rows == 0) return hipSuccess;
+    if (n_experts * n_mats > (size_t)KQ_MAXE || n_experts > 64 || !kq_supported(w_type, n_rows, k, total_rows) ||
+        total_rows > (size_t)INT32_MAX)
+        return hipErrorInvalidValue;
+    KQArgs a = kq_args(w_type, n_rows, k, xq, y);
+    for (size_t i = 0; i < n_experts * n_mats; i++) a.wt.w[i] = static_cast<const uint8_t*>(W[i]);
+    a.offsets = offsets;
+    a.ne = (int)n_experts;
+    a.nmat = (int)n_mats;
+    a.total_rows = total_rows;
+    a.ymat = y_mat_stride;
+    const size_t per_expert = (total_rows + n_experts - 1) / n_experts;
+    return w_type == TYPE_Q4_K ? kq_dispatch<KQ4, true>(a, per_expert, s) : kq_dispatch<KQ6, true>(a, per_expert, s);
+}
+
+}  // namespace barq

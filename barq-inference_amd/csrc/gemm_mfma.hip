@@ -672,9 +672,11 @@ static int pick_bm(int M, int N) {
     return bm;
 }
 
+// BARQ_GEMM_IMPL: 2 = the format-generic kernel of gemm_kq.hip (default),
+// 1 = the Q4_K-only kernel above, 0 = the 16x16x64 kernel (tuning experiments)
 static int read_env_v3() {
-    if (const char* e = getenv("BARQ_GEMM_V3")) return atoi(e);
-    return 1;
+    if (const char* e = getenv("BARQ_GEMM_IMPL")) return atoi(e);
+    return 2;
 }
 static int g_use_v3 = read_env_v3();
 // BARQ_GEMM_XCD=0 turns off the XCD-aware tile order (tuning experiments)
@@ -741,8 +743,9 @@ hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t
                                 float* y, hipStream_t s) {
     if (m == 0 || n_rows == 0) return hipSuccess;
     if (!gemm_mfma_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
+    if (g_use_v3 == 2 && kq_supported(w_type, n_rows, k, m)) return kq_gemm_launch(w_type, W, n_rows, k, xq, m, y, s);
     switch (w_type) {
-    case TYPE_Q4_K: return g_use_v3 ? dispatch_q4k_v3(W, n_rows, k, xq, m, y, s) : dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
+    case TYPE_Q4_K: return g_use_v3 == 1 ? dispatch_q4k_v3(W, n_rows, k, xq, m, y, s) : dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
     case TYPE_Q6_K: return dispatch_kq<GQ6K>(W, n_rows, k, xq, m, y, s);
     default: return hipErrorInvalidValue;
     }

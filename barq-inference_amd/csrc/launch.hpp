@@ -17,6 +17,11 @@ hipError_t dequant_split_launch(int kind_q8_0, const uint8_t* quants, size_t n_q
 hipError_t quantize_q8_0_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s);
 hipError_t quantize_q8_k_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s);
 hipError_t quantize_q4_0_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s);
+// Q8_K rows of x[rows_idx[i] * k ..] for i < n_rows (gather fused in)
+hipError_t quantize_q8_k_gather_launch(const float* x, const int32_t* rows_idx, size_t n_rows, size_t k, void* out,
+                                       hipStream_t s);
+// Q8_K rows of silu(g) * u (k-element rows; the product is not stored)
+hipError_t swiglu_q8_k_launch(const float* g, const float* u, size_t n_rows, size_t k, void* out, hipStream_t s);
 
 // gemv.hip
 hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,
@@ -29,6 +34,18 @@ void gemv_set_config(int rows_per_wave, int waves);
 hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k,
                                 const void* xq, size_t m, float* y, hipStream_t s);
 bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m);
+
+// gemm_kq.hip: the same product with 32x32x32 int8 MFMA tiles fed by
+// buffer->LDS loads; Q4_K any k % 256 == 0, Q6_K an even number of super-blocks.
+bool kq_supported(int w_type, size_t n_rows, size_t k, size_t m);
+hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
+                          hipStream_t s);
+// Expert-grouped form: rows [offsets[e], offsets[e+1]) of xq, and of
+// y + mat * y_mat_stride, use weights W[mat * n_experts + e] (offsets on the
+// device; n_experts * n_mats <= 64).  total_rows bounds offsets[n_experts].
+hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
+                             size_t total_rows, size_t n_rows, size_t k, const void* xq, float* y, size_t y_mat_stride,
+                             hipStream_t s);
 
 // f32blas.hip
 hipError_t gemm_f32_launch(const float* a, const float* b, size_t m, size_t k, size_t n, float* c,

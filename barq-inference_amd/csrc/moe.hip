@@ -86,6 +86,13 @@ __global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict
             rowpos[a] = pos;
         }
     }
+    __syncthreads();
+    // rows past the last assignment (skipped ids) point at token 0, so that
+    // consumers may process all rows * k rows without knowing the count
+    for (int p = cnt[ne] + lane; p < n; p += 64) {
+        tokens[p] = 0;
+        wts[p] = 0.0f;
+    }
 }
 
 hipError_t moe_group_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,

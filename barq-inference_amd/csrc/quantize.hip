@@ -33,13 +33,7 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
 // max = the signed value of the first element with the largest |x|;
 // iscale = -127/max; q = min(127, rint(iscale*x)); d = 1/iscale;
 // bsums[g] = sum of q[16g .. 16g+16).  An all-zero block stores zeros.
-__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x,
-                                                            uint8_t* __restrict__ out, size_t nb) {
-    const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= nb) return;  // whole waves exit together
-    const int lane = threadIdx.x & 63;
-    const float4 v = reinterpret_cast<const float4*>(x + b * 256)[lane];
-    const float vv[4] = {v.x, v.y, v.z, v.w};
+__device__ __forceinline__ void q8_k_block(const float (&vv)[4], int lane, uint8_t* __restrict__ blk) {
     float ba = 0.0f, bv = 0.0f;
     int bi = 0x7fffffff;
     #pragma unroll
@@ -54,7 +48,6 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restr
         const int oi = __shfl_xor(bi, off);
         if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
     }
-    uint8_t* blk = out + b * 292;
     if (ba == 0.0f) {
         reinterpret_cast<uint32_t*>(blk + 4)[lane] = 0u;
         if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = 0;
@@ -76,6 +69,50 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restr
     s += __shfl_xor(s, 2);
     if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
     if (lane == 0) *reinterpret_cast<float*>(blk) = 1.0f / iscale;
+}
+
+__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x,
+                                                            uint8_t* __restrict__ out, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;  // whole waves exit together
+    const int lane = threadIdx.x & 63;
+    const float4 v = reinterpret_cast<const float4*>(x + b * 256)[lane];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    q8_k_block(vv, lane, out + b * 292);
+}
+
+// Q8_K of rows x[rows_idx[i]] (a MoE row gather fused into the quantizer);
+// nbr blocks per row.
+__global__ __launch_bounds__(256) void quantize_q8_k_gather_kernel(const float* __restrict__ x,
+                                                                   const int32_t* __restrict__ rows_idx, size_t nbr,
+                                                                   uint8_t* __restrict__ out, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;
+    const int lane = threadIdx.x & 63;
+    const size_t i = b / nbr, cb = b - i * nbr;
+    const float4 v = reinterpret_cast<const float4*>(x + ((size_t)rows_idx[i] * nbr + cb) * 256)[lane];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    q8_k_block(vv, lane, out + b * 292);
+}
+
+// Q8_K of h = silu(g) * u, silu(g) = g / (1 + exp(-g)) rounded first
+// (ops.rs:191-211, moe_fused.rs:61-66): the SwiGLU product is formed in
+// registers and never stored.
+__global__ __launch_bounds__(256) void swiglu_q8_k_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          uint8_t* __restrict__ out, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;
+    const int lane = threadIdx.x & 63;
+    const float4 gv = reinterpret_cast<const float4*>(g + b * 256)[lane];
+    const float4 uv = reinterpret_cast<const float4*>(u + b * 256)[lane];
+    const float ga[4] = {gv.x, gv.y, gv.z, gv.w}, ua[4] = {uv.x, uv.y, uv.z, uv.w};
+    float vv[4];
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float a = ga[j] / (1.0f + expf(-ga[j]));
+        vv[j] = a * ua[j];
+    }
+    q8_k_block(vv, lane, out + b * 292);
 }
 
 // quant::Q4_0::quantize (quant/src/q4_0.rs:23-67): scale = max_abs/8 (0 for an
@@ -119,6 +156,23 @@ hipError_t quantize_q8_k_launch(const float* x, size_t n_rows, size_t k, void* o
     const size_t nb = n_rows * (k / 256);
     if (nb == 0) return hipSuccess;
     hipLaunchKernelGGL(quantize_q8_k_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x,
+                       static_cast<uint8_t*>(out), nb);
+    return hipGetLastError();
+}
+
+hipError_t quantize_q8_k_gather_launch(const float* x, const int32_t* rows_idx, size_t n_rows, size_t k, void* out,
+                                      hipStream_t s) {
+    const size_t nbr = k / 256, nb = n_rows * nbr;
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8_k_gather_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, rows_idx, nbr,
+                       static_cast<uint8_t*>(out), nb);
+    return hipGetLastError();
+}
+
+hipError_t swiglu_q8_k_launch(const float* g, const float* u, size_t n_rows, size_t k, void* out, hipStream_t s) {
+    const size_t nb = n_rows * (k / 256);
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_q8_k_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, g, u,
                        static_cast<uint8_t*>(out), nb);
     return hipGetLastError();
 }

@@ -286,3 +286,45 @@ def test_moe_ffn_small(be, orc, act):
     # host-memory entry point gives the same result
     out_h = be.moe_ffn(B.Q4_K, gates, B.Q4_K, ups, B.Q6_K, downs, hid, nff, x, rows, ids, w, k, a, mem=B.MEM_HOST)
     assert np.array_equal(out_h, host(out))
+
+
+def _moe_case(orc, ne, hid, nff, rows, k, seed, gt=B.Q4_K, ut=B.Q4_K, dt=B.Q6_K):
+    gen = {B.Q4_K: synth.gen_q4_k, B.Q6_K: synth.gen_q6_k}
+    gates = [gen[gt](nff, hid, seed + e) for e in range(ne)]
+    ups = [gen[ut](nff, hid, seed + 100 + e) for e in range(ne)]
+    downs = [gen[dt](hid, nff, seed + 200 + e) for e in range(ne)]
+    x = synth.gen_f32(rows * hid, seed + 300).reshape(rows, hid)
+    ids, w = orc.moe_select_top_k(synth.gen_f32(rows * ne, seed + 301).reshape(rows, ne), k)
+    return gates, ups, downs, x, np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(w, np.float32)
+
+
+# Expert-grouped integer path (one launch per weight set, row ranges read on
+# the device): skewed and empty experts, skipped and repeated ids, more
+# experts than one launch carries, mixed gate/up types, 64-row tiles, and the
+# per-expert fallback for Q6_K with an odd number of super-blocks.
+MOE_CASES = {
+    "skew": dict(ne=5, hid=512, nff=1024, rows=40, k=2),
+    "many_experts": dict(ne=40, hid=256, nff=512, rows=24, k=3),
+    "mixed_types": dict(ne=3, hid=512, nff=512, rows=20, k=2, gt=B.Q6_K, ut=B.Q4_K),
+    "wide_tiles": dict(ne=2, hid=256, nff=512, rows=80, k=2),
+    "odd_q6k_fallback": dict(ne=3, hid=256, nff=768, rows=12, k=2),
+}
+
+
+@pytest.mark.parametrize("name", list(MOE_CASES))
+def test_moe_ffn_grouped_cases(be, orc, name):
+    c = dict(MOE_CASES[name])
+    ne, hid, nff, rows, k = c.pop("ne"), c.pop("hid"), c.pop("nff"), c.pop("rows"), c.pop("k")
+    gt, ut, dt = c.get("gt", B.Q4_K), c.get("ut", B.Q4_K), B.Q6_K
+    gates, ups, downs, x, ids, w = _moe_case(orc, ne, hid, nff, rows, k, 500 + len(name), gt, ut, dt)
+    if name == "skew":
+        ids[:, 0] = 0           # expert 0: 40 rows (two 32-row tiles); expert 3 stays empty
+        ids[:, 1] = np.where(ids[:, 1] == 3, 1, ids[:, 1])
+        ids[ids[:, 1] == 0, 1] = 2
+        ids[5, 1] = -1          # skipped ids
+        ids[6, 1] = ne
+        ids[7, :] = [2, 2]      # a repeated expert
+    out = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs], hid, nff,
+                     dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
+    ref = orc.moe_ffn(gt, gates, ut, ups, dt, downs, hid, nff, x, ids, w, orc.Q8_K)
+    assert_close_1e3(host(out), ref)
