@@ -27,6 +27,7 @@
 #include "mfma_common.hpp"
 
 #include <cstdlib>
+#include <utility>
 
 namespace barq {
 
@@ -37,12 +38,15 @@ struct KQWeights {
     const uint8_t* w[KQ_MAXE];
 };
 
+// XC: 16-byte chunks per staged activation row: the 256 quants, for Q4_K the
+// 16 bsums (sub-block sums for the mins), and one pad chunk that keeps rows
+// of a 32-row fragment read on distinct LDS banks.
 struct KQ4 {
-    static constexpr int TYPE = TYPE_Q4_K, BB = Q4_K_BYTES, RS = 144, PIECES = 9;
+    static constexpr int TYPE = TYPE_Q4_K, BB = Q4_K_BYTES, RS = 144, PIECES = 9, XC = 19, XRS = 16 * XC;
     static __device__ __forceinline__ uint32_t soff(int b) { return (uint32_t)b * 144u; }
 };
 struct KQ6 {
-    static constexpr int TYPE = TYPE_Q6_K, BB = Q6_K_BYTES, RS = 224, PIECES = 14;
+    static constexpr int TYPE = TYPE_Q6_K, BB = Q6_K_BYTES, RS = 224, PIECES = 14, XC = 17, XRS = 16 * XC;
     // the dword-aligned start of block b's window (row bytes are a multiple of 4)
     static __device__ __forceinline__ uint32_t soff(int b) { return (uint32_t)b * 210u & ~3u; }
 };
@@ -50,7 +54,7 @@ struct KQ6 {
 // LDS stage layout and per-wave load counts
 template <class F, int BM, int NW>
 struct KQL {
-    static constexpr int X_CHUNKS = BM * 17;                   // 272-byte rows in 16-byte chunks
+    static constexpr int X_CHUNKS = BM * F::XC;                // activation rows in 16-byte chunks
     static constexpr int X_INSTR_ALL = (X_CHUNKS + 63) / 64;
     static constexpr int XQ = 0;
     static constexpr int W = X_INSTR_ALL * 1024;
@@ -77,9 +81,9 @@ __device__ __forceinline__ void kq_offsets(KQOff<F, BM, NW>& o, uint32_t xrb, ui
     using L = KQL<F, BM, NW>;
     #pragma unroll
     for (int q = 0; q < L::X_INSTR; q++) {
-        const int p = (q * NW + wave) * 64 + l, r = p / 17, c = p - r * 17;
-        // the pad chunk (c == 16) reloads the row's first chunk
-        o.x[q] = (uint32_t)r * xrb + 4u + 16u * (uint32_t)(c < 16 ? c : 0);
+        const int p = (q * NW + wave) * 64 + l, r = p / F::XC, c = p - r * F::XC;
+        // quants at 4 + 16c, bsums at 260 + 16 (c - 16); the pad chunk reloads chunk 0
+        o.x[q] = (uint32_t)r * xrb + 4u + 16u * (uint32_t)(c < F::XC - 1 ? c : 0);
     }
     #pragma unroll
     for (int q = 0; q < L::W_INSTR; q++) {
@@ -121,9 +125,23 @@ __device__ __forceinline__ void kq_dx(const uint8_t* xd, int mbase, int g2, floa
 }
 
 // ---- Q4_K super-block --------------------------------------------------------
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Eight signed 16-bit values as f16 (exact: |bsum| <= 16 * 128)
+__device__ __forceinline__ h8 i16x8_to_h8(uint4 w) {
+    h8 r;
+    r[0] = (_Float16)(short)(w.x & 0xFFFFu); r[1] = (_Float16)(short)(w.x >> 16);
+    r[2] = (_Float16)(short)(w.y & 0xFFFFu); r[3] = (_Float16)(short)(w.y >> 16);
+    r[4] = (_Float16)(short)(w.z & 0xFFFFu); r[5] = (_Float16)(short)(w.z >> 16);
+    r[6] = (_Float16)(short)(w.w & 0xFFFFu); r[7] = (_Float16)(short)(w.w >> 16);
+    return r;
+}
+
 template <int MT>
 __device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* xrow, const uint8_t* xd, int mbase,
                                             int g2, float (&acc)[MT][16]) {
+    constexpr int XRS = KQ4::XRS;
     const uint4 hdr = *reinterpret_cast<const uint4*>(wrow);
     const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
     // get_scale_min_k4 (gguf.rs:825-837) for the eight sub-blocks, bytewise
@@ -133,7 +151,26 @@ __device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* 
     const uint32_t mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
     const uint32_t s1A = (scA >> 3) & 0x07070707u, s0A = scA & 0x07070707u;
     const uint32_t s1B = (scB >> 3) & 0x07070707u, s0B = scB & 0x07070707u;
-    v16i ch[MT], cl[MT], cm[MT];
+    // Mins: sum_j m_j * (sum of x over sub-block j) as one f16 MFMA with
+    // K = the 16 bsums: lane group g2 holds bsums 8 g2 .. 8 g2 + 7, i.e. both
+    // halves of sub-blocks 4 g2 .. 4 g2 + 3, against m of those sub-blocks.
+    // Every value and partial sum is an integer below 2^24: exact in f32.
+    const uint32_t mm = g2 ? mB : mA;
+    h8 bmin;
+    #pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const _Float16 m = (_Float16)(float)((mm >> (8 * q)) & 0xFFu);
+        bmin[2 * q] = m;
+        bmin[2 * q + 1] = m;
+    }
+    f32x16 cm[MT];
+    #pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const h8 amin = i16x8_to_h8(*reinterpret_cast<const uint4*>(xrow + 32 * t * XRS + 256));
+        const f32x16 z = {};
+        cm[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, bmin, z, 0, 0, 0);
+    }
+    v16i ch[MT], cl[MT];
     #pragma unroll
     for (int pr = 0; pr < 4; pr++) {
         // sub-blocks 2pr (low nibbles) and 2pr+1 (high nibbles) share qs[32pr + 16g2 .. +16)
@@ -144,19 +181,16 @@ __device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* 
             const uint32_t bsel = (uint32_t)(j & 3);
             const uint32_t s1 = __builtin_amdgcn_perm(0u, j < 4 ? s1A : s1B, 0x0c000c00u | (bsel << 16) | bsel);
             const uint32_t s0 = __builtin_amdgcn_perm(0u, j < 4 ? s0A : s0B, 0x0c000c00u | (bsel << 16) | bsel);
-            const int mb = (int)__builtin_amdgcn_perm(0u, j < 4 ? mA : mB, bsel * 0x01010101u);
             const uint32_t n0 = (qs.x >> (4 * h)) & 0x0F0F0F0Fu, n1 = (qs.y >> (4 * h)) & 0x0F0F0F0Fu;
             const uint32_t n2 = (qs.z >> (4 * h)) & 0x0F0F0F0Fu, n3 = (qs.w >> (4 * h)) & 0x0F0F0F0Fu;
             const v4i bh = {(int)mul_u16x2(n0, s1), (int)mul_u16x2(n1, s1), (int)mul_u16x2(n2, s1), (int)mul_u16x2(n3, s1)};
             const v4i bl = {(int)mul_u16x2(n0, s0), (int)mul_u16x2(n1, s0), (int)mul_u16x2(n2, s0), (int)mul_u16x2(n3, s0)};
-            const v4i bm = {mb, mb, mb, mb};
             #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * 272 + 32 * j);
+                const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * XRS + 32 * j);
                 const v16i z = {};
                 ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
                 cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
-                cm[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bm, j ? cm[t] : z, 0, 0, 0);
             }
         }
     }
@@ -167,7 +201,7 @@ __device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* 
         #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int c = (ch[t][r] << 3) + cl[t][r];
-            const float v = __builtin_fmaf(-dmin, (float)cm[t][r], d * (float)c);
+            const float v = __builtin_fmaf(-dmin, cm[t][r], d * (float)c);
             acc[t][r] = __builtin_fmaf(dx[t][r], v, acc[t][r]);
         }
 }
@@ -226,7 +260,7 @@ __device__ __forceinline__ void kq6_compute(const uint8_t* wrow, const uint8_t* 
                 const v4i bh = {hv[0], hv[1], hv[2], hv[3]}, bl = {lv[0], lv[1], lv[2], lv[3]};
                 #pragma unroll
                 for (int t = 0; t < MT; t++) {
-                    const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * 272 + 32 * j);
+                    const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * KQ6::XRS + 32 * j);
                     const v16i z = {};
                     ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
                     cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
@@ -249,8 +283,10 @@ __device__ __forceinline__ void kq6_compute(const uint8_t* wrow, const uint8_t* 
 // One step: super-block b computed from stage S (= b % NS) while the loads of
 // b+NS-1 go to stage (S-1) % NS.  Each stage is its own LDS array; the raw
 // s_barrier (no memory fence) does not drain the in-flight stages.
+constexpr int KQ_MAX_NS = 6;
+
 template <class F, int BM, int NW, int NS, int S>
-__device__ __forceinline__ void kq_step(uint8_t* const (&stages)[4], int b, int nsb, i32x4v xr, i32x4v wr,
+__device__ __forceinline__ void kq_step(uint8_t* const (&stages)[KQ_MAX_NS], int b, int nsb, i32x4v xr, i32x4v wr,
                                         const KQOff<F, BM, NW>& off, int wave, int l,
                                         float (&acc)[KQL<F, BM, NW>::MTW][16]) {
     using L = KQL<F, BM, NW>;
@@ -268,7 +304,7 @@ __device__ __forceinline__ void kq_step(uint8_t* const (&stages)[4], int b, int 
     const int n = l & 31, g2 = l >> 5;
     const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
     const uint8_t* wrow = st + L::W + (32 * slice + n) * F::RS;
-    const uint8_t* xrow = st + L::XQ + (mbase + n) * 272 + 16 * g2;
+    const uint8_t* xrow = st + L::XQ + (mbase + n) * F::XRS + 16 * g2;
     if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, acc);
     else kq6_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, b, acc);
 }
@@ -276,8 +312,16 @@ __device__ __forceinline__ void kq_step(uint8_t* const (&stages)[4], int b, int 
 // One BM x 128 output tile: rows [m0, m0 + BM) of the `count` activation rows
 // at X (row bytes xrb) against weight rows [n0, n0 + 128) of W; results to
 // Y[row * N + col].  All waves of the workgroup call it with the same values.
+// NS consecutive steps (one per stage), unrolled so that stage indices are constants
+template <class F, int BM, int NW, int NS, int... S>
+__device__ __forceinline__ void kq_round(std::integer_sequence<int, S...>, uint8_t* const (&stages)[KQ_MAX_NS], int b,
+                                         int nsb, i32x4v xr, i32x4v wr, const KQOff<F, BM, NW>& off, int wave, int l,
+                                         float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    (kq_step<F, BM, NW, NS, S>(stages, b + S, nsb, xr, wr, off, wave, l, acc), ...);
+}
+
 template <class F, int BM, int NS, int NW>
-__device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[4], const uint8_t* W, uint32_t wrb, const uint8_t* X,
+__device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], const uint8_t* W, uint32_t wrb, const uint8_t* X,
                                         uint32_t xrb, float* Y, int count, int N, int nsb, int m0, int n0, int wave,
                                         int l) {
     using L = KQL<F, BM, NW>;
@@ -296,12 +340,8 @@ __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[4], const uint8
     #pragma unroll
     for (int s = 0; s < NS - 1; s++)
         if (s < nsb) kq_issue<F, BM, NW>(stages[s], xr, wr, off, s, wave);
-    for (int b = 0; b < nsb; b += NS) {
-        kq_step<F, BM, NW, NS, 0>(stages, b, nsb, xr, wr, off, wave, l, acc);
-        kq_step<F, BM, NW, NS, 1>(stages, b + 1, nsb, xr, wr, off, wave, l, acc);
-        kq_step<F, BM, NW, NS, 2>(stages, b + 2, nsb, xr, wr, off, wave, l, acc);
-        if constexpr (NS == 4) kq_step<F, BM, NW, NS, 3>(stages, b + 3, nsb, xr, wr, off, wave, l, acc);
-    }
+    for (int b = 0; b < nsb; b += NS)
+        kq_round<F, BM, NW, NS>(std::make_integer_sequence<int, NS>{}, stages, b, nsb, xr, wr, off, wave, l, acc);
 
     const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
     if (col < N) {
@@ -327,13 +367,16 @@ __global__ __launch_bounds__(64 * NW, 1)
 void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb, float* __restrict__ Y, int M,
                int N, int nsb, int tiles_m, int tiles_n, const int32_t* __restrict__ offsets, int ne, int nmat,
                size_t ymat, int xcd_order) {
-    static_assert(NS == 3 || NS == 4, "stage count");
+    static_assert(NS >= 3 && NS <= KQ_MAX_NS, "stage count");
     using L = KQL<F, BM, NW>;
+    // one array per stage (stages beyond NS are unused 16-byte stubs)
     __shared__ __align__(16) uint8_t st0[L::STAGE];
     __shared__ __align__(16) uint8_t st1[L::STAGE];
     __shared__ __align__(16) uint8_t st2[L::STAGE];
-    __shared__ __align__(16) uint8_t st3[NS == 4 ? L::STAGE : 16];
-    uint8_t* const stages[4] = {st0, st1, st2, st3};   // with NS == 3 the fourth is never used
+    __shared__ __align__(16) uint8_t st3[NS > 3 ? L::STAGE : 16];
+    __shared__ __align__(16) uint8_t st4[NS > 4 ? L::STAGE : 16];
+    __shared__ __align__(16) uint8_t st5[NS > 5 ? L::STAGE : 16];
+    uint8_t* const stages[KQ_MAX_NS] = {st0, st1, st2, st3, st4, st5};
     const int l = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
@@ -427,7 +470,11 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// rows: M (ungrouped) or the expected rows per expert (grouped)
+static const int g_kq_ns = kq_env("BARQ_GEMM_NS", 0);   // stage-count override for tuning
+
+// rows: M (ungrouped) or the expected rows per expert (grouped).  Stage
+// counts are the most that fit the 160 KiB of LDS (deeper pipelines keep
+// more HBM requests in flight per CU).
 template <class F, bool GROUPED>
 static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // measured on MI355X: 64x128 tiles with eight waves (two per SIMD) above
@@ -435,10 +482,13 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 65 : 32);
     if constexpr (F::TYPE == TYPE_Q4_K) {
         if (bm == 65) return kq_launch_t<F, 64, 4, 8, GROUPED>(a, s);
-        return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+        if (g_kq_ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+        if (g_kq_ns == 4) return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);
+        return kq_launch_t<F, 32, 5, 4, GROUPED>(a, s);
     } else {
         if (bm == 65) return kq_launch_t<F, 64, 3, 8, GROUPED>(a, s);
-        return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+        if (g_kq_ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+        return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);
     }
 }
 

@@ -197,11 +197,31 @@ static hipError_t launch_f32(const uint8_t* W, size_t row_bytes, const float* x,
     return hipGetLastError();
 }
 
+// Formats that take the LDS-streaming GEMV (gemv_dma.hip) when its layout
+// conditions hold; BARQ_GEMV_DMA_TYPES (bit per format, tuning) overrides.
+static int dma_bit(int w_type) {
+    switch (w_type) {
+    case TYPE_Q4_K: return 1;
+    case TYPE_Q6_K: return 2;
+    case TYPE_Q4_0: return 4;
+    case TYPE_Q8_0: return 8;
+    case TYPE_Q4_0_BARQ: return 16;
+    default: return 0;
+    }
+}
+static int read_env_dma_types() {
+    if (const char* e = getenv("BARQ_GEMV_DMA_TYPES")) return atoi(e);
+    return 2 | 4 | 8 | 16;
+}
+static const int g_dma_types = read_env_dma_types();
+
 hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,
                           float* y, hipStream_t s) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     const int n = (int)n_rows, kk = (int)k;
+    if (g_dma_types & dma_bit(w_type) && gemv_dma_supported(w_type, W, n_rows, k, xq))
+        return gemv_dma_launch(w_type, W, n_rows, k, xq, y, s);
     switch (w_type) {
     case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, {2, 2});
     case TYPE_Q6_K: return dispatch_q8<FmtQ6K>(w, k / 256 * 210, x, y, n, kk, s, {1, 8});

@@ -1,0 +1,394 @@
+// Batch-1 quantized GEMV with coalesced weight streaming (gfx950).
+//
+// GGUF blocks are 18, 20, 34, 144 or 210 bytes, so the per-lane loads of a
+// register-direct GEMV are often only 2-byte aligned and every row costs
+// many partially overlapping memory instructions.  Here each wave copies
+// whole 4096-element row slices into its own LDS buffers with buffer->LDS
+// direct loads (every lane 16 contiguous bytes per instruction), D slices
+// ahead of the arithmetic, and the lanes then read their part of the blocks
+// from LDS with aligned loads (plus a funnel shift where a block starts 2
+// bytes past a dword).  Q6_K slices are copied as one 27-chunk window per
+// block pair (420 bytes), so every block starts 0 or 2 bytes past a 16-byte
+// LDS boundary.  The activation vector is staged in LDS once per workgroup
+// (Q8_K blocks with quants, bsums and scale on 16-byte boundaries; Q8_0 as
+// is).
+//
+// The per-lane arithmetic is the register GEMV's (FmtQ4K::dot etc.): the
+// same integer dot products, scale handling and reduction.
+#include "gemv_formats.hpp"
+#include "launch.hpp"
+#include "mfma_common.hpp"
+
+namespace barq {
+
+// 16 bytes at p + sh, p 16-byte aligned, sh in {0, 2}
+__device__ __forceinline__ uint4 lds_rd16(const uint8_t* p, uint32_t sh) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t e = *reinterpret_cast<const uint32_t*>(p + 16);
+    return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+                      __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh));
+}
+
+typedef uint32_t u32a4 __attribute__((aligned(4)));
+
+// N dwords from a 4-byte aligned LDS address
+template <int N>
+__device__ __forceinline__ void lds_dwords(const uint8_t* p, uint32_t (&w)[N]) {
+    #pragma unroll
+    for (int i = 0; i < N; i++) w[i] = reinterpret_cast<const u32a4*>(p)[i];
+}
+
+__device__ __forceinline__ uint4 shift2(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t e) {
+    return make_uint4(__builtin_amdgcn_alignbyte(b, a, 2), __builtin_amdgcn_alignbyte(c, b, 2),
+                      __builtin_amdgcn_alignbyte(d, c, 2), __builtin_amdgcn_alignbyte(e, d, 2));
+}
+
+constexpr uint32_t DMA_SKIP = 0x80000000u;   // per-lane offset past every descriptor's range: loads zeros
+
+// ---- staged activation layouts ---------------------------------------------
+// Q8_K: each 292-byte block as 19 chunks: quants 0..15 (16-byte aligned),
+// bsums in chunks 16-17, the f32 scale at byte 288.
+struct XStageQ8K {
+    static constexpr int BLK_ELEMS = 256;
+    static __device__ __forceinline__ int chunks(int nblk) { return nblk * 19; }
+    static __device__ __forceinline__ uint32_t src(int j, int nblk) {
+        const int b = j / 19, c = j - b * 19;
+        if (b >= nblk) return DMA_SKIP;
+        return (uint32_t)b * Q8_K_BYTES + (c < 16 ? 4u + 16u * c : c < 18 ? 260u + 16u * (c - 16) : 0u);
+    }
+    static __device__ __forceinline__ const uint8_t* blk(const uint8_t* xs, int b) { return xs + 304 * b; }
+};
+// Q8_0: the 34-byte blocks copied as they are (pairs of blocks are 4-byte aligned)
+struct XStageQ80 {
+    static constexpr int BLK_ELEMS = 32;
+    static __device__ __forceinline__ int chunks(int nblk) { return (nblk * Q8_0_BYTES + 15) / 16; }
+    static __device__ __forceinline__ uint32_t src(int j, int nblk) {
+        return j < chunks(nblk) ? 16u * (uint32_t)j : DMA_SKIP;
+    }
+};
+
+// Q8_0 activation of lane l's block pair (2b, 2b + 1) from the staged copy
+__device__ __forceinline__ void stage_x_q8_0(XQ80& x, const uint8_t* xs, int b) {
+    uint32_t w[17];
+    lds_dwords<17>(xs + 34 * b, w);
+    x.dx[0] = f16_bits_to_f32(w[0] & 0xFFFFu);
+    x.v[0] = shift2(w[0], w[1], w[2], w[3], w[4]);
+    x.v[1] = shift2(w[4], w[5], w[6], w[7], w[8]);
+    x.dx[1] = f16_bits_to_f32(w[8] >> 16);
+    x.v[2] = make_uint4(w[9], w[10], w[11], w[12]);
+    x.v[3] = make_uint4(w[13], w[14], w[15], w[16]);
+    x.s[0] = bytesum16(x.v[0]) + bytesum16(x.v[1]);
+    x.s[1] = bytesum16(x.v[2]) + bytesum16(x.v[3]);
+}
+
+// ---- weight slice layouts (4096 elements of one row per slice) ------------
+// Q6_K: eight 27-chunk windows, one per block pair, so each block starts 0 or
+// 2 bytes past a 16-byte boundary of the LDS copy.
+struct DQ6K {
+    using F = FmtQ6K;
+    using XS = XStageQ8K;
+    static constexpr int SLICE_BLOCKS = 16, SLICE_BYTES = 16 * Q6_K_BYTES, SLICE_INSTR = 4;
+    static __device__ __forceinline__ uint32_t slice_src(int i) {
+        const int p = i / 27, c = i - p * 27;
+        return p < 8 ? (uint32_t)(420 * p + 16 * c) : DMA_SKIP;
+    }
+    static __device__ __forceinline__ void load_w(F::Wt& w, const uint8_t* sl, const F::Lane& c) {
+        const uint32_t sh = 2u * (uint32_t)(c.bl & 1);
+        const uint8_t* blk = sl + 432 * (c.bl >> 1) + 208 * (c.bl & 1);
+        w.a = lds_rd16(blk + 64 * c.h + c.lr, sh);
+        w.b = lds_rd16(blk + 64 * c.h + 32 + c.lr, sh);
+        w.h = lds_rd16(blk + 128 + 32 * c.h + c.lr, sh);
+        const uint2 s2 = *reinterpret_cast<const uint2*>(blk + 192 + 8 * c.h);
+        const uint32_t e = *reinterpret_cast<const uint32_t*>(blk + 200 + 8 * c.h);
+        w.sc = make_uint2(__builtin_amdgcn_alignbyte(s2.y, s2.x, sh), __builtin_amdgcn_alignbyte(e, s2.y, sh));
+        const uint32_t dw = *reinterpret_cast<const uint32_t*>(blk + 208);
+        w.d = sh ? dw >> 16 : dw & 0xFFFFu;
+    }
+    static __device__ __forceinline__ void load_x(F::X& x, const uint8_t* xs, int it, const F::Lane& c, int nblk) {
+        const int b = it * 16 + c.bl;
+        const uint8_t* xb = XS::blk(xs, b < nblk ? b : 0);
+        x.dx = *reinterpret_cast<const float*>(xb + 288);
+        #pragma unroll
+        for (int qd = 0; qd < 4; qd++) x.v[qd] = *reinterpret_cast<const uint4*>(xb + 16 * (8 * c.h + c.s0 + 2 * qd));
+        const uint4 bs = *reinterpret_cast<const uint4*>(xb + 16 * (16 + c.h));
+        const uint32_t o = 16u * (uint32_t)c.s0;
+        x.bs32[0] = 32 * sext16(bs.x, o);
+        x.bs32[1] = 32 * sext16(bs.y, o);
+        x.bs32[2] = 32 * sext16(bs.z, o);
+        x.bs32[3] = 32 * sext16(bs.w, o);
+    }
+};
+
+// Q4_K: the slice is 144 contiguous 16-byte aligned chunks
+struct DQ4K {
+    using F = FmtQ4K;
+    using XS = XStageQ8K;
+    static constexpr int SLICE_BLOCKS = 16, SLICE_BYTES = 16 * Q4_K_BYTES, SLICE_INSTR = 3;
+    static __device__ __forceinline__ uint32_t slice_src(int i) { return i < 144 ? 16u * (uint32_t)i : DMA_SKIP; }
+    static __device__ __forceinline__ void load_w(F::Wt& w, const uint8_t* sl, const F::Lane& c) {
+        const uint8_t* b = sl + 144 * c.sbl;
+        w.hdr = *reinterpret_cast<const uint4*>(b);
+        w.q0 = *reinterpret_cast<const uint4*>(b + 16 + 32 * c.p);
+        w.q1 = *reinterpret_cast<const uint4*>(b + 32 + 32 * c.p);
+    }
+    static __device__ __forceinline__ void load_x(F::X& x, const uint8_t* xs, int it, const F::Lane& c, int nblk) {
+        const int b = it * 16 + c.sbl;
+        const uint8_t* xb = XS::blk(xs, b < nblk ? b : 0);
+        x.dx = *reinterpret_cast<const float*>(xb + 288);
+        #pragma unroll
+        for (int i = 0; i < 4; i++) x.v[i] = *reinterpret_cast<const uint4*>(xb + 16 * (4 * c.p + i));
+        const uint2 bs = *reinterpret_cast<const uint2*>(xb + 16 * (16 + (c.p >> 1)) + 8 * (c.p & 1));
+        x.sa = sext16(bs.x, 0) + sext16(bs.x, 16);
+        x.sb = sext16(bs.y, 0) + sext16(bs.y, 16);
+    }
+};
+
+// Q4_0 (18-byte blocks): lane l's block pair is 36 bytes at 36 l
+struct DQ40 {
+    using F = FmtQ40;
+    using XS = XStageQ80;
+    static constexpr int SLICE_BLOCKS = 128, SLICE_BYTES = 128 * Q4_0_BYTES, SLICE_INSTR = 3;
+    static __device__ __forceinline__ uint32_t slice_src(int i) { return i < 144 ? 16u * (uint32_t)i : DMA_SKIP; }
+    static __device__ __forceinline__ void load_w(F::Wt& w, const uint8_t* sl, const F::Lane& c) {
+        uint32_t v[9];
+        lds_dwords<9>(sl + 36 * c.l, v);
+        w.d[0] = v[0] & 0xFFFFu;
+        w.q[0] = shift2(v[0], v[1], v[2], v[3], v[4]);
+        w.d[1] = v[4] >> 16;
+        w.q[1] = make_uint4(v[5], v[6], v[7], v[8]);
+    }
+    static __device__ __forceinline__ void load_x(F::X& x, const uint8_t* xs, int it, const F::Lane& c, int nblk) {
+        const int b = it * 128 + 2 * c.l;
+        stage_x_q8_0(x, xs, b < nblk ? b : 0);
+    }
+};
+
+// Q8_0 weights (34-byte blocks): lane l's block pair is 68 bytes at 68 l
+struct DQ80 {
+    using F = FmtQ80;
+    using XS = XStageQ80;
+    static constexpr int SLICE_BLOCKS = 128, SLICE_BYTES = 128 * Q8_0_BYTES, SLICE_INSTR = 5;
+    static __device__ __forceinline__ uint32_t slice_src(int i) { return i < 272 ? 16u * (uint32_t)i : DMA_SKIP; }
+    static __device__ __forceinline__ void load_w(F::Wt& w, const uint8_t* sl, const F::Lane& c) {
+        uint32_t v[17];
+        lds_dwords<17>(sl + 68 * c.l, v);
+        w.d[0] = v[0] & 0xFFFFu;
+        w.q[0] = shift2(v[0], v[1], v[2], v[3], v[4]);
+        w.q[1] = shift2(v[4], v[5], v[6], v[7], v[8]);
+        w.d[1] = v[8] >> 16;
+        w.q[2] = make_uint4(v[9], v[10], v[11], v[12]);
+        w.q[3] = make_uint4(v[13], v[14], v[15], v[16]);
+    }
+    static __device__ __forceinline__ void load_x(F::X& x, const uint8_t* xs, int it, const F::Lane& c, int nblk) {
+        const int b = it * 128 + 2 * c.l;
+        stage_x_q8_0(x, xs, b < nblk ? b : 0);
+    }
+};
+
+// Q4_0_BARQ (20-byte blocks): lane l's block pair is 40 bytes at 40 l
+struct DQ40B {
+    using F = FmtQ40Barq;
+    using XS = XStageQ80;
+    static constexpr int SLICE_BLOCKS = 128, SLICE_BYTES = 128 * Q4_0_BARQ_BYTES, SLICE_INSTR = 3;
+    static __device__ __forceinline__ uint32_t slice_src(int i) { return i < 160 ? 16u * (uint32_t)i : DMA_SKIP; }
+    static __device__ __forceinline__ void load_w(F::Wt& w, const uint8_t* sl, const F::Lane& c) {
+        uint32_t v[10];
+        lds_dwords<10>(sl + 40 * c.l, v);
+        w.sc[0] = __builtin_bit_cast(float, v[0]);
+        w.q[0] = make_uint4(v[1], v[2], v[3], v[4]);
+        w.sc[1] = __builtin_bit_cast(float, v[5]);
+        w.q[1] = make_uint4(v[6], v[7], v[8], v[9]);
+    }
+    static __device__ __forceinline__ void load_x(F::X& x, const uint8_t* xs, int it, const F::Lane& c, int nblk) {
+        const int b = it * 128 + 2 * c.l;
+        XQ80 r;
+        stage_x_q8_0(r, xs, b < nblk ? b : 0);
+        #pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint4 lo = r.v[2 * j], hi = r.v[2 * j + 1];
+            const uint32_t X8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            #pragma unroll
+            for (int t = 0; t < 4; t++) {
+                x.e[j][t] = __builtin_amdgcn_perm(X8[2 * t + 1], X8[2 * t], 0x06040200u);
+                x.o[j][t] = __builtin_amdgcn_perm(X8[2 * t + 1], X8[2 * t], 0x07050301u);
+            }
+            x.s[j] = r.s[j];
+            x.dx[j] = r.dx[j];
+        }
+    }
+};
+
+// W waves per workgroup, R rows per wave, D slices in flight per wave.
+template <class P, int W, int R, int D>
+__global__ __launch_bounds__(W * 64)
+void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t* __restrict__ xq, uint32_t x_bytes,
+                     float* __restrict__ y, int n_rows, int nblk, uint32_t x_region) {
+    using F = typename P::F;
+    constexpr int SI = P::SLICE_INSTR, SL = 1024 * SI;
+    static_assert(R % D == 0, "slice buffers rotate with the row index");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int l = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = (blockIdx.x * W + wave) * R;
+    const int n_it = (nblk + P::SLICE_BLOCKS - 1) / P::SLICE_BLOCKS;
+    uint8_t* xs = smem;
+    uint8_t* bufs = smem + x_region + wave * (D * SL);
+
+    // activation: every wave copies part of it
+    {
+        const i32x4v xr = make_rsrc4(xq, x_bytes);
+        const int n_instr = (P::XS::chunks(nblk) + 63) / 64;
+        for (int q = wave; q < n_instr; q += W) lds_load16(xr, xs + 1024 * q, P::XS::src(64 * q + l, nblk), 0);
+    }
+    const bool live = row0 < n_rows;
+    const int rows_here = live ? min(R, n_rows - row0) : 1;
+    const i32x4v wr = make_rsrc4(Wq + (size_t)(live ? row0 : 0) * rb, (uint32_t)rows_here * rb);
+    uint32_t voff[SI];
+    #pragma unroll
+    for (int q = 0; q < SI; q++) voff[q] = P::slice_src(64 * q + l);
+    // the whole offset goes in the per-lane operand, which the descriptor's
+    // range check covers: reads past this wave's rows return zeros
+    auto issue = [&](int u) {
+        const int it = u / R, r = u - it * R;
+        const uint32_t so = (uint32_t)r * rb + (uint32_t)it * P::SLICE_BYTES;
+        uint8_t* dst = bufs + (u % D) * SL;
+        #pragma unroll
+        for (int q = 0; q < SI; q++) lds_load16(wr, dst + 1024 * q, voff[q] == DMA_SKIP ? DMA_SKIP : voff[q] + so, 0);
+    };
+    const int U = n_it * R;   // >= R >= D
+    if (live) {
+        #pragma unroll
+        for (int u = 0; u < D; u++) issue(u);
+        wait_vmcnt<SI * (D - 1)>();   // this wave's activation part and first slice
+    } else {
+        wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (!live) return;   // after the barrier: the other waves needed this wave's activation part
+
+    const typename F::Lane c = F::lane(l);
+    float acc[R];
+    #pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int it = 0; it < n_it; it++) {
+        const bool act = F::active(it, c, nblk);
+        typename F::X x;
+        P::load_x(x, xs, it, c, nblk);
+        #pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int u = it * R + r;
+            if (u > 0) {
+                if (u + D - 1 < U) wait_vmcnt<SI * (D - 1)>();
+                else wait_vmcnt<0>();
+                asm volatile("" ::: "memory");
+            }
+            typename F::Wt w;
+            P::load_w(w, bufs + (r % D) * SL, c);
+            const float v = F::dot(w, x, c);
+            if (act) acc[r] += v;
+            // the slice buffer is reused for unit u + D once its values are in registers
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (u + D < U) issue(u + D);
+        }
+    }
+
+    #pragma unroll
+    for (int g = 0; g < R; g += 4) {
+        const float v = reduce4(acc[g], g + 1 < R ? acc[g + 1] : 0.0f, g + 2 < R ? acc[g + 2] : 0.0f,
+                                g + 3 < R ? acc[g + 3] : 0.0f);
+        if ((l & 15) == 0) {
+            const int rr = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+            if (rr < R && row0 + rr < n_rows) y[row0 + rr] = v;
+        }
+    }
+}
+
+// ---- launch ------------------------------------------------------------------
+static int dma_env(const char* name, int def) {
+    if (const char* e = getenv(name)) return atoi(e);
+    return def;
+}
+// tuning: W*100+R*10+D selects another launch shape (e.g. 842); -1 turns the path off
+static const int g_dma_cfg = dma_env("BARQ_GEMV_DMA", 0);
+
+template <class P, int W, int R, int D>
+static hipError_t launch_dma(const uint8_t* Wq, uint32_t rb, size_t n_rows, int nblk, const uint8_t* xq,
+                             uint32_t x_bytes, uint32_t x_region, float* y, hipStream_t s) {
+    const size_t lds = x_region + (size_t)W * D * 1024 * P::SLICE_INSTR;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    static size_t attr = 0;   // largest dynamic LDS size enabled so far for this instance
+    if (lds > attr) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_dma_kernel<P, W, R, D>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = lds;
+    }
+    const unsigned grid = (unsigned)((n_rows + (size_t)W * R - 1) / ((size_t)W * R));
+    hipLaunchKernelGGL((gemv_dma_kernel<P, W, R, D>), dim3(grid), dim3(W * 64), lds, s, Wq, rb, xq, x_bytes, y,
+                       (int)n_rows, nblk, x_region);
+    return hipGetLastError();
+}
+
+template <class P>
+static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const void* xq, float* y, hipStream_t s,
+                               int blk_bytes, int x_blk_bytes) {
+    const int nblk = (int)(k / (P::SLICE_BLOCKS == 16 ? 256 : 32));
+    const uint32_t rb = (uint32_t)(nblk * blk_bytes);
+    const int xnb = P::XS::BLK_ELEMS == 256 ? (int)(k / 256) : nblk;
+    const uint32_t x_bytes = (uint32_t)(xnb * x_blk_bytes);
+    const int xch = P::SLICE_BLOCKS == 16 ? xnb * 19 : (xnb * x_blk_bytes + 15) / 16;
+    const uint32_t x_region = (uint32_t)((xch + 63) / 64 * 1024);
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+#define BARQ_DMA_CASE(WW, RR, DD) \
+    case WW * 100 + RR * 10 + DD: return launch_dma<P, WW, RR, DD>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    switch (g_dma_cfg) {
+    BARQ_DMA_CASE(4, 2, 2) BARQ_DMA_CASE(4, 4, 4) BARQ_DMA_CASE(4, 8, 2) BARQ_DMA_CASE(8, 2, 2)
+    BARQ_DMA_CASE(8, 4, 2) BARQ_DMA_CASE(2, 2, 2) BARQ_DMA_CASE(2, 4, 2) BARQ_DMA_CASE(4, 1, 1)
+    BARQ_DMA_CASE(8, 1, 1)
+    default:
+        // measured on MI355X: four rows per wave for the 128256-row Q6_K head
+        // (C3), two for the 4096-row Q4_0 matrix (C1)
+        if constexpr (P::SLICE_BLOCKS == 16) return launch_dma<P, 4, 4, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+        else return launch_dma<P, 4, 2, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    }
+#undef BARQ_DMA_CASE
+}
+
+// Rows are streamed in 4096-element slices: weight rows and the activation
+// must be 4-byte aligned, a Q6_K row must hold an even number of blocks (so
+// block pairs start on 4-byte boundaries), the 32-element formats need whole
+// block pairs per lane, offsets within one wave's rows stay below 2 GiB and
+// the staged activation fits in LDS beside the slice buffers.
+bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq) {
+    if (g_dma_cfg < 0 || k == 0 || n_rows > (size_t)INT32_MAX) return false;
+    if (((uintptr_t)W & 3) || ((uintptr_t)xq & 3)) return false;
+    size_t rb = 0, xch = 0;
+    switch (w_type) {
+    case TYPE_Q6_K: if (k % 512) return false; rb = k / 256 * Q6_K_BYTES; xch = k / 256 * 19; break;
+    case TYPE_Q4_K: if (k % 256) return false; rb = k / 256 * Q4_K_BYTES; xch = k / 256 * 19; break;
+    case TYPE_Q4_0: if (k % 64) return false; rb = k / 32 * Q4_0_BYTES; xch = (k / 32 * Q8_0_BYTES + 15) / 16; break;
+    case TYPE_Q8_0: if (k % 64) return false; rb = k / 32 * Q8_0_BYTES; xch = (k / 32 * Q8_0_BYTES + 15) / 16; break;
+    case TYPE_Q4_0_BARQ: if (k % 64) return false; rb = k / 32 * Q4_0_BARQ_BYTES; xch = (k / 32 * Q8_0_BYTES + 15) / 16; break;
+    default: return false;
+    }
+    return rb * 8 < (1ull << 31) && (xch + 63) / 64 * 1024 <= 96 * 1024;
+}
+
+hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, float* y,
+                           hipStream_t s) {
+    if (n_rows == 0) return hipSuccess;
+    switch (w_type) {
+    case TYPE_Q6_K: return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES);
+    case TYPE_Q4_K: return dispatch_dma<DQ4K>(W, n_rows, k, xq, y, s, Q4_K_BYTES, Q8_K_BYTES);
+    case TYPE_Q4_0: return dispatch_dma<DQ40>(W, n_rows, k, xq, y, s, Q4_0_BYTES, Q8_0_BYTES);
+    case TYPE_Q8_0: return dispatch_dma<DQ80>(W, n_rows, k, xq, y, s, Q8_0_BYTES, Q8_0_BYTES);
+    case TYPE_Q4_0_BARQ: return dispatch_dma<DQ40B>(W, n_rows, k, xq, y, s, Q4_0_BARQ_BYTES, Q8_0_BYTES);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace barq

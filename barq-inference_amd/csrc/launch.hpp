@@ -30,6 +30,11 @@ hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, c
                            float* y, hipStream_t s);
 void gemv_set_config(int rows_per_wave, int waves);
 
+// gemv_dma.hip: the same GEMV streaming row slices through LDS
+bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq);
+hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, float* y,
+                           hipStream_t s);
+
 // gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows)
 hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k,
                                 const void* xq, size_t m, float* y, hipStream_t s);

@@ -54,42 +54,80 @@ hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, 
     return hipGetLastError();
 }
 
-// batch_by_expert (moe_fused.rs:196-223): one wave builds the CSR grouping.
-// Tokens are visited in ascending order and each token's ids in routing
+// batch_by_expert (moe_fused.rs:196-223): one workgroup builds the CSR
+// grouping.  Assignments are visited in ascending (token, routing slot)
 // order; ids outside [0, n_experts) are skipped (batches.get_mut -> None).
+// Each assignment's place inside its expert is its rank among the earlier
+// assignments of that expert, so the fill is parallel and deterministic.
 // rowpos[t*k+i] is the grouped row of assignment (t, i), or -1.
-__global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict__ ids,
-                                                       const float* __restrict__ weights, int rows, int k,
-                                                       int ne, int32_t* __restrict__ offsets,
-                                                       int32_t* __restrict__ tokens, float* __restrict__ wts,
-                                                       int32_t* __restrict__ rowpos) {
+constexpr int MOE_GROUP_THREADS = 256;
+
+__global__ __launch_bounds__(MOE_GROUP_THREADS) void moe_group_kernel(const int32_t* __restrict__ ids,
+                                                                      const float* __restrict__ weights, int rows,
+                                                                      int k, int ne, int32_t* __restrict__ offsets,
+                                                                      int32_t* __restrict__ tokens,
+                                                                      float* __restrict__ wts,
+                                                                      int32_t* __restrict__ rowpos) {
     __shared__ int cnt[MOE_MAX_EXPERTS + 1];
-    const int lane = threadIdx.x;
-    for (int e = lane; e <= ne; e += 64) cnt[e] = 0;
+    __shared__ int cid[MOE_GROUP_THREADS];
+    const int tid = threadIdx.x;
+    for (int e = tid; e <= ne; e += MOE_GROUP_THREADS) cnt[e] = 0;
     __syncthreads();
     const int n = rows * k;
-    for (int a = lane; a < n; a += 64) {
+    for (int a = tid; a < n; a += MOE_GROUP_THREADS) {
         const int e = ids[a];
         if (e >= 0 && e < ne) atomicAdd(&cnt[e + 1], 1);
     }
     __syncthreads();
-    if (lane == 0) {
-        for (int e = 0; e < ne; e++) cnt[e + 1] += cnt[e];
-        for (int e = 0; e <= ne; e++) offsets[e] = cnt[e];
-        // fill in ascending (token, routing slot) order: deterministic
-        for (int a = 0; a < n; a++) {
-            const int e = ids[a];
-            if (e < 0 || e >= ne) { rowpos[a] = -1; continue; }
-            const int pos = cnt[e]++;
-            tokens[pos] = a / k;
-            wts[pos] = weights[a];
-            rowpos[a] = pos;
+    // cnt[e] <- first row of expert e: one wave scans four entries per lane
+    if (tid < 64) {
+        int v[4], run = 0;
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = 4 * tid + i + 1;
+            v[i] = idx <= ne ? cnt[idx] : 0;
+            run += v[i];
+        }
+        int inc = run;
+        #pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(inc, o);
+            if (tid >= o) inc += t;
+        }
+        int p = inc - run;
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = 4 * tid + i + 1;
+            p += v[i];
+            if (idx <= ne) cnt[idx] = p;
         }
     }
     __syncthreads();
+    for (int e = tid; e <= ne; e += MOE_GROUP_THREADS) offsets[e] = cnt[e];
+    const int total = cnt[ne];
+    for (int c0 = 0; c0 < n; c0 += MOE_GROUP_THREADS) {
+        const int a = c0 + tid;
+        int e = a < n ? ids[a] : -1;
+        if (e >= ne) e = -1;
+        cid[tid] = e < 0 ? -1 : e;
+        __syncthreads();
+        if (e >= 0) {
+            int r = 0;
+            for (int j = 0; j < tid; j++) r += cid[j] == e;
+            const int pos = cnt[e] + r;
+            tokens[pos] = a / k;
+            wts[pos] = weights[a];
+            rowpos[a] = pos;
+        } else if (a < n) {
+            rowpos[a] = -1;
+        }
+        __syncthreads();
+        if (e >= 0) atomicAdd(&cnt[e], 1);
+        __syncthreads();
+    }
     // rows past the last assignment (skipped ids) point at token 0, so that
     // consumers may process all rows * k rows without knowing the count
-    for (int p = cnt[ne] + lane; p < n; p += 64) {
+    for (int p = total + tid; p < n; p += MOE_GROUP_THREADS) {
         tokens[p] = 0;
         wts[p] = 0.0f;
     }
@@ -98,7 +136,7 @@ __global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict
 hipError_t moe_group_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
                             size_t n_experts, int32_t* offsets, int32_t* tokens, float* wts,
                             int32_t* rowpos, hipStream_t s) {
-    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64), 0, s, ids, weights, (int)rows, (int)top_k,
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(MOE_GROUP_THREADS), 0, s, ids, weights, (int)rows, (int)top_k,
                        (int)n_experts, offsets, tokens, wts, rowpos);
     return hipGetLastError();
 }

@@ -115,7 +115,7 @@ def test_quantize_q4_0_barq_bit_exact(be, orc):
 # ---- matvec ----------------------------------------------------------------
 
 SHAPES_K = [(1, 256), (5, 512), (67, 4096), (33, 4352), (129, 14336), (1023, 768)]
-SHAPES_32 = [(1, 32), (7, 96), (67, 4096), (33, 4128), (130, 4064)]
+SHAPES_32 = [(1, 32), (7, 96), (5, 64), (67, 4096), (33, 4128), (70, 4160), (130, 4064), (33, 14336)]
 
 
 def shapes_for(t):
