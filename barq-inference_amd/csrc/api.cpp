@@ -547,6 +547,9 @@ struct MoeArena {
     size_t off, tok, wts, pos, xg, g, u, yg, q, wf, end;
 };
 
+// K slices of the grouped down projection (each writes a partial product)
+constexpr size_t MOE_DOWN_KS = 2;
+
 MoeArena moe_arena(size_t base, size_t ne, size_t hidden, size_t n_ff, size_t na, bool q8) {
     Arena a;
     a.used = base;
@@ -559,7 +562,7 @@ MoeArena moe_arena(size_t base, size_t ne, size_t hidden, size_t n_ff, size_t na
     // gate and up results are adjacent (one grouped launch writes both)
     m.g = a.add(2 * na * n_ff * 4);
     m.u = m.g + na * n_ff * 4;
-    m.yg = a.add(na * hidden * 4);
+    m.yg = a.add(MOE_DOWN_KS * na * hidden * 4);   // room for the K-slice partials of the down projection
     const size_t qrow = (hidden > n_ff ? hidden : n_ff) / 256 * 292;
     m.q = a.add(q8 ? na * qrow : 0);
     // the literal path dequantizes one expert matrix at a time
@@ -604,21 +607,28 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
                 wp.assign(gate + e0, gate + e0 + c);
                 wp.insert(wp.end(), up + e0, up + e0 + c);
                 BARQ_CHECK(launched(barq::kq_grouped_launch(gt, wp.data(), c, 2, offsets + e0, na, n_ff, hidden, qb, gb,
-                                                            na * n_ff, s), "moe gate/up"));
+                                                            na * n_ff, 1, 0, s), "moe gate/up"));
             } else {
                 BARQ_CHECK(launched(barq::kq_grouped_launch(gt, gate + e0, c, 1, offsets + e0, na, n_ff, hidden, qb, gb,
-                                                            0, s), "moe gate"));
+                                                            0, 1, 0, s), "moe gate"));
                 BARQ_CHECK(launched(barq::kq_grouped_launch(ut, up + e0, c, 1, offsets + e0, na, n_ff, hidden, qb, ub,
-                                                            0, s), "moe up"));
+                                                            0, 1, 0, s), "moe up"));
             }
         }
         BARQ_CHECK(launched(barq::swiglu_q8_k_launch(gb, ub, na, n_ff, qb, s), "swiglu"));
+        // the down projection has only hidden / 128 column tiles per expert:
+        // two K slices give every CU two workgroups; the scatter adds them
+        // (at most MOE_DOWN_KS partials: the arena holds that many)
+        const int ovr = barq::kq_k_slices_override();
+        size_t ks = ovr > 0 ? (size_t)ovr : ((n_ff / 256) % 4 == 0 && hidden / 128 * ne < 512 ? 2 : 1);
+        if (ks > MOE_DOWN_KS || (n_ff / 256) % (2 * ks) != 0) ks = 1;
         for (size_t e0 = 0; e0 < ne; e0 += 64) {
             const size_t c = ne - e0 < 64 ? ne - e0 : 64;
-            BARQ_CHECK(launched(barq::kq_grouped_launch(dt, down + e0, c, 1, offsets + e0, na, hidden, n_ff, qb, yg, 0, s),
-                                "moe down"));
+            BARQ_CHECK(launched(barq::kq_grouped_launch(dt, down + e0, c, 1, offsets + e0, na, hidden, n_ff, qb, yg, 0, ks,
+                                                        na * hidden, s), "moe down"));
         }
-        return launched(barq::moe_scatter_launch(yg, ids, weights, rowpos, rows, k, hidden, out, s), "moe_scatter");
+        return launched(barq::moe_scatter_launch(yg, ids, weights, rowpos, rows, k, hidden, out, s, (int)ks,
+                                                 na * hidden), "moe_scatter");
     }
     std::vector<int32_t> off(ne + 1);
     BARQ_HIP(hipMemcpyAsync(off.data(), offsets, (ne + 1) * 4, hipMemcpyDeviceToHost, s));

@@ -65,7 +65,8 @@ struct KQL {
     static constexpr int X_INSTR = (X_INSTR_ALL + NW - 1) / NW;
     static constexpr int W_INSTR = (W_INSTR_ALL + NW - 1) / NW;
     static constexpr int LOADS_MIN = X_INSTR_ALL / NW + W_INSTR_ALL / NW;
-    static constexpr int MTW = BM / 32 / (NW / 4);              // 32x32 MFMA tiles per wave
+    // 32x32 MFMA row tiles per wave; 16-row tiles use the 16x16 path (two column blocks per wave)
+    static constexpr int MTW = BM >= 32 ? BM / 32 / (NW / 4) : 1;
     static_assert(KQ_BN * F::PIECES % 64 == 0, "weight tile is whole load instructions");
 };
 
@@ -279,6 +280,131 @@ __device__ __forceinline__ void kq6_compute(const uint8_t* wrow, const uint8_t* 
         }
 }
 
+// ---- 16-row tiles (v_mfma_i32_16x16x64_i8) ------------------------------------
+// For expert groups of a few tokens: a wave covers 16 rows x 32 columns as two
+// 16x16 column blocks.  16x16x64 layout: lane (row/column l % 16, k group
+// g4 = l / 16: k = 16 g4 .. 16 g4 + 15 of each 64); C: rows 4 g4 + r, column
+// l % 16.  A lane's 16 k-values lie in one Q4_K sub-block (32) or one Q6_K
+// sub-block (16), so the scales still fold into its B operand.
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void kq16_dx(const uint8_t* xd, int g4, float (&dx)[4]) {
+    const float4 v = *reinterpret_cast<const float4*>(xd + 16 * g4);
+    dx[0] = v.x; dx[1] = v.y; dx[2] = v.z; dx[3] = v.w;
+}
+
+// acc[0][4 cb + r]: column block cb, row 4 g4 + r
+__device__ __forceinline__ void kq4_compute16(const uint8_t* st, int wave, int l, float (&acc)[1][16]) {
+    using L = KQL<KQ4, 16, 4>;
+    const int n = l & 15, g4 = l >> 4;
+    const uint8_t* xrow = st + L::XQ + n * KQ4::XRS + 16 * g4;
+    // A fragments for the four k-steps and the bsums (mins)
+    v4i a[4];
+    #pragma unroll
+    for (int t = 0; t < 4; t++) a[t] = *reinterpret_cast<const v4i*>(xrow + 64 * t);
+    h8v amin;
+    {
+        const uint4 bs = *reinterpret_cast<const uint4*>(st + L::XQ + n * KQ4::XRS + 256 + 16 * (g4 & 1));
+        amin = i16x8_to_h8(bs);
+        if (g4 >= 2) amin = h8v{};
+    }
+    float dx[4];
+    kq16_dx(st + L::XD, g4, dx);
+    #pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+        const uint8_t* wrow = st + L::W + (32 * wave + 16 * cb + n) * KQ4::RS;
+        const uint4 hdr = *reinterpret_cast<const uint4*>(wrow);
+        const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
+        const uint32_t scA = hdr.y & 0x3F3F3F3Fu;
+        const uint32_t scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+        const uint32_t mA = hdr.z & 0x3F3F3F3Fu;
+        const uint32_t mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+        // mins: k = bsum index for g4 < 2 (sub-block k / 2), zero above
+        h8v bmin = {};
+        if (g4 < 2) {
+            const uint32_t mm = g4 ? mB : mA;
+            #pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const _Float16 m = (_Float16)(float)((mm >> (8 * q)) & 0xFFu);
+                bmin[2 * q] = m;
+                bmin[2 * q + 1] = m;
+            }
+        }
+        const f32x4 zf = {};
+        const f32x4 cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(amin, bmin, zf, 0, 0, 0);
+        v4i ch = {}, cl = {};
+        #pragma unroll
+        for (int t = 0; t < 4; t++) {
+            // k-step t: sub-block j = 2t + g4 / 2 from qs[32t + 16 (g4 & 1) ..], nibble g4 / 2
+            const uint4 qs = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * t + 16 * (g4 & 1));
+            const int hsh = 4 * (g4 >> 1);
+            const uint32_t bsel = (uint32_t)(2 * t + (g4 >> 1)) & 3u;
+            const uint32_t scw = t < 2 ? scA : scB;
+            const uint32_t s1 = __builtin_amdgcn_perm(0u, (scw >> 3) & 0x07070707u, 0x0c000c00u | (bsel << 16) | bsel);
+            const uint32_t s0 = __builtin_amdgcn_perm(0u, scw & 0x07070707u, 0x0c000c00u | (bsel << 16) | bsel);
+            const uint32_t n0 = (qs.x >> hsh) & 0x0F0F0F0Fu, n1 = (qs.y >> hsh) & 0x0F0F0F0Fu;
+            const uint32_t n2 = (qs.z >> hsh) & 0x0F0F0F0Fu, n3 = (qs.w >> hsh) & 0x0F0F0F0Fu;
+            const v4i bh = {(int)mul_u16x2(n0, s1), (int)mul_u16x2(n1, s1), (int)mul_u16x2(n2, s1), (int)mul_u16x2(n3, s1)};
+            const v4i bl = {(int)mul_u16x2(n0, s0), (int)mul_u16x2(n1, s0), (int)mul_u16x2(n2, s0), (int)mul_u16x2(n3, s0)};
+            ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bh, ch, 0, 0, 0);
+            cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bl, cl, 0, 0, 0);
+        }
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int c = (ch[r] << 3) + cl[r];
+            const float v = __builtin_fmaf(-dmin, cm[r], d * (float)c);
+            acc[0][4 * cb + r] = __builtin_fmaf(dx[r], v, acc[0][4 * cb + r]);
+        }
+    }
+}
+
+__device__ __forceinline__ void kq6_compute16(const uint8_t* st, int wave, int l, int b, float (&acc)[1][16]) {
+    using L = KQL<KQ6, 16, 4>;
+    const int n = l & 15, g4 = l >> 4;
+    const uint8_t* xrow = st + L::XQ + n * KQ6::XRS + 16 * g4;
+    v4i a[4];
+    #pragma unroll
+    for (int t = 0; t < 4; t++) a[t] = *reinterpret_cast<const v4i*>(xrow + 64 * t);
+    float dx[4];
+    kq16_dx(st + L::XD, g4, dx);
+    const uint32_t sh = 2u * (uint32_t)(b & 1);
+    #pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+        const uint8_t* wrow = st + L::W + (32 * wave + 16 * cb + n) * KQ6::RS;
+        const uint32_t dw = *reinterpret_cast<const uint32_t*>(wrow + 208);
+        const float d = f16_bits_to_f32(sh ? dw >> 16 : dw & 0xFFFFu);
+        v4i ch = {}, cl = {};
+        #pragma unroll
+        for (int t = 0; t < 4; t++) {
+            // element 64t + 16 g4 + i = 128 half + 32 qd + l: half = t / 2,
+            // qd = 2 (t & 1) + g4 / 2, l = 16 (g4 & 1) + i
+            const int half = t >> 1, qd = 2 * (t & 1) + (g4 >> 1);
+            const uint4 ql = lds16_sh(wrow + 64 * half + 32 * (g4 >> 1) + 16 * (g4 & 1), sh);
+            const uint4 qh = lds16_sh(wrow + 128 + 32 * half + 16 * (g4 & 1), sh);
+            const int sc = (int)(int8_t)wrow[sh + 192 + 8 * half + (g4 & 1) + 2 * qd];
+            const uint32_t scv = ((uint32_t)sc & 0xFFFFu) * 0x00010001u;
+            const uint32_t off = ((uint32_t)(-32 * sc) & 0xFFFFu) * 0x00010001u;
+            const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w}, qhw[4] = {qh.x, qh.y, qh.z, qh.w};
+            const int lsh = 4 * (t & 1), hsh = 2 * qd;
+            int hv[4], lv[4];
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t q4 = ((qlw[i] >> lsh) & 0x0F0F0F0Fu) | (((qhw[i] >> hsh) & 0x03030303u) << 4);
+                q6_split4(q4, scv, off, hv[i], lv[i]);
+            }
+            const v4i bh = {hv[0], hv[1], hv[2], hv[3]}, bl = {lv[0], lv[1], lv[2], lv[3]};
+            ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bh, ch, 0, 0, 0);
+            cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], bl, cl, 0, 0, 0);
+        }
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int c = (ch[r] << 7) + cl[r];
+            acc[0][4 * cb + r] = __builtin_fmaf(dx[r], d * (float)c, acc[0][4 * cb + r]);
+        }
+    }
+}
+
 // ---- pipeline ----------------------------------------------------------------
 // One step: super-block b computed from stage S (= b % NS) while the loads of
 // b+NS-1 go to stage (S-1) % NS.  Each stage is its own LDS array; the raw
@@ -301,6 +427,11 @@ __device__ __forceinline__ void kq_step(uint8_t* const (&stages)[KQ_MAX_NS], int
     asm volatile("" ::: "memory");
     if (b + NS - 1 < nsb) kq_issue<F, BM, NW>(stages[(S + NS - 1) % NS], xr, wr, off, b + NS - 1, wave);
     const uint8_t* st = stages[S];
+    if constexpr (BM == 16) {
+        if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute16(st, wave, l, acc);
+        else kq6_compute16(st, wave, l, b, acc);
+        return;
+    }
     const int n = l & 31, g2 = l >> 5;
     const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
     const uint8_t* wrow = st + L::W + (32 * slice + n) * F::RS;
@@ -323,11 +454,13 @@ __device__ __forceinline__ void kq_round(std::integer_sequence<int, S...>, uint8
 template <class F, int BM, int NS, int NW>
 __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], const uint8_t* W, uint32_t wrb, const uint8_t* X,
                                         uint32_t xrb, float* Y, int count, int N, int nsb, int m0, int n0, int wave,
-                                        int l) {
+                                        int l, int kb0 = 0) {
     using L = KQL<F, BM, NW>;
     constexpr int MT = L::MTW;
-    const i32x4v xr = make_rsrc4(X + (size_t)m0 * xrb, (uint32_t)((size_t)(count - m0) * xrb));
-    const i32x4v wr = make_rsrc4(W + (size_t)n0 * wrb, (uint32_t)((size_t)(N - n0) * wrb));
+    // super-blocks [kb0, kb0 + nsb) of each row (kb0 even: Q6_K windows keep their parity)
+    const uint32_t xk = (uint32_t)kb0 * Q8_K_BYTES, wk = (uint32_t)kb0 * F::BB;
+    const i32x4v xr = make_rsrc4(X + (size_t)m0 * xrb + xk, (uint32_t)((size_t)(count - m0) * xrb) - xk);
+    const i32x4v wr = make_rsrc4(W + (size_t)n0 * wrb + wk, (uint32_t)((size_t)(N - n0) * wrb) - wk);
 
     float acc[MT][16];
     #pragma unroll
@@ -343,6 +476,20 @@ __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], con
     for (int b = 0; b < nsb; b += NS)
         kq_round<F, BM, NW, NS>(std::make_integer_sequence<int, NS>{}, stages, b, nsb, xr, wr, off, wave, l, acc);
 
+    if constexpr (BM == 16) {
+        #pragma unroll
+        for (int cb = 0; cb < 2; cb++) {
+            const int col = n0 + 32 * wave + 16 * cb + (l & 15);
+            if (col < N) {
+                #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = m0 + 4 * (l >> 4) + r;
+                    if (row < count) Y[(size_t)row * N + col] = acc[0][4 * cb + r];
+                }
+            }
+        }
+        return;
+    }
     const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
     if (col < N) {
         #pragma unroll
@@ -366,8 +513,8 @@ template <class F, int BM, int NS, int NW, bool GROUPED>
 __global__ __launch_bounds__(64 * NW, 1)
 void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb, float* __restrict__ Y, int M,
                int N, int nsb, int tiles_m, int tiles_n, const int32_t* __restrict__ offsets, int ne, int nmat,
-               size_t ymat, int xcd_order) {
-    static_assert(NS >= 3 && NS <= KQ_MAX_NS, "stage count");
+               size_t ymat, int ks, size_t ykstride, int xcd_order) {
+    static_assert(NS >= 2 && NS <= KQ_MAX_NS, "stage count");
     using L = KQL<F, BM, NW>;
     // one array per stage (stages beyond NS are unused 16-byte stubs)
     __shared__ __align__(16) uint8_t st0[L::STAGE];
@@ -402,9 +549,10 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
             if (l >= o) inc += v;
         }
         const int s_total = __builtin_amdgcn_readfirstlane(__shfl(inc, 63));
-        const int total = s_total * nmat * tiles_n;
+        const int total = s_total * nmat * ks * tiles_n;
+        const int nsb_k = nsb / ks;
         for (int t = blockIdx.x; t < total; t += gridDim.x) {
-            const int ntile = t % tiles_n, r = t / tiles_n, mat = r % nmat, s = r / nmat;
+            const int ntile = t % tiles_n, rk = t / tiles_n, ksl = rk % ks, r = rk / ks, mat = r % nmat, s = r / nmat;
             // expert of m-slot s: the number of experts whose tiles all lie before it
             const int e = __builtin_amdgcn_readfirstlane(__popcll(__ballot(inc <= s)));
             const int mt = s - __builtin_amdgcn_readfirstlane(__shfl(inc - nt, e));
@@ -413,8 +561,8 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
             // the previous tile's last stages have been read by every wave
             if (t != (int)blockIdx.x) __builtin_amdgcn_s_barrier();
             kq_tile<F, BM, NS, NW>(stages, wt.w[mat * ne + e], wrb, X + (size_t)row0 * xrb, xrb,
-                                   Y + (size_t)mat * ymat + (size_t)row0 * N, count, N, nsb, mt * BM, ntile * KQ_BN,
-                                   wave, l);
+                                   Y + (size_t)mat * ymat + (size_t)ksl * ykstride + (size_t)row0 * N, count, N, nsb_k,
+                                   mt * BM, ntile * KQ_BN, wave, l, ksl * nsb_k);
         }
     }
 }
@@ -449,6 +597,8 @@ struct KQArgs {
     int ne, nmat;        // grouped: experts per weight set, weight sets
     size_t total_rows;   // grouped: rows over all experts
     size_t ymat;
+    int ks;              // grouped: K slices, each writing its partial product
+    size_t ykstride;
 };
 
 template <class F, int BM, int NS, int NW, bool GROUPED>
@@ -459,18 +609,20 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     if constexpr (GROUPED) {
         // m-tiles over all experts: sum of ceil(c_e / BM) <= (total + ne (BM - 1)) / BM
         const size_t slots = (a.total_rows + (size_t)a.ne * (BM - 1)) / BM;
-        const size_t tiles = slots * (size_t)a.nmat * (size_t)tiles_n;
+        const size_t tiles = slots * (size_t)a.nmat * (size_t)a.ks * (size_t)tiles_n;
         const size_t per_cu = 163840 / (NS * (size_t)KQL<F, BM, NW>::STAGE);
         const size_t cap = (size_t)cu_count() * (per_cu ? per_cu : 1);
         grid = (unsigned)(tiles < cap ? tiles : cap);
         tiles_m = 0;
     }
     hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, GROUPED>), dim3(grid), dim3(64 * NW), 0, s, a.wt, a.wrb, a.X, a.xrb,
-                       a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, g_kq_xcd);
+                       a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, a.ks, a.ykstride,
+                       g_kq_xcd);
     return hipGetLastError();
 }
 
 static const int g_kq_ns = kq_env("BARQ_GEMM_NS", 0);   // stage-count override for tuning
+static const int g_kq_ks = kq_env("BARQ_GEMM_KS", 0);   // K-slice override for grouped launches (tuning)
 
 // rows: M (ungrouped) or the expected rows per expert (grouped).  Stage
 // counts are the most that fit the 160 KiB of LDS (deeper pipelines keep
@@ -480,14 +632,24 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // measured on MI355X: 64x128 tiles with eight waves (two per SIMD) above
     // 32 rows, 32-row tiles with four waves for small expert groups
     const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 65 : 32);
+    if (bm == 16) {
+        if (g_kq_ns == 2) return kq_launch_t<F, 16, 2, 4, GROUPED>(a, s);
+        if (g_kq_ns == 4) return kq_launch_t<F, 16, 4, 4, GROUPED>(a, s);
+        return kq_launch_t<F, 16, 3, 4, GROUPED>(a, s);
+    }
+    // 32-row tiles: two stages per workgroup and two workgroups per CU for
+    // expert groups (measured best for C5), the deepest pipeline otherwise
+    const int ns = g_kq_ns ? g_kq_ns : (GROUPED ? 2 : 0);
     if constexpr (F::TYPE == TYPE_Q4_K) {
         if (bm == 65) return kq_launch_t<F, 64, 4, 8, GROUPED>(a, s);
-        if (g_kq_ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
-        if (g_kq_ns == 4) return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);
+        if (ns == 2) return kq_launch_t<F, 32, 2, 4, GROUPED>(a, s);
+        if (ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+        if (ns == 4) return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);
         return kq_launch_t<F, 32, 5, 4, GROUPED>(a, s);
     } else {
         if (bm == 65) return kq_launch_t<F, 64, 3, 8, GROUPED>(a, s);
-        if (g_kq_ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
+        if (ns == 2) return kq_launch_t<F, 32, 2, 4, GROUPED>(a, s);
+        if (ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
         return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);
     }
 }
@@ -495,6 +657,8 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
 // Raw buffer loads use 32-bit offsets: each weight matrix and the activation
 // rows must stay below 2 GiB.  Q6_K needs row bytes that are a multiple of 4
 // (an even number of super-blocks).
+int kq_k_slices_override() { return g_kq_ks; }
+
 bool kq_supported(int w_type, size_t n_rows, size_t k, size_t m) {
     if ((w_type != TYPE_Q4_K && w_type != TYPE_Q6_K) || k % 256 != 0 || k == 0 || n_rows == 0) return false;
     const size_t nsb = k / 256;
@@ -512,7 +676,7 @@ static KQArgs kq_args(int w_type, size_t n_rows, size_t k, const void* xq, float
     a.X = static_cast<const uint8_t*>(xq);
     a.Y = y;
     a.N = (int)n_rows;
-    a.ne = a.nmat = 1;
+    a.ne = a.nmat = a.ks = 1;
     return a;
 }
 
@@ -528,10 +692,10 @@ hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, co
 
 hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
                              size_t total_rows, size_t n_rows, size_t k, const void* xq, float* y, size_t y_mat_stride,
-                             hipStream_t s) {
+                             size_t k_slices, size_t y_k_stride, hipStream_t s) {
     if (n_experts == 0 || n_mats == 0 || total_rows == 0 || n_rows == 0) return hipSuccess;
     if (n_experts * n_mats > (size_t)KQ_MAXE || n_experts > 64 || !kq_supported(w_type, n_rows, k, total_rows) ||
-        total_rows > (size_t)INT32_MAX)
+        total_rows > (size_t)INT32_MAX || k_slices == 0 || (k_slices > 1 && (k / 256) % (2 * k_slices) != 0))
         return hipErrorInvalidValue;
     KQArgs a = kq_args(w_type, n_rows, k, xq, y);
     for (size_t i = 0; i < n_experts * n_mats; i++) a.wt.w[i] = static_cast<const uint8_t*>(W[i]);
@@ -540,6 +704,8 @@ hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts,
     a.nmat = (int)n_mats;
     a.total_rows = total_rows;
     a.ymat = y_mat_stride;
+    a.ks = (int)k_slices;
+    a.ykstride = y_k_stride;
     const size_t per_expert = (total_rows + n_experts - 1) / n_experts;
     return w_type == TYPE_Q4_K ? kq_dispatch<KQ4, true>(a, per_expert, s) : kq_dispatch<KQ6, true>(a, per_expert, s);
 }

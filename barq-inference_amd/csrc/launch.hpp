@@ -48,9 +48,12 @@ hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, co
 // Expert-grouped form: rows [offsets[e], offsets[e+1]) of xq, and of
 // y + mat * y_mat_stride, use weights W[mat * n_experts + e] (offsets on the
 // device; n_experts * n_mats <= 64).  total_rows bounds offsets[n_experts].
+// With k_slices > 1 slice i covers super-blocks [i, i + 1) * nsb / k_slices
+// and writes its partial product to y + i * y_k_stride (nsb / k_slices even).
 hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
                              size_t total_rows, size_t n_rows, size_t k, const void* xq, float* y, size_t y_mat_stride,
-                             hipStream_t s);
+                             size_t k_slices, size_t y_k_stride, hipStream_t s);
+int kq_k_slices_override();
 
 // f32blas.hip
 hipError_t gemm_f32_launch(const float* a, const float* b, size_t m, size_t k, size_t n, float* c,
@@ -76,8 +79,9 @@ hipError_t moe_gather_launch(const float* x, const int32_t* tokens, size_t n_ass
 hipError_t swiglu_launch(const float* g, const float* u, size_t n, float* h, hipStream_t s);
 // out[t] = sum over t's assignments in ascending expert id of w * yg[row]
 // rowpos[t*top_k+i] is the grouped row of assignment (t, i) or -1
+// yg holds `parts` partial results yg + i * part_stride that are summed first
 hipError_t moe_scatter_launch(const float* yg, const int32_t* ids, const float* weights,
                               const int32_t* rowpos, size_t rows, size_t top_k, size_t hidden,
-                              float* out, hipStream_t s);
+                              float* out, hipStream_t s, int parts = 1, size_t part_stride = 0);
 
 }  // namespace barq

@@ -187,7 +187,8 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restric
                                                           const int32_t* __restrict__ ids,
                                                           const float* __restrict__ weights,
                                                           const int32_t* __restrict__ rowpos, int k,
-                                                          int hidden, float* __restrict__ out) {
+                                                          int hidden, float* __restrict__ out, int parts,
+                                                          size_t part_stride) {
     const int t = blockIdx.y;
     const int32_t* tid = ids + (size_t)t * k;
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < hidden; c += gridDim.x * blockDim.x) {
@@ -203,7 +204,10 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restric
                 if (after && (e < be || (e == be && i < bi))) { be = e; bi = i; }
             }
             if (bi < 0) break;
-            const float p = yg[(size_t)rowpos[(size_t)t * k + bi] * hidden + c] * weights[(size_t)t * k + bi];
+            const size_t at = (size_t)rowpos[(size_t)t * k + bi] * hidden + c;
+            float yv = yg[at];
+            for (int q = 1; q < parts; q++) yv += yg[at + q * part_stride];
+            const float p = yv * weights[(size_t)t * k + bi];
             acc = acc + p;
             last_e = be; last_i = bi;
         }
@@ -213,11 +217,11 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restric
 
 hipError_t moe_scatter_launch(const float* yg, const int32_t* ids, const float* weights,
                               const int32_t* rowpos, size_t rows, size_t top_k, size_t hidden,
-                              float* out, hipStream_t s) {
+                              float* out, hipStream_t s, int parts, size_t part_stride) {
     if (rows == 0) return hipSuccess;
     const unsigned gx = (unsigned)((hidden + 255) / 256 < 64 ? (hidden + 255) / 256 : 64);
     hipLaunchKernelGGL(moe_scatter_kernel, dim3(gx, (unsigned)rows), dim3(256), 0, s, yg, ids, weights,
-                       rowpos, (int)top_k, (int)hidden, out);
+                       rowpos, (int)top_k, (int)hidden, out, parts, part_stride);
     return hipGetLastError();
 }
 

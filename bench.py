@@ -92,8 +92,9 @@ def time_launches(launch, K, eager):
     return t0.elapsed_time(t1) / K, "eager"
 
 
-KERNEL_OF_CONFIG = {1: "gemv_q8_kernel<barq::FmtQ40", 2: "gemv_q8_kernel<barq::FmtQ4K",
-                    3: "gemv_q8_kernel<barq::FmtQ6K", 4: "gemm_kq_kernel<barq::GQ4K"}
+# dominant kernel of each config (config 5: every kernel of the MoE step)
+KERNEL_OF_CONFIG = {1: "gemv_dma_kernel<barq::DQ40", 2: "gemv_q8_kernel<barq::FmtQ4K",
+                    3: "gemv_dma_kernel<barq::DQ6K", 4: "kq_kernel<barq::KQ4, 64", 5: "barq::"}
 
 
 def measure_traffic(config):
@@ -125,8 +126,17 @@ def measure_traffic(config):
         if r.returncode != 0 and not files:
             return None, f"{counter} run failed: {r.stderr.decode(errors='replace')[-300:]}"
         rows = [row for f in files for row in csv.DictReader(open(f))]
-        kern = [float(row["Counter_Value"]) for row in rows if name in row["Kernel_Name"]]
         copies = [float(row["Counter_Value"]) for row in rows if "copyBuffer" in row["Kernel_Name"]][-5:]
+        if config == 5:
+            # per step: the median of every kernel of the step, summed
+            by = {}
+            for row in rows:
+                kn = row["Kernel_Name"]
+                if name in kn and "moe_route" not in kn:
+                    by.setdefault(kn.split("(")[0], []).append(float(row["Counter_Value"]))
+            kern = [sum(st.median(v) for v in by.values())] if by else []
+        else:
+            kern = [float(row["Counter_Value"]) for row in rows if name in row["Kernel_Name"]]
         if not kern or len(copies) < 5:
             return None, f"{counter}: kernel or copy-probe dispatches missing"
         vals[counter] = (st.median(kern), 262144.0 / st.median(copies))
@@ -276,8 +286,20 @@ def bench_moe(args):
         "config": {"workload": c["name"], "experts_used": len(used), "tokens_per_expert": counts, "timing": "eager"},
         "us_per_step": round(ms * 1e3, 2), "parity_rel_err_4_tokens": rel,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
+                     "scope": "the whole step (grouping, quantizers, grouped GEMMs, scatter)"},
     }
+    if args.probe_copy:
+        src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    if not args.no_traffic:
+        log("measuring HBM traffic per step (rocprofv3 --pmc child runs)")
+        traffic, detail = measure_traffic(5)
+        result["roofline"]["traffic"] = round(traffic) if traffic else None
+        result["roofline"]["traffic_detail"] = detail
     be.close()
     print(json.dumps(result), flush=True)
     return 0
