@@ -374,8 +374,10 @@ def main():
     except Exception as e:
         log(f"parity check skipped: {e}")
 
+    fmt_name = {B.Q4_0: "Q4_0", B.Q8_0: "Q8_0", B.Q4_K: "Q4_K", B.Q6_K: "Q6_K"}.get(w_type, "quantized")
+    metric = METRIC if args.config == 2 else f"{fmt_name} GEMV achieved HBM GB/s (% of peak) + µs/call, 1 GPU"
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
