@@ -57,6 +57,13 @@ class Backend:
     def quantize_act_raw(self, act_type, x, rows, k, out, mem):
         L.check(self._lib.barq_rocm_quantize_act(self.h, act_type, _ptr(x), rows, k, _ptr(out), mem))
 
+    def rms_norm_raw(self, x, weight, rows, n, eps, y, mem):
+        L.check(self._lib.barq_rocm_rms_norm(self.h, _ptr(x), _ptr(weight), rows, n, eps, _ptr(y), mem))
+
+    def rms_norm_quantize_raw(self, act_type, x, weight, rows, n, eps, out, mem):
+        L.check(self._lib.barq_rocm_rms_norm_quantize(self.h, act_type, _ptr(x), _ptr(weight), rows, n, eps,
+                                                      _ptr(out), mem))
+
     def matvec_raw(self, w_type, w, n_rows, k, act_type, x, y, mem):
         L.check(self._lib.barq_rocm_matvec(self.h, w_type, _ptr(w), n_rows, k, act_type, _ptr(x), _ptr(y), mem))
 
@@ -79,6 +86,32 @@ class Backend:
         out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         self.quantize_act_raw(act_type, x, rows, k, out, L.MEM_DEVICE)
         if sync:
+            self.sync()
+        return out
+
+    def rms_norm(self, x, weight, eps, mem=L.MEM_DEVICE, sync=True):
+        """RMSNorm of each row of x ([rows, n]); numpy arrays with mem=MEM_HOST."""
+        rows, n = (1, x.size if mem == L.MEM_HOST else x.numel()) if x.ndim == 1 else tuple(x.shape)
+        if mem == L.MEM_HOST:
+            y = np.empty((rows, n), dtype=np.float32)
+        else:
+            import torch
+            y = torch.empty((rows, n), dtype=torch.float32, device=x.device)
+        self.rms_norm_raw(x, weight, rows, n, eps, y, mem)
+        if sync and mem == L.MEM_DEVICE:
+            self.sync()
+        return y
+
+    def rms_norm_quantize(self, act_type, x, weight, eps, mem=L.MEM_DEVICE, sync=True):
+        rows, n = (1, x.size if mem == L.MEM_HOST else x.numel()) if x.ndim == 1 else tuple(x.shape)
+        nbytes = rows * (n // L.BLOCK_ELEMS[act_type]) * L.BLOCK_BYTES[act_type]
+        if mem == L.MEM_HOST:
+            out = np.empty(nbytes, dtype=np.uint8)
+        else:
+            import torch
+            out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        self.rms_norm_quantize_raw(act_type, x, weight, rows, n, eps, out, mem)
+        if sync and mem == L.MEM_DEVICE:
             self.sync()
         return out
 

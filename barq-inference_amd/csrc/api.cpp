@@ -286,6 +286,64 @@ int barq_rocm_quantize_act(barq_rocm_handle* h, int act_type, const float* x, si
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm (transformer.rs:148-172), alone and fused with the quantizer
+
+int barq_rocm_rms_norm(barq_rocm_handle* h, const float* x, const float* weight, size_t rows, size_t n, float eps,
+                       float* y, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (rows == 0 || n == 0) return ok();
+    if (!barq::rms_norm_supported(n)) return fail(BARQ_E_DIM, "rms_norm: n=%zu must be a multiple of 4 and at most 16384", n);
+    if (!x || !weight || !y) return fail(BARQ_E_INVALID, "rms_norm: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(y, 16))
+            return fail(BARQ_E_INVALID, "rms_norm: buffers must be 16-byte aligned");
+        return launched(barq::rms_norm_launch(x, weight, rows, n, eps, y, h->stream), "rms_norm");
+    }
+    Arena a;
+    const size_t ox = a.add(rows * n * 4), ow = a.add(n * 4), oy = a.add(rows * n * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, rows * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ow), weight, n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::rms_norm_launch(at<float>(h, ox), at<float>(h, ow), rows, n, eps, at<float>(h, oy), h->stream),
+                        "rms_norm"));
+    BARQ_HIP(hipMemcpyAsync(y, at<float>(h, oy), rows * n * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* x, const float* weight, size_t rows,
+                                size_t n, float eps, void* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (act_type != BARQ_TYPE_Q8_0 && act_type != BARQ_TYPE_Q8_K)
+        return fail(BARQ_E_UNSUPPORTED, "rms_norm_quantize: act_type must be Q8_0 or Q8_K, got %d", act_type);
+    if (rows == 0 || n == 0) return ok();
+    if (n % 256 != 0 || !barq::rms_norm_supported(n))
+        return fail(BARQ_E_DIM, "rms_norm_quantize: n=%zu must be a multiple of 256 and at most 16384", n);
+    if (!x || !weight || !out) return fail(BARQ_E_INVALID, "rms_norm_quantize: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const size_t out_bytes = rows * row_bytes_of(act_type, n);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, act_type == BARQ_TYPE_Q8_K ? 4 : 2))
+            return fail(BARQ_E_INVALID, "rms_norm_quantize: misaligned buffer (x, weight 16-byte; out %d-byte)",
+                        act_type == BARQ_TYPE_Q8_K ? 4 : 2);
+        return launched(barq::rms_norm_quantize_launch(act_type, x, weight, rows, n, eps, out, h->stream), "rms_norm_quantize");
+    }
+    Arena a;
+    const size_t ox = a.add(rows * n * 4), ow = a.add(n * 4), oo = a.add(out_bytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, rows * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ow), weight, n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::rms_norm_quantize_launch(act_type, at<float>(h, ox), at<float>(h, ow), rows, n, eps,
+                                                       at<uint8_t>(h, oo), h->stream), "rms_norm_quantize"));
+    BARQ_HIP(hipMemcpyAsync(out, at<uint8_t>(h, oo), out_bytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
 // matvec / matmul
 
 namespace {

@@ -23,6 +23,14 @@ hipError_t quantize_q8_k_gather_launch(const float* x, const int32_t* rows_idx, 
 // Q8_K rows of silu(g) * u (k-element rows; the product is not stored)
 hipError_t swiglu_q8_k_launch(const float* g, const float* u, size_t n_rows, size_t k, void* out, hipStream_t s);
 
+// norm.hip: RMSNorm rows (transformer.rs:148-172), alone or fused with the
+// Q8_K / Q8_0 quantizer (n % 256 == 0 for the fused form)
+bool rms_norm_supported(size_t n);
+hipError_t rms_norm_launch(const float* x, const float* w, size_t rows, size_t n, float eps, float* y,
+                           hipStream_t s);
+hipError_t rms_norm_quantize_launch(int act_type, const float* x, const float* w, size_t rows, size_t n, float eps,
+                                    void* out, hipStream_t s);
+
 // gemv.hip
 hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,
                           float* y, hipStream_t s);

@@ -1,0 +1,184 @@
+// RMSNorm (models/src/transformer.rs:148-172), alone and fused with the
+// activation quantizer that the next projection consumes.
+//
+//   eps' = max(eps, f32::EPSILON)                      (:158)
+//   sum_sq = sum of x^2 over the row                   (:162)
+//   rms_inv = 1 / sqrt(sum_sq / n + eps')              (:163-164)
+//   y = (x * rms_inv) * w                              (:166)
+//
+// One workgroup (a wave per 256 elements, up to 16) per row; the row is held in registers, so the
+// fused variant reads x once and writes only Q8_K / Q8_0 blocks.  The sum of
+// squares runs in a fixed tree order (per lane, then a butterfly across the
+// wave, then the wave partials in order); the reference sums
+// sequentially, so the two agree to float rounding, not bit for bit.  Every
+// later step (the products and the quantizer) is the reference's own
+// sequence of single IEEE operations.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace barq {
+
+constexpr int NORM_MAX_WAVES = 16;
+
+// q8_k_block / q8_0 quantizers of quantize.hip, restated for values already
+// in registers: 4 elements per lane, a Q8_K block per wave, a Q8_0 block per
+// 8 lanes.
+__device__ __forceinline__ void norm_q8_k_block(const float (&vv)[4], int lane, uint8_t* __restrict__ blk) {
+    float ba = 0.0f, bv = 0.0f;
+    int bi = 0x7fffffff;
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float ax = fabsf(vv[j]);
+        if (ax > ba) { ba = ax; bv = vv[j]; bi = 4 * lane + j; }
+    }
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(ba, off);
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
+    }
+    if (ba == 0.0f) {
+        reinterpret_cast<uint32_t*>(blk + 4)[lane] = 0u;
+        if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = 0;
+        if (lane == 0) *reinterpret_cast<float*>(blk) = 0.0f;
+        return;
+    }
+    const float iscale = -127.0f / bv;
+    int q[4];
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int t = (int)rintf(iscale * vv[j]);
+        q[j] = t < 127 ? t : 127;
+    }
+    reinterpret_cast<uint32_t*>(blk + 4)[lane] = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                                                 ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
+    if (lane == 0) *reinterpret_cast<float*>(blk) = 1.0f / iscale;
+}
+
+// Q8_0 block of 32 = lanes 8g .. 8g + 7 (4 elements each): d = amax / 127
+// (stored f16), q = roundf(x * (1 / d)).
+__device__ __forceinline__ void norm_q8_0_block(const float (&vv)[4], int lane, uint8_t* __restrict__ blk) {
+    float a = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    const float d = a / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int l8 = lane & 7;
+    uint32_t packed = 0;
+    #pragma unroll
+    for (int j = 0; j < 4; j++) packed |= (uint32_t)((int)roundf(vv[j] * id) & 0xFF) << (8 * j);
+    // bytes 2 + 4 l8 .. : 2-byte aligned, so two 16-bit stores
+    uint16_t* qs = reinterpret_cast<uint16_t*>(blk + 2 + 4 * l8);
+    qs[0] = (uint16_t)(packed & 0xFFFFu);
+    qs[1] = (uint16_t)(packed >> 16);
+    if (l8 == 0) *reinterpret_cast<uint16_t*>(blk) = f32_to_f16_bits(d);
+}
+
+// W waves, V float4 chunks per lane: chunk i of wave w is float4
+// 64 (w + W i) + lane, i.e. lane `lane` of 256-element block w + W i.
+// OUT: 0 f32 rows, 1 Q8_K, 2 Q8_0.
+template <int W, int V, int OUT>
+__global__ __launch_bounds__(64 * W)
+void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n, float eps,
+                     void* __restrict__ out) {
+    __shared__ float part[W];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t row = blockIdx.x;
+    const int n4 = n / 4;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * (size_t)n);
+    const float4* wr = reinterpret_cast<const float4*>(w);
+    float4 v[V], wv[V];
+    // the weight is loaded with x, so the row costs one memory round trip
+    #pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int f = 64 * (wave + W * i) + lane;
+        v[i] = f < n4 ? xr[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        wv[i] = f < n4 ? wr[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float ss = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < V; i++) {
+        ss = ss + v[i].x * v[i].x;
+        ss = ss + v[i].y * v[i].y;
+        ss = ss + v[i].z * v[i].z;
+        ss = ss + v[i].w * v[i].w;
+    }
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    float sum_sq = part[0];
+    #pragma unroll
+    for (int i = 1; i < W; i++) sum_sq = sum_sq + part[i];
+    const float e = fmaxf(eps, 1.1920929e-7f);
+    const float rms_inv = 1.0f / sqrtf(sum_sq / (float)n + e);
+    #pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int blk = wave + W * i, f = 64 * blk + lane;
+        if (64 * blk >= n4) break;   // whole waves: n is a multiple of 256 for the quantized outputs
+        float y[4] = {(v[i].x * rms_inv) * wv[i].x, (v[i].y * rms_inv) * wv[i].y, (v[i].z * rms_inv) * wv[i].z,
+                      (v[i].w * rms_inv) * wv[i].w};
+        if constexpr (OUT == 0) {
+            if (f < n4) reinterpret_cast<float4*>(static_cast<float*>(out) + row * (size_t)n)[f] =
+                make_float4(y[0], y[1], y[2], y[3]);
+        } else if constexpr (OUT == 1) {
+            uint8_t* o = static_cast<uint8_t*>(out) + (row * (size_t)(n / 256) + blk) * Q8_K_BYTES;
+            norm_q8_k_block(y, lane, o);
+        } else {
+            uint8_t* o = static_cast<uint8_t*>(out) + (row * (size_t)(n / 32) + 8 * blk + (lane >> 3)) * Q8_0_BYTES;
+            norm_q8_0_block(y, lane, o);
+        }
+    }
+}
+
+// One wave per 256 elements up to 16 waves (short rows still spread over
+// many SIMDs), then up to four float4 chunks per lane.
+template <int W, int OUT>
+static hipError_t launch_norm_w(const float* x, const float* w, size_t rows, size_t n, float eps, void* out,
+                                hipStream_t s) {
+    const size_t chunks = (n / 4 + 64 * W - 1) / (64 * W);   // float4 chunks per lane
+#define BARQ_NORM_CASE(VV) \
+    if (chunks <= VV) { \
+        hipLaunchKernelGGL((rms_norm_kernel<W, VV, OUT>), dim3((unsigned)rows), dim3(64 * W), 0, s, x, w, (int)n, \
+                           eps, out); \
+        return hipGetLastError(); \
+    }
+    BARQ_NORM_CASE(1) BARQ_NORM_CASE(2) BARQ_NORM_CASE(4)
+#undef BARQ_NORM_CASE
+    return hipErrorInvalidValue;
+}
+
+template <int OUT>
+static hipError_t launch_norm(const float* x, const float* w, size_t rows, size_t n, float eps, void* out,
+                              hipStream_t s) {
+    const size_t blocks = (n + 255) / 256;
+    if (blocks <= 1) return launch_norm_w<1, OUT>(x, w, rows, n, eps, out, s);
+    if (blocks <= 2) return launch_norm_w<2, OUT>(x, w, rows, n, eps, out, s);
+    if (blocks <= 4) return launch_norm_w<4, OUT>(x, w, rows, n, eps, out, s);
+    if (blocks <= 8) return launch_norm_w<8, OUT>(x, w, rows, n, eps, out, s);
+    return launch_norm_w<16, OUT>(x, w, rows, n, eps, out, s);
+}
+
+// rows of up to 16 waves x 4 float4 chunks per lane (16384 elements) are held in registers
+bool rms_norm_supported(size_t n) { return n > 0 && n % 4 == 0 && n <= 4 * 4 * 64 * NORM_MAX_WAVES; }
+
+hipError_t rms_norm_launch(const float* x, const float* w, size_t rows, size_t n, float eps, float* y,
+                           hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    return launch_norm<0>(x, w, rows, n, eps, y, s);
+}
+
+hipError_t rms_norm_quantize_launch(int act_type, const float* x, const float* w, size_t rows, size_t n, float eps,
+                                    void* out, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (n % 256 != 0) return hipErrorInvalidValue;
+    return act_type == TYPE_Q8_K ? launch_norm<1>(x, w, rows, n, eps, out, s) : launch_norm<2>(x, w, rows, n, eps, out, s);
+}
+
+}  // namespace barq

@@ -49,6 +49,8 @@ def parse():
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     p.add_argument("--no-traffic", action="store_true",
                    help="skip the two rocprofv3 --pmc child runs that measure HBM traffic per launch")
+    p.add_argument("--norm", action="store_true",
+                   help="time the fused RMSNorm -> Q8_K quantizer (the step before each projection) instead of a config")
     p.add_argument("--probe-copy", action="store_true",
                    help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -305,6 +307,60 @@ def bench_moe(args):
     return 0
 
 
+def bench_norm(args):
+    """RMSNorm fused with the Q8_K quantizer of the next projection
+    (transformer.rs:148-172 then the activation quantize), Llama-3-8B hidden
+    4096, at 1 and 512 rows, beside the unfused pair (rms_norm then
+    quantize_act).  HBM-bound: x and the norm weight read, Q8_K written."""
+    import numpy as np
+    import torch
+
+    import barq_rocm as B
+    from barq_rocm import synth
+
+    be = B.Backend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    n = 4096
+    lines = {}
+    for rows in (1, 512):
+        x = torch.from_numpy(synth.gen_f32(rows * n, 7).reshape(rows, n)).cuda()
+        w = torch.from_numpy((1.0 + 0.25 * synth.gen_f32(n, 8)).astype(np.float32)).cuda()
+        q = torch.empty(rows * (n // 256) * 292, dtype=torch.uint8, device="cuda")
+        y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+
+        def fused(i):
+            be.rms_norm_quantize_raw(B.Q8_K, x, w, rows, n, 1e-5, q, B.MEM_DEVICE)
+
+        def unfused(i):
+            be.rms_norm_raw(x, w, rows, n, 1e-5, y, B.MEM_DEVICE)
+            be.quantize_act_raw(B.Q8_K, y, rows, n, q, B.MEM_DEVICE)
+        for i in range(args.warmup):
+            fused(i)
+            unfused(i)
+        ms_f, method = time_launches(fused, args.steps, args.eager)
+        ms_u, _ = time_launches(unfused, args.steps, args.eager)
+        alg = rows * n * 4 + n * 4 + rows * (n // 256) * 292
+        lines[rows] = dict(us_fused=round(ms_f * 1e3, 3), us_unfused=round(ms_u * 1e3, 3),
+                           gbs_fused=round(alg / (ms_f * 1e-3) / 1e9, 2), alg_bytes=alg, timing=method)
+    big = lines[512]
+    result = {
+        "metric": "RMSNorm -> Q8_K fused achieved HBM GB/s (512 x 4096 rows) + us/call, 1 GPU",
+        "value": big["gbs_fused"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(big["us_fused"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "RMSNorm(4096) -> Q8_K, 1 and 512 rows", "rows": lines},
+        "roofline": {"bound": "hbm", "achieved": big["gbs_fused"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(big["gbs_fused"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "alg_bytes_per_launch": big["alg_bytes"]},
+    }
+    be.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -318,6 +374,8 @@ def main():
     from barq_rocm import synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.norm:
+        return bench_norm(args)
     if args.config == 5:
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]

@@ -120,6 +120,26 @@ int barq_rocm_dequantize(barq_rocm_handle* h, int type, const void* blocks,
 int barq_rocm_quantize_act(barq_rocm_handle* h, int act_type, const float* x,
                            size_t n_rows, size_t k, void* out_blocks, int mem);
 
+/* ---- RMSNorm -------------------------------------------------------------
+ * Replaces LlamaTransformer::rms_norm (models/src/transformer.rs:148-172),
+ * the step before every projection (:132, :139, :469): per row of n,
+ * y = (x * (1 / sqrt(sum(x^2) / n + max(eps, FLT_EPSILON)))) * weight.
+ * The sum of squares runs in a fixed tree order (the reference sums
+ * sequentially): results agree with the reference to float rounding.
+ * n % 4 == 0, n <= 16384; x, weight, y 16-byte aligned on the device. */
+int barq_rocm_rms_norm(barq_rocm_handle* h, const float* x, const float* weight,
+                       size_t rows, size_t n, float eps, float* y, int mem);
+
+/* RMSNorm fused with the activation quantizer of the next projection:
+ * writes act_type (BARQ_TYPE_Q8_K or BARQ_TYPE_Q8_0) blocks of the
+ * normalized rows without storing them in f32.  Byte-identical to
+ * barq_rocm_quantize_act(act_type, barq_rocm_rms_norm(x)).  The reference
+ * has no fused form (its projections take f32, transformer.rs:274).
+ * n % 256 == 0, n <= 16384. */
+int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* x,
+                                const float* weight, size_t rows, size_t n, float eps,
+                                void* out_blocks, int mem);
+
 /* ---- matvec / matmul ---------------------------------------------------
  * Replace blas::gemv_f32 (blas.rs:229-304; the output head,
  * transformer.rs:486) and blas::gemm_f32 (blas.rs:103-213; every

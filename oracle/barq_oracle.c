@@ -15,6 +15,8 @@
 /* small helpers                                                             */
 /* ------------------------------------------------------------------------ */
 
+#define FLT_EPSILON_ORC 1.1920929e-7f   /* f32::EPSILON = 2^-23 */
+
 static float f32_from_bits(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static uint32_t bits_from_f32(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
@@ -355,6 +357,29 @@ void orc_quantize_q8_k(const float* x, size_t k, uint8_t* out) {
 /* ------------------------------------------------------------------------ */
 /* the reference's f32 GEMV / GEMM                                           */
 /* ------------------------------------------------------------------------ */
+
+/* LlamaTransformer::rms_norm (models/src/transformer.rs:148-172), row by
+   row: eps' = eps.max(f32::EPSILON) (:158); sum_sq sequential over the row
+   (:162, Iterator::sum folds left); mean_square = sum_sq / n (:163);
+   rms_inv = 1.0 / (mean_square + eps').sqrt() (:164);
+   y = hidden * rms_inv * weight, left to right (:166). */
+void orc_rms_norm(const float* x, const float* w, size_t rows, size_t n, float eps, float* y) {
+    const float e = eps > FLT_EPSILON_ORC ? eps : FLT_EPSILON_ORC;
+    for (size_t r = 0; r < rows; r++) {
+        const float* xr = x + r * n;
+        float sum_sq = 0.0f;
+        for (size_t j = 0; j < n; j++) {
+            const float sq = xr[j] * xr[j];
+            sum_sq = sum_sq + sq;
+        }
+        const float mean_square = sum_sq / (float)n;
+        const float rms_inv = 1.0f / sqrtf(mean_square + e);
+        for (size_t j = 0; j < n; j++) {
+            const float t = xr[j] * rms_inv;
+            y[r * n + j] = t * w[j];
+        }
+    }
+}
 
 void orc_gemv_f32(const float* a, const float* x, size_t m, size_t n, float* y) {
     for (size_t i = 0; i < m; i++) {

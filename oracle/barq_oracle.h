@@ -80,6 +80,8 @@ void orc_quantize_q8_k(const float* x, size_t k, uint8_t* out);
 /* ---- the reference's f32 arithmetic ----------------------------------- */
 /* blas::gemv_f32 CPU fallback, barq_core/src/blas.rs:292-303:
    y[i] = sum_j a[i*n+j]*x[j], sequential f32, unfused. */
+/* RMSNorm rows (transformer.rs:148-172), sequential sum of squares */
+void orc_rms_norm(const float* x, const float* w, size_t rows, size_t n, float eps, float* y);
 void orc_gemv_f32(const float* a, const float* x, size_t m, size_t n, float* y);
 /* blas::gemm_f32 CPU fallback, blas.rs:193-212: C[m x n] = A[m x k] B[k x n],
    per (i,j) a sequential unfused f32 sum over kk. */

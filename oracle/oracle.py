@@ -39,6 +39,7 @@ def lib():
             "orc_quantize_q8_0": (None, [_vp, _sz, _vp]),
             "orc_quantize_q8_k": (None, [_vp, _sz, _vp]),
             "orc_gemv_f32": (None, [_vp, _vp, _sz, _sz, _vp]),
+            "orc_rms_norm": (None, [_vp, _vp, _sz, _sz, ctypes.c_float, _vp]),
             "orc_gemm_f32": (None, [_vp, _vp, _sz, _sz, _sz, _vp]),
             "orc_matvec": (_i, [_i, _vp, _sz, _sz, _i, _vp, _vp]),
             "orc_matmul": (_i, [_i, _vp, _sz, _sz, _i, _vp, _sz, _vp]),
@@ -136,6 +137,16 @@ def quantize_q8_k(x: np.ndarray) -> np.ndarray:
 
 def quantize_act(act_type: int, x: np.ndarray) -> np.ndarray:
     return quantize_q8_0(x) if act_type == Q8_0 else quantize_q8_k(x)
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """transformer.rs:148-172 on each row of x ([rows, n])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, n = (1, x.size) if x.ndim == 1 else x.shape
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty((rows, n), dtype=np.float32)
+    lib().orc_rms_norm(_p(x), _p(w), rows, n, eps, _p(y))
+    return y
 
 
 def gemv_f32(a: np.ndarray, x: np.ndarray, m: int, n: int) -> np.ndarray:
