@@ -20,9 +20,11 @@ E_DIM = 3
 E_QUANT = 4
 E_INVALID = 5
 E_ALLOC = 6
+E_GGUF = 7
+E_IO = 8
 STATUS_NAMES = {
     OK: "Ok", E_BACKEND: "Backend", E_UNSUPPORTED: "Unsupported", E_DIM: "DimensionMismatch",
-    E_QUANT: "Quantization", E_INVALID: "Tensor", E_ALLOC: "Allocation",
+    E_QUANT: "Quantization", E_INVALID: "Tensor", E_ALLOC: "Allocation", E_GGUF: "InvalidGguf", E_IO: "Io",
 }
 
 # barq_type (GgufTensorType discriminants, barq_core/src/gguf.rs:117-137)
@@ -53,7 +55,10 @@ EXPORTS = (
     "barq_rocm_matvec", "barq_rocm_matmul",
     "barq_rocm_gemm_f32", "barq_rocm_gemv_f32", "barq_rocm_dequantize_split",
     "barq_rocm_quantized_matmul_split", "barq_rocm_quantize_q4_0_barq", "barq_rocm_moe_route",
-    "barq_rocm_moe_ffn",
+    "barq_rocm_moe_ffn", "barq_rocm_gguf_open", "barq_rocm_gguf_close", "barq_rocm_gguf_info",
+    "barq_rocm_gguf_tensor", "barq_rocm_gguf_find_tensor", "barq_rocm_gguf_kv_type", "barq_rocm_gguf_kv_int",
+    "barq_rocm_gguf_kv_number", "barq_rocm_gguf_kv_string", "barq_rocm_cache_create", "barq_rocm_cache_get",
+    "barq_rocm_cache_bytes", "barq_rocm_cache_destroy",
 )
 
 
@@ -68,6 +73,8 @@ _lib = None
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _i = ctypes.c_int
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
 
 
 def _declare(lib):
@@ -95,6 +102,24 @@ def _declare(lib):
         "barq_rocm_quantize_q4_0_barq": (_i, [_vp, _vp, _sz, _vp, _i]),
         "barq_rocm_moe_route": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i]),
         "barq_rocm_moe_ffn": (_i, [_vp, _sz, _i, _vp, _i, _vp, _i, _vp, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp, _i]),
+        "barq_rocm_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+        "barq_rocm_gguf_close": (_i, [_vp]),
+        "barq_rocm_gguf_info": (_i, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u64), ctypes.POINTER(_u64),
+                                     ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
+        "barq_rocm_gguf_tensor": (_i, [_vp, _u64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i),
+                                       ctypes.POINTER(_u32), ctypes.POINTER(_u64), ctypes.POINTER(_u64),
+                                       ctypes.POINTER(_u64), ctypes.POINTER(_vp)]),
+        "barq_rocm_gguf_find_tensor": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
+        "barq_rocm_gguf_kv_type": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                                        ctypes.POINTER(_u64)]),
+        "barq_rocm_gguf_kv_int": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+        "barq_rocm_gguf_kv_number": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+        "barq_rocm_gguf_kv_string": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
+        "barq_rocm_cache_create": (_i, [_vp, _vp, ctypes.POINTER(_vp)]),
+        "barq_rocm_cache_get": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_u64),
+                                     ctypes.POINTER(_u64), ctypes.POINTER(_vp)]),
+        "barq_rocm_cache_bytes": (_u64, [_vp]),
+        "barq_rocm_cache_destroy": (_i, [_vp]),
     }
     for name, (res, args) in P.items():
         fn = getattr(lib, name)

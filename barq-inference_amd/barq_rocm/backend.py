@@ -17,6 +17,8 @@ from . import _lib as L
 def _ptr(t) -> int:
     if t is None:
         return 0
+    if isinstance(t, int):   # a raw device pointer (e.g. from the weight cache)
+        return t
     if isinstance(t, np.ndarray):
         return t.ctypes.data
     return t.data_ptr()

@@ -10,21 +10,14 @@
 #include <string>
 #include <vector>
 
+#include "api_internal.hpp"
 #include "launch.hpp"
 
-struct barq_rocm_handle {
-    int device = 0;
-    hipStream_t own = nullptr;
-    hipStream_t stream = nullptr;
-    void* ws = nullptr;        // device workspace, grown on demand
-    size_t ws_size = 0;
-};
-
 namespace {
-
 thread_local std::string g_last_error;
+}
 
-int fail(int code, const char* fmt, ...) {
+int barq_api::fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -34,7 +27,11 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-int ok() { return BARQ_OK; }
+namespace {
+
+using barq_api::DeviceGuard;
+using barq_api::fail;
+using barq_api::ok;
 
 #define BARQ_HIP(expr)                                                                          \
     do {                                                                                        \
@@ -47,20 +44,6 @@ int ok() { return BARQ_OK; }
         int rc_ = (rc_expr);         \
         if (rc_ != BARQ_OK) return rc_; \
     } while (0)
-
-// Make the handle's device current for the duration of a call.
-struct DeviceGuard {
-    int prev = -1;
-    bool changed = false;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
-            changed = hipSetDevice(dev) == hipSuccess;
-        }
-    }
-    ~DeviceGuard() {
-        if (changed) (void)hipSetDevice(prev);
-    }
-};
 
 bool is_weight_type(int t) {
     return t == BARQ_TYPE_Q4_0 || t == BARQ_TYPE_Q8_0 || t == BARQ_TYPE_Q4_K || t == BARQ_TYPE_Q6_K ||

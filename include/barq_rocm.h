@@ -47,7 +47,9 @@ typedef enum {
     BARQ_E_DIM = 3,          /* Error::DimensionMismatch (error.rs:27) */
     BARQ_E_QUANT = 4,        /* Error::Quantization (error.rs:44): k not a whole number of blocks */
     BARQ_E_INVALID = 5,      /* Error::Tensor (error.rs:11): null pointer or bad argument */
-    BARQ_E_ALLOC = 6         /* Error::Allocation (error.rs:15) */
+    BARQ_E_ALLOC = 6,        /* Error::Allocation (error.rs:15) */
+    BARQ_E_GGUF = 7,         /* Error::InvalidGguf (error.rs:39-40): malformed GGUF file */
+    BARQ_E_IO = 8            /* Error::Io (error.rs:31): file cannot be read, or ends early */
 } barq_status;
 
 /* Type ids: the GgufTensorType discriminants (barq_core/src/gguf.rs:117-137),
@@ -214,6 +216,57 @@ int barq_rocm_moe_ffn(barq_rocm_handle* h, size_t n_experts,
                       size_t hidden, size_t n_ff, const float* x, size_t rows,
                       const int32_t* ids, const float* weights, size_t top_k,
                       int act, float* out, int mem);
+
+/* ---- GGUF files: packed loader ------------------------------------------
+ * Replaces GgufReader::open / tensor_info / get / get_tensor_info
+ * (barq_core/src/gguf.rs:250-413).  The file is memory-mapped and read with
+ * the reference's rules: magic "GGUF", version <= 3, u64 counts, KV values
+ * of the 13 GgufType kinds (arrays nest), general.alignment when it is a
+ * u32 (default 32), tensor infos, data section aligned after them.  A
+ * tensor is handed out as its packed bytes at data_offset + offset (where
+ * load_tensor seeks, gguf.rs:428-431) instead of being dequantized at load
+ * (:437-475).  GGUF type 2 is the 18-byte GGUF Q4_0 block (BARQ_TYPE_Q4_0).
+ * Errors: BARQ_E_GGUF for malformed content (bad magic, version, value or
+ * tensor type, non-UTF-8 string), BARQ_E_IO when the file ends early. */
+typedef struct barq_rocm_gguf barq_rocm_gguf;
+
+int barq_rocm_gguf_open(const char* path, barq_rocm_gguf** out);
+int barq_rocm_gguf_close(barq_rocm_gguf* g);
+int barq_rocm_gguf_info(const barq_rocm_gguf* g, uint32_t* version, uint64_t* n_tensors,
+                        uint64_t* n_kv, uint32_t* alignment, uint64_t* data_offset);
+/* Tensor `index` in file order: name (owned by g), GGUF type id, dims
+ * (dims[0] innermost; up to 4, more fold into dims[3]), offset in the data
+ * section, packed size (0 for types whose block layout is not known here,
+ * as the reference cannot load them either), and a host pointer to the bytes
+ * inside the mapping (BARQ_E_IO if they run past the end of the file). */
+int barq_rocm_gguf_tensor(const barq_rocm_gguf* g, uint64_t index, const char** name, int* type,
+                          uint32_t* n_dims, uint64_t* dims, uint64_t* offset, uint64_t* nbytes,
+                          const void** data);
+int barq_rocm_gguf_find_tensor(const barq_rocm_gguf* g, const char* name, uint64_t* index);
+/* KV access (GgufReader::get, gguf.rs:390): value type (GgufType id) and,
+ * for arrays, element type and length; scalars as int64 or double; strings
+ * as a pointer into the mapping and a length (not NUL-terminated). */
+int barq_rocm_gguf_kv_type(const barq_rocm_gguf* g, const char* key, int* type, int* array_type,
+                           uint64_t* array_len);
+int barq_rocm_gguf_kv_int(const barq_rocm_gguf* g, const char* key, int64_t* value);
+int barq_rocm_gguf_kv_number(const barq_rocm_gguf* g, const char* key, double* value);
+int barq_rocm_gguf_kv_string(const barq_rocm_gguf* g, const char* key, const char** ptr, uint64_t* len);
+
+/* ---- packed weight cache --------------------------------------------------
+ * Replaces WeightCache::initialize / build_transposed_entry / get_proj /
+ * get_raw (models/src/weight_cache.rs:48-244) without the dequantize and
+ * transpose: every sized tensor of the file is copied once, packed, into
+ * one device allocation on the handle's device (256-byte aligned each).
+ * cache_get returns the device pointer for barq_rocm_matvec / matmul /
+ * moe_ffn, with k = dims[0] and n_rows = dims[1] * dims[2] * dims[3].
+ * The cache allocates at creation only and frees at destroy. */
+typedef struct barq_rocm_cache barq_rocm_cache;
+
+int barq_rocm_cache_create(barq_rocm_handle* h, const barq_rocm_gguf* g, barq_rocm_cache** out);
+int barq_rocm_cache_get(const barq_rocm_cache* c, const char* name, int* type, uint64_t* n_rows,
+                        uint64_t* k, const void** device_ptr);
+uint64_t barq_rocm_cache_bytes(const barq_rocm_cache* c);
+int barq_rocm_cache_destroy(barq_rocm_cache* c);
 
 #ifdef __cplusplus
 }
