@@ -1,7 +1,9 @@
 // Batched K-quant x Q8_K GEMM on gfx950 int8 MFMA: Y[m, n] = sum_k X[m, k] W[n, k]
 // for Q4_K and Q6_K weights (GGUF rows, blocks along k) and Q8_K activation
-// rows.  This is the prefill / MoE-expert-group path (M >= 16); it computes
-// the same quantity as the batch-1 GEMV, row by row.
+// rows with 16x16x64 tiles and register-staged loads.  gemm_kq.hip's
+// 32x32x32 kernel takes every shape it supports; this one remains for Q6_K
+// rows with an odd number of super-blocks (and for comparison runs with
+// BARQ_GEMM_IMPL=0).
 //
 // Per workgroup: a tile of BM activation rows x 64 weight rows; per 256-element
 // super-block, the Q8_K rows (int8 + scale + bsums) and the packed weight
@@ -392,251 +394,6 @@ void gemm_kq_kernel(const uint8_t* __restrict__ W, size_t w_row_bytes, const uin
 // independent accumulation chains); per super-block C = 8*Ch + Cl and
 // y += dx * (d*C - dmin*Cm).
 // ---------------------------------------------------------------------------
-typedef int v16i __attribute__((ext_vector_type(16)));
-constexpr int G3_BN = 128;
-
-// Buffer -> LDS direct loads (lane i's bytes land at the wave's LDS base + i * size).
-// Issued as inline asm so the compiler's wait-count insertion does not treat
-// every in-flight stage as a pending write to the stage being read (it drains
-// all of them otherwise); the kernel waits on its own loads with wait_vmcnt
-// before each barrier.  The descriptor is passed as four SGPRs.
-typedef int i32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-#ifdef BARQ_DMA_BUILTIN
-typedef brsrc dma_rsrc;
-__device__ __forceinline__ dma_rsrc make_dma_rsrc(const void* base, uint32_t bytes) { return make_brsrc(base, bytes); }
-__device__ __forceinline__ void lds_load16(dma_rsrc r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void lds_load4(dma_rsrc r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 4, voff, soff, 0, 0);
-}
-#else
-typedef i32x4v dma_rsrc;
-__device__ __forceinline__ i32x4v make_rsrc4(const void* base, uint32_t bytes);
-__device__ __forceinline__ dma_rsrc make_dma_rsrc(const void* base, uint32_t bytes) { return make_rsrc4(base, bytes); }
-__device__ __forceinline__ void lds_load16(i32x4v r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_load4(i32x4v r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
-}
-#endif
-__device__ __forceinline__ i32x4v make_rsrc4(const void* base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    return i32x4v{(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xFFFF, (int)bytes, 0x00020000};
-}
-
-template <int BM, int NW = 4>
-struct G3 {
-    static constexpr int XQ = 0;                              // BM rows x 272 B: 256 int8 + a 16-byte pad chunk
-    static constexpr int W = (BM * 17 + 63) / 64 * 1024;      // 128 x 144 packed Q4_K blocks (after the padded activation rows)
-    static constexpr int XD = W + G3_BN * Q4_K_BYTES;         // BM f32 block scales (room for one 64-lane load)
-    static constexpr int XD_LOADS = BM < 64 ? 1 : BM / 64;
-    static constexpr int STAGE = XD + XD_LOADS * 256;
-    static constexpr int X_CHUNKS = BM * 17;                  // activation tile in 16-byte chunks, pads included
-    static constexpr int X_INSTR_ALL = (X_CHUNKS + 63) / 64;  // 64-chunk load instructions for the whole tile
-    static constexpr int X_INSTR = (X_INSTR_ALL + NW - 1) / NW;   // per wave (the last one may be partial or absent)
-    static constexpr int W_INSTR_ALL = G3_BN * 9 / 64;        // 18 for the weight tile
-    static constexpr int LOADS_MIN = X_INSTR_ALL / NW + W_INSTR_ALL / NW;   // load instructions every wave issues per stage (at least)
-    static constexpr int W_INSTR = (W_INSTR_ALL + NW - 1) / NW;
-    static constexpr int MTW = BM / 32 / (NW / 4);             // 32x32 MFMA tiles per wave
-};
-
-// Per-thread offsets of the stage loads (independent of the super-block).
-template <int BM, int NW>
-struct G3Off {
-    uint32_t x[G3<BM, NW>::X_INSTR];
-    uint32_t w[G3<BM, NW>::W_INSTR];
-    uint32_t xd;
-};
-
-template <int BM, int NW>
-__device__ __forceinline__ void g3_offsets(G3Off<BM, NW>& o, uint32_t xrb, uint32_t wrb, int wave, int l) {
-    using L = G3<BM, NW>;
-    #pragma unroll
-    for (int q = 0; q < L::X_INSTR; q++) {
-        const int p = (q * NW + wave) * 64 + l, r = p / 17, c = p - r * 17;
-        // the pad chunk (c == 16) and chunks past the tile reload a valid chunk of the row
-        o.x[q] = (uint32_t)r * xrb + 4u + 16u * (uint32_t)(c < 16 ? c : 0);
-    }
-    #pragma unroll
-    for (int q = 0; q < L::W_INSTR; q++) {
-        const int p = (q * NW + wave) * 64 + l, row = p / 9, piece = p - row * 9;
-        o.w[q] = (uint32_t)row * wrb + 16u * (uint32_t)piece;
-    }
-    o.xd = (uint32_t)(64 * wave + l) * xrb;
-}
-
-template <int BM, int NW>
-__device__ __forceinline__ void g3_issue(uint8_t* stage, dma_rsrc xr, dma_rsrc wr, const G3Off<BM, NW>& o, int b, int wave) {
-    using L = G3<BM, NW>;
-    const uint32_t xs = (uint32_t)b * Q8_K_BYTES, ws = (uint32_t)b * Q4_K_BYTES;
-    #pragma unroll
-    for (int q = 0; q < L::X_INSTR; q++) {
-        const int idx = q * NW + wave;
-        if (idx < L::X_INSTR_ALL) lds_load16(xr, stage + L::XQ + 1024 * idx, o.x[q], xs);
-    }
-    #pragma unroll
-    for (int q = 0; q < L::W_INSTR; q++) {
-        const int idx = q * NW + wave;
-        if (idx < L::W_INSTR_ALL) lds_load16(wr, stage + L::W + 1024 * idx, o.w[q], ws);
-    }
-    if (wave < L::XD_LOADS) lds_load4(xr, stage + L::XD + 256 * wave, o.xd, xs);
-}
-
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-template <int BM, int NW>
-__device__ __forceinline__ void g3_compute(const uint8_t* stage, float (&acc)[G3<BM, NW>::MTW][16], int wave, int l) {
-    using L = G3<BM, NW>;
-    constexpr int MT = L::MTW;
-    const int n = l & 31, g2 = l >> 5;
-    const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // 8 waves: two per 32-column slice, one per half of the rows
-    const uint8_t* wrow = stage + L::W + (32 * slice + n) * Q4_K_BYTES;
-    const uint4 hdr = *reinterpret_cast<const uint4*>(wrow);
-    const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
-    // get_scale_min_k4 (gguf.rs:825-837) for the eight sub-blocks, bytewise
-    const uint32_t scA = hdr.y & 0x3F3F3F3Fu;
-    const uint32_t scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
-    const uint32_t mA = hdr.z & 0x3F3F3F3Fu;
-    const uint32_t mB = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
-    // s = 8*s1 + s0 for four sub-blocks at a time
-    const uint32_t s1A = (scA >> 3) & 0x07070707u, s0A = scA & 0x07070707u;
-    const uint32_t s1B = (scB >> 3) & 0x07070707u, s0B = scB & 0x07070707u;
-    // this lane's activation row (tile 0) and k-group: chunk 2j + g2 of a 272-byte row
-    const uint8_t* xrow = stage + L::XQ + (mbase + n) * 272 + 16 * g2;
-    v16i ch[MT], cl[MT], cm[MT];
-    #pragma unroll
-    for (int pr = 0; pr < 4; pr++) {
-        // sub-blocks 2pr (low nibbles) and 2pr+1 (high nibbles) share qs[32pr + 16g2 .. +16)
-        const uint4 qs = *reinterpret_cast<const uint4*>(wrow + 16 + 32 * pr + 16 * g2);
-        #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int j = 2 * pr + h;
-            // byte j&3 of the packed scales / mins, broadcast with one v_perm each
-            const uint32_t bsel = (uint32_t)(j & 3);
-            const uint32_t s1 = __builtin_amdgcn_perm(0u, j < 4 ? s1A : s1B, 0x0c000c00u | (bsel << 16) | bsel);
-            const uint32_t s0 = __builtin_amdgcn_perm(0u, j < 4 ? s0A : s0B, 0x0c000c00u | (bsel << 16) | bsel);
-            const int mb = (int)__builtin_amdgcn_perm(0u, j < 4 ? mA : mB, bsel * 0x01010101u);
-            const uint32_t n0 = (qs.x >> (4 * h)) & 0x0F0F0F0Fu, n1 = (qs.y >> (4 * h)) & 0x0F0F0F0Fu;
-            const uint32_t n2 = (qs.z >> (4 * h)) & 0x0F0F0F0Fu, n3 = (qs.w >> (4 * h)) & 0x0F0F0F0Fu;
-            const v4i bh = {(int)mul_u16x2(n0, s1), (int)mul_u16x2(n1, s1), (int)mul_u16x2(n2, s1), (int)mul_u16x2(n3, s1)};
-            const v4i bl = {(int)mul_u16x2(n0, s0), (int)mul_u16x2(n1, s0), (int)mul_u16x2(n2, s0), (int)mul_u16x2(n3, s0)};
-            const v4i bm = {mb, mb, mb, mb};
-            #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * 272 + 32 * j);
-                const v16i z = {};
-                ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
-                cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
-                cm[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bm, j ? cm[t] : z, 0, 0, 0);
-            }
-        }
-    }
-    // C layout of the 32x32 MFMA: lane (n, g2), register r -> row 8*(r/4) + 4*g2 + r%4, column n
-    #pragma unroll
-    for (int t = 0; t < MT; t++) {
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 dx = *reinterpret_cast<const float4*>(stage + L::XD + 4 * (mbase + 32 * t + 8 * q + 4 * g2));
-            const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
-            #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = 4 * q + i;
-                const int c = (ch[t][r] << 3) + cl[t][r];
-                const float v = __builtin_fmaf(-dmin, (float)cm[t][r], d * (float)c);
-                acc[t][r] = __builtin_fmaf(dxv[i], v, acc[t][r]);
-            }
-        }
-    }
-}
-
-// One pipeline step: super-block b computed from stage S (= b % NS) while the
-// loads of b+NS-1 go to stage (S-1) % NS.  Each stage is its own LDS array,
-// so the compiler's wait counting separates the in-flight stages; the raw
-// s_barrier (no memory fence) does not drain them.
-template <int BM, int NW, int NS, int S>
-__device__ __forceinline__ void g3_step(uint8_t* const (&stages)[4], int b, int nsb, dma_rsrc xr, dma_rsrc wr,
-                                        const G3Off<BM, NW>& off, int wave, int l, float (&acc)[G3<BM, NW>::MTW][16]) {
-    using L = G3<BM, NW>;
-    if (b >= nsb) return;
-    // this thread's loads of super-block b are done once at most the later
-    // stages' loads are still outstanding; then every thread's are after the barrier
-    if (b + NS - 2 < nsb) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
-    else wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (b + NS - 1 < nsb) g3_issue<BM, NW>(stages[(S + NS - 1) % NS], xr, wr, off, b + NS - 1, wave);
-    g3_compute<BM, NW>(stages[S], acc, wave, l);
-}
-
-template <int BM, int NS, int NW>
-__global__ __launch_bounds__(64 * NW, (BM <= 32 ? 2 : 1))
-void gemm_q4k_v3_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb,
-                        float* __restrict__ Y, int M, int N, int nsb, int tiles_m, int n_tiles, int xcd_order) {
-    using L = G3<BM, NW>;
-    constexpr int MT = L::MTW;
-    static_assert(NS == 3 || NS == 4, "stage count");
-    __shared__ __align__(16) uint8_t st0[L::STAGE];
-    __shared__ __align__(16) uint8_t st1[L::STAGE];
-    __shared__ __align__(16) uint8_t st2[L::STAGE];
-    __shared__ __align__(16) uint8_t st3[NS == 4 ? L::STAGE : 16];
-    uint8_t* const stages[4] = {st0, st1, st2, st3};   // with NS == 3 the fourth is never used
-
-    int tile = blockIdx.x;
-    if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
-    const int mt = tile % tiles_m, ntile = tile / tiles_m;
-    const int m0 = mt * BM, n0 = ntile * G3_BN;
-    const int l = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-
-    const dma_rsrc xr = make_dma_rsrc(X + (size_t)m0 * xrb, (uint32_t)((size_t)(M - m0) * xrb));
-    const dma_rsrc wr = make_dma_rsrc(W + (size_t)n0 * wrb, (uint32_t)((size_t)(N - n0) * wrb));
-
-    float acc[MT][16];
-    #pragma unroll
-    for (int t = 0; t < MT; t++)
-        #pragma unroll
-        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
-
-    G3Off<BM, NW> off;
-    g3_offsets<BM, NW>(off, xrb, wrb, wave, l);
-    #pragma unroll
-    for (int s = 0; s < NS - 1; s++)
-        if (s < nsb) g3_issue<BM, NW>(stages[s], xr, wr, off, s, wave);
-    for (int b = 0; b < nsb; b += NS) {
-        g3_step<BM, NW, NS, 0>(stages, b, nsb, xr, wr, off, wave, l, acc);
-        g3_step<BM, NW, NS, 1>(stages, b + 1, nsb, xr, wr, off, wave, l, acc);
-        g3_step<BM, NW, NS, 2>(stages, b + 2, nsb, xr, wr, off, wave, l, acc);
-        if constexpr (NS == 4) g3_step<BM, NW, NS, 3>(stages, b + 3, nsb, xr, wr, off, wave, l, acc);
-    }
-
-    const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
-    if (col < N) {
-        #pragma unroll
-        for (int t = 0; t < MT; t++)
-            #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + mb + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (row < M) Y[(size_t)row * N + col] = acc[t][r];
-            }
-    }
-}
-
 // ---- launch ---------------------------------------------------------------
 static int read_env_bm() {
     if (const char* e = getenv("BARQ_GEMM_BM")) return atoi(e);
@@ -672,47 +429,13 @@ static int pick_bm(int M, int N) {
     return bm;
 }
 
-// BARQ_GEMM_IMPL: 2 = the format-generic kernel of gemm_kq.hip (default),
-// 1 = the Q4_K-only kernel above, 0 = the 16x16x64 kernel (tuning experiments)
-static int read_env_v3() {
+// BARQ_GEMM_IMPL=0 selects this file's 16x16x64 kernel for every shape
+// (comparison runs); by default gemm_kq.hip takes every shape it supports.
+static int read_env_impl() {
     if (const char* e = getenv("BARQ_GEMM_IMPL")) return atoi(e);
     return 2;
 }
-static int g_use_v3 = read_env_v3();
-// BARQ_GEMM_XCD=0 turns off the XCD-aware tile order (tuning experiments)
-static int read_env_xcd() {
-    if (const char* e = getenv("BARQ_GEMM_XCD")) return atoi(e);
-    return 1;
-}
-static int g_xcd_order = read_env_xcd();
-
-template <int BM, int NS, int NW = 4>
-static hipError_t launch_q4k_v3(const uint8_t* W, uint32_t wrb, const uint8_t* X, uint32_t xrb, float* Y, int M,
-                                int N, int nsb, hipStream_t s) {
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + G3_BN - 1) / G3_BN;
-    const int n_tiles = tiles_m * tiles_n;
-    hipLaunchKernelGGL((gemm_q4k_v3_kernel<BM, NS, NW>), dim3(n_tiles), dim3(64 * NW), 0, s, W, wrb, X, xrb, Y, M, N, nsb,
-                       tiles_m, n_tiles, g_xcd_order);
-    return hipGetLastError();
-}
-
-static hipError_t dispatch_q4k_v3(const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
-                                  hipStream_t s) {
-    const int nsb = (int)(k / 256);
-    const uint32_t wrb = (uint32_t)(nsb * Q4_K_BYTES), xrb = (uint32_t)(nsb * Q8_K_BYTES);
-    const uint8_t* w = static_cast<const uint8_t*>(W);
-    const uint8_t* x = static_cast<const uint8_t*>(xq);
-    const int M = (int)m, N = (int)n_rows;
-    const int tiles_n = (N + G3_BN - 1) / G3_BN;
-    // Tile choice (measured on MI355X): 64x128 workgroup tiles with eight
-    // waves (two per SIMD, each a 32x32 MFMA tile) for M > 32; 32-row tiles
-    // with four waves for the small expert groups of a MoE step.
-    const int bm = g_bm_override ? g_bm_override : (M > 32 ? 65 : 32);
-    (void)tiles_n;
-    if (bm == 65) return launch_q4k_v3<64, 4, 8>(w, wrb, x, xrb, y, M, N, nsb, s);
-    if (bm == 64) return launch_q4k_v3<64, 4>(w, wrb, x, xrb, y, M, N, nsb, s);
-    return launch_q4k_v3<32, 3>(w, wrb, x, xrb, y, M, N, nsb, s);
-}
+static const int g_impl = read_env_impl();
 
 template <class F>
 static hipError_t dispatch_kq(const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
@@ -743,9 +466,9 @@ hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t
                                 float* y, hipStream_t s) {
     if (m == 0 || n_rows == 0) return hipSuccess;
     if (!gemm_mfma_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
-    if (g_use_v3 == 2 && kq_supported(w_type, n_rows, k, m)) return kq_gemm_launch(w_type, W, n_rows, k, xq, m, y, s);
+    if (g_impl != 0 && kq_supported(w_type, n_rows, k, m)) return kq_gemm_launch(w_type, W, n_rows, k, xq, m, y, s);
     switch (w_type) {
-    case TYPE_Q4_K: return g_use_v3 == 1 ? dispatch_q4k_v3(W, n_rows, k, xq, m, y, s) : dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
+    case TYPE_Q4_K: return dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
     case TYPE_Q6_K: return dispatch_kq<GQ6K>(W, n_rows, k, xq, m, y, s);
     default: return hipErrorInvalidValue;
     }
