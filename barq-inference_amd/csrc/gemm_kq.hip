@@ -406,6 +406,26 @@ __device__ __forceinline__ void kq6_compute16(const uint8_t* st, int wave, int l
 }
 
 // ---- pipeline ----------------------------------------------------------------
+// Super-block b of the tile from one LDS stage into the accumulators (b's
+// parity places the Q6_K windows).
+template <class F, int BM, int NW>
+__device__ __forceinline__ void kq_compute(const uint8_t* st, int b, int wave, int l,
+                                           float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    using L = KQL<F, BM, NW>;
+    constexpr int MT = L::MTW;
+    if constexpr (BM == 16) {
+        if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute16(st, wave, l, acc);
+        else kq6_compute16(st, wave, l, b, acc);
+    } else {
+        const int n = l & 31, g2 = l >> 5;
+        const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
+        const uint8_t* wrow = st + L::W + (32 * slice + n) * F::RS;
+        const uint8_t* xrow = st + L::XQ + (mbase + n) * F::XRS + 16 * g2;
+        if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, acc);
+        else kq6_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, b, acc);
+    }
+}
+
 // One step: super-block b computed from stage S (= b % NS) while the loads of
 // b+NS-1 go to stage (S-1) % NS.  Each stage is its own LDS array; the raw
 // s_barrier (no memory fence) does not drain the in-flight stages.
@@ -426,18 +446,7 @@ __device__ __forceinline__ void kq_step(uint8_t* const (&stages)[KQ_MAX_NS], int
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (b + NS - 1 < nsb) kq_issue<F, BM, NW>(stages[(S + NS - 1) % NS], xr, wr, off, b + NS - 1, wave);
-    const uint8_t* st = stages[S];
-    if constexpr (BM == 16) {
-        if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute16(st, wave, l, acc);
-        else kq6_compute16(st, wave, l, b, acc);
-        return;
-    }
-    const int n = l & 31, g2 = l >> 5;
-    const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
-    const uint8_t* wrow = st + L::W + (32 * slice + n) * F::RS;
-    const uint8_t* xrow = st + L::XQ + (mbase + n) * F::XRS + 16 * g2;
-    if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, acc);
-    else kq6_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, b, acc);
+    kq_compute<F, BM, NW>(stages[S], b, wave, l, acc);
 }
 
 // One BM x 128 output tile: rows [m0, m0 + BM) of the `count` activation rows
@@ -449,6 +458,37 @@ __device__ __forceinline__ void kq_round(std::integer_sequence<int, S...>, uint8
                                          int nsb, i32x4v xr, i32x4v wr, const KQOff<F, BM, NW>& off, int wave, int l,
                                          float (&acc)[KQL<F, BM, NW>::MTW][16]) {
     (kq_step<F, BM, NW, NS, S>(stages, b + S, nsb, xr, wr, off, wave, l, acc), ...);
+}
+
+// Tile results to Y[row * N + col] for rows < count and columns < N.
+template <class F, int BM, int NW>
+__device__ __forceinline__ void kq_store(const float (&acc)[KQL<F, BM, NW>::MTW][16], float* Y, int count, int N,
+                                         int m0, int n0, int wave, int l) {
+    constexpr int MT = KQL<F, BM, NW>::MTW;
+    if constexpr (BM == 16) {
+        #pragma unroll
+        for (int cb = 0; cb < 2; cb++) {
+            const int col = n0 + 32 * wave + 16 * cb + (l & 15);
+            if (col < N) {
+                #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = m0 + 4 * (l >> 4) + r;
+                    if (row < count) Y[(size_t)row * N + col] = acc[0][4 * cb + r];
+                }
+            }
+        }
+        return;
+    }
+    const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
+    if (col < N) {
+        #pragma unroll
+        for (int t = 0; t < MT; t++)
+            #pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + mb + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
+                if (row < count) Y[(size_t)row * N + col] = acc[t][r];
+            }
+    }
 }
 
 template <class F, int BM, int NS, int NW>
@@ -476,30 +516,107 @@ __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], con
     for (int b = 0; b < nsb; b += NS)
         kq_round<F, BM, NW, NS>(std::make_integer_sequence<int, NS>{}, stages, b, nsb, xr, wr, off, wave, l, acc);
 
-    if constexpr (BM == 16) {
-        #pragma unroll
-        for (int cb = 0; cb < 2; cb++) {
-            const int col = n0 + 32 * wave + 16 * cb + (l & 15);
-            if (col < N) {
-                #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = m0 + 4 * (l >> 4) + r;
-                    if (row < count) Y[(size_t)row * N + col] = acc[0][4 * cb + r];
-                }
-            }
+    kq_store<F, BM, NW>(acc, Y, count, N, m0, n0, wave, l);
+}
+
+// ---- grouped: one pipeline across the workgroup's tiles ------------------------
+// A grouped workgroup runs several tiles; its loads run NS-1 super-blocks
+// ahead across tile boundaries, so a new tile does not start with an empty
+// pipeline.  Each step is still one stage: wait for this thread's loads of
+// the stage, barrier, issue the stage NS-1 steps ahead (into the stage every
+// wave finished before the barrier), compute.
+struct KQTile {
+    const uint8_t* W;
+    const uint8_t* X;
+    float* Y;
+    int count, m0, n0, kb0;
+};
+
+template <class F>
+__device__ __forceinline__ void kq_tile_rsrc(const KQTile& t, uint32_t xrb, uint32_t wrb, int N, i32x4v& xr, i32x4v& wr) {
+    const uint32_t xk = (uint32_t)t.kb0 * Q8_K_BYTES, wk = (uint32_t)t.kb0 * F::BB;
+    xr = make_rsrc4(t.X + (size_t)t.m0 * xrb + xk, (uint32_t)((size_t)(t.count - t.m0) * xrb) - xk);
+    wr = make_rsrc4(t.W + (size_t)t.n0 * wrb + wk, (uint32_t)((size_t)(N - t.n0) * wrb) - wk);
+}
+
+template <class F, int BM, int NW, class Dec>
+struct KQStream {
+    const Dec& decode;
+    int total, grid, nsb, N;
+    uint32_t xrb, wrb;
+    KQOff<F, BM, NW> off;
+    int wave, l;
+    // load cursor
+    int lt, lb;
+    i32x4v lxr, lwr;
+    // compute cursor
+    int ct, cb;
+    KQTile cT;
+
+    __device__ __forceinline__ void issue_next(uint8_t* stage) {
+        kq_issue<F, BM, NW>(stage, lxr, lwr, off, lb, wave);
+        if (++lb == nsb) {
+            lb = 0;
+            lt += grid;
+            if (lt < total) kq_tile_rsrc<F>(decode(lt), xrb, wrb, N, lxr, lwr);
         }
-        return;
     }
-    const int col = n0 + 32 * (wave & 3) + (l & 31), g2 = l >> 5, mb = 32 * MT * (wave >> 2);
-    if (col < N) {
+};
+
+template <class F, int BM, int NW, int NS, int S, class Dec>
+__device__ __forceinline__ void kq_stream_step(KQStream<F, BM, NW, Dec>& st, uint8_t* const (&stages)[KQ_MAX_NS],
+                                               int h, int G, float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    using L = KQL<F, BM, NW>;
+    constexpr int MT = L::MTW;
+    if (h >= G) return;
+    if (h + NS - 2 < G) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (h + NS - 1 < G) st.issue_next(stages[(S + NS - 1) % NS]);
+    kq_compute<F, BM, NW>(stages[S], st.cb, st.wave, st.l, acc);
+    if (++st.cb == st.nsb) {
+        kq_store<F, BM, NW>(acc, st.cT.Y, st.cT.count, st.N, st.cT.m0, st.cT.n0, st.wave, st.l);
         #pragma unroll
         for (int t = 0; t < MT; t++)
             #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + mb + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (row < count) Y[(size_t)row * N + col] = acc[t][r];
-            }
+            for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+        st.cb = 0;
+        st.ct += st.grid;
+        if (st.ct < st.total) st.cT = st.decode(st.ct);
     }
+}
+
+template <class F, int BM, int NW, int NS, class Dec, int... S>
+__device__ __forceinline__ void kq_stream_round(std::integer_sequence<int, S...>, KQStream<F, BM, NW, Dec>& st,
+                                                uint8_t* const (&stages)[KQ_MAX_NS], int g, int G,
+                                                float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    (kq_stream_step<F, BM, NW, NS, S>(st, stages, g + S, G, acc), ...);
+}
+
+template <class F, int BM, int NS, int NW, class Dec>
+__device__ __forceinline__ void kq_grouped_stream(uint8_t* const (&stages)[KQ_MAX_NS], const Dec& decode, int total,
+                                                  int nsb, uint32_t xrb, uint32_t wrb, int N, int wave, int l) {
+    using L = KQL<F, BM, NW>;
+    constexpr int MT = L::MTW;
+    const int t0 = blockIdx.x, grid = gridDim.x;
+    if (t0 >= total) return;
+    const int G = ((total - 1 - t0) / grid + 1) * nsb;   // this workgroup's steps
+    KQStream<F, BM, NW, Dec> st{decode, total, grid, nsb, N, xrb, wrb, {}, wave, l, t0, 0, {}, {}, t0, 0, {}};
+    kq_offsets<F, BM, NW>(st.off, xrb, wrb, wave, l);
+    st.cT = decode(t0);
+    kq_tile_rsrc<F>(st.cT, xrb, wrb, N, st.lxr, st.lwr);
+    #pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < G) st.issue_next(stages[s]);
+    float acc[MT][16];
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+    for (int g = 0; g < G; g += NS)
+        kq_stream_round<F, BM, NW, NS>(std::make_integer_sequence<int, NS>{}, st, stages, g, G, acc);
 }
 
 // Ungrouped: one tile per workgroup of the M x N product with weights wt.w[0].
@@ -551,19 +668,23 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
         const int s_total = __builtin_amdgcn_readfirstlane(__shfl(inc, 63));
         const int total = s_total * nmat * ks * tiles_n;
         const int nsb_k = nsb / ks;
-        for (int t = blockIdx.x; t < total; t += gridDim.x) {
+        auto decode = [&](int t) {
             const int ntile = t % tiles_n, rk = t / tiles_n, ksl = rk % ks, r = rk / ks, mat = r % nmat, s = r / nmat;
             // expert of m-slot s: the number of experts whose tiles all lie before it
             const int e = __builtin_amdgcn_readfirstlane(__popcll(__ballot(inc <= s)));
             const int mt = s - __builtin_amdgcn_readfirstlane(__shfl(inc - nt, e));
             const int row0 = __builtin_amdgcn_readfirstlane(__shfl(r0, e));
-            const int count = __builtin_amdgcn_readfirstlane(__shfl(cnt, e));
-            // the previous tile's last stages have been read by every wave
-            if (t != (int)blockIdx.x) __builtin_amdgcn_s_barrier();
-            kq_tile<F, BM, NS, NW>(stages, wt.w[mat * ne + e], wrb, X + (size_t)row0 * xrb, xrb,
-                                   Y + (size_t)mat * ymat + (size_t)ksl * ykstride + (size_t)row0 * N, count, N, nsb_k,
-                                   mt * BM, ntile * KQ_BN, wave, l, ksl * nsb_k);
-        }
+            KQTile T;
+            T.W = wt.w[mat * ne + e];
+            T.X = X + (size_t)row0 * xrb;
+            T.Y = Y + (size_t)mat * ymat + (size_t)ksl * ykstride + (size_t)row0 * N;
+            T.count = __builtin_amdgcn_readfirstlane(__shfl(cnt, e));
+            T.m0 = mt * BM;
+            T.n0 = ntile * KQ_BN;
+            T.kb0 = ksl * nsb_k;
+            return T;
+        };
+        kq_grouped_stream<F, BM, NS, NW>(stages, decode, total, nsb_k, xrb, wrb, N, wave, l);
     }
 }
 
