@@ -65,6 +65,7 @@ struct KQL {
     static constexpr int X_INSTR = (X_INSTR_ALL + NW - 1) / NW;
     static constexpr int W_INSTR = (W_INSTR_ALL + NW - 1) / NW;
     static constexpr int LOADS_MIN = X_INSTR_ALL / NW + W_INSTR_ALL / NW;
+    static constexpr int LOADS_MIN_W = W_INSTR_ALL / NW;   // when activation loads may be skipped
     // 32x32 MFMA row tiles per wave; 16-row tiles use the 16x16 path (two column blocks per wave)
     static constexpr int MTW = BM >= 32 ? BM / 32 / (NW / 4) : 1;
     static_assert(KQ_BN * F::PIECES % 64 == 0, "weight tile is whole load instructions");
@@ -94,15 +95,18 @@ __device__ __forceinline__ void kq_offsets(KQOff<F, BM, NW>& o, uint32_t xrb, ui
     o.xd = (uint32_t)(64 * wave + l) * xrb;
 }
 
+// x_instr: activation load instructions to issue (fewer when the tile has
+// fewer rows; the rows left out keep stale bytes whose results are never
+// stored, and their dx loads as zero).
 template <class F, int BM, int NW>
 __device__ __forceinline__ void kq_issue(uint8_t* stage, i32x4v xr, i32x4v wr, const KQOff<F, BM, NW>& o, int b,
-                                         int wave) {
+                                         int wave, int x_instr = KQL<F, BM, NW>::X_INSTR_ALL) {
     using L = KQL<F, BM, NW>;
     const uint32_t xs = (uint32_t)b * Q8_K_BYTES, ws = F::soff(b);
     #pragma unroll
     for (int q = 0; q < L::X_INSTR; q++) {
         const int idx = q * NW + wave;
-        if (idx < L::X_INSTR_ALL) lds_load16(xr, stage + L::XQ + 1024 * idx, o.x[q], xs);
+        if (idx < x_instr) lds_load16(xr, stage + L::XQ + 1024 * idx, o.x[q], xs);
     }
     #pragma unroll
     for (int q = 0; q < L::W_INSTR; q++) {
@@ -431,33 +435,37 @@ __device__ __forceinline__ void kq_compute(const uint8_t* st, int b, int wave, i
 // s_barrier (no memory fence) does not drain the in-flight stages.
 constexpr int KQ_MAX_NS = 6;
 
-template <class F, int BM, int NW, int NS, int S>
-__device__ __forceinline__ void kq_step(uint8_t* const (&stages)[KQ_MAX_NS], int b, int nsb, i32x4v xr, i32x4v wr,
-                                        const KQOff<F, BM, NW>& off, int wave, int l,
+// With KG K-groups a stage holds KG consecutive super-blocks, one per group:
+// group kg (its own NW waves, `wave` counted within the group) loads and
+// computes super-block KG * b + kg of step b.
+template <class F, int BM, int NW, int NS, int KG, int S>
+__device__ __forceinline__ void kq_step(uint8_t* const (&stages)[KQ_MAX_NS], int b, int nst, i32x4v xr, i32x4v wr,
+                                        const KQOff<F, BM, NW>& off, int kg, int wave, int l,
                                         float (&acc)[KQL<F, BM, NW>::MTW][16]) {
     using L = KQL<F, BM, NW>;
-    constexpr int MT = L::MTW;
-    if (b >= nsb) return;
-    // this thread's loads of super-block b are done once at most the later
+    if (b >= nst) return;
+    // this thread's loads of step b are done once at most the later
     // stages' loads are outstanding; every thread's are after the barrier
-    if (b + NS - 2 < nsb) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
+    if (b + NS - 2 < nst) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
     else wait_vmcnt<0>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (b + NS - 1 < nsb) kq_issue<F, BM, NW>(stages[(S + NS - 1) % NS], xr, wr, off, b + NS - 1, wave);
-    kq_compute<F, BM, NW>(stages[S], b, wave, l, acc);
+    const int sub = kg * L::STAGE;
+    if (b + NS - 1 < nst)
+        kq_issue<F, BM, NW>(stages[(S + NS - 1) % NS] + sub, xr, wr, off, KG * (b + NS - 1) + kg, wave);
+    kq_compute<F, BM, NW>(stages[S] + sub, KG * b + kg, wave, l, acc);
 }
 
 // One BM x 128 output tile: rows [m0, m0 + BM) of the `count` activation rows
 // at X (row bytes xrb) against weight rows [n0, n0 + 128) of W; results to
 // Y[row * N + col].  All waves of the workgroup call it with the same values.
 // NS consecutive steps (one per stage), unrolled so that stage indices are constants
-template <class F, int BM, int NW, int NS, int... S>
+template <class F, int BM, int NW, int NS, int KG, int... S>
 __device__ __forceinline__ void kq_round(std::integer_sequence<int, S...>, uint8_t* const (&stages)[KQ_MAX_NS], int b,
-                                         int nsb, i32x4v xr, i32x4v wr, const KQOff<F, BM, NW>& off, int wave, int l,
-                                         float (&acc)[KQL<F, BM, NW>::MTW][16]) {
-    (kq_step<F, BM, NW, NS, S>(stages, b + S, nsb, xr, wr, off, wave, l, acc), ...);
+                                         int nst, i32x4v xr, i32x4v wr, const KQOff<F, BM, NW>& off, int kg, int wave,
+                                         int l, float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    (kq_step<F, BM, NW, NS, KG, S>(stages, b + S, nst, xr, wr, off, kg, wave, l, acc), ...);
 }
 
 // Tile results to Y[row * N + col] for rows < count and columns < N.
@@ -491,12 +499,41 @@ __device__ __forceinline__ void kq_store(const float (&acc)[KQL<F, BM, NW>::MTW]
     }
 }
 
-template <class F, int BM, int NS, int NW>
+// K-group kg > 0 hands its partial sums to group 0 through LDS (stage 0,
+// free once every wave has passed the first barrier); group 0 adds them in
+// group order.
+template <class F, int BM, int NW, int KG>
+__device__ __forceinline__ void kq_reduce_groups(uint8_t* lds, float (&acc)[KQL<F, BM, NW>::MTW][16], int kg, int wave,
+                                                 int l) {
+    constexpr int MT = KQL<F, BM, NW>::MTW, LANES = 64 * NW;
+    static_assert((KG - 1) * MT * 16 * LANES * 4 <= KG * KQL<F, BM, NW>::STAGE, "reduction fits stage 0");
+    float* red = reinterpret_cast<float*>(lds);
+    const int lane = 64 * wave + l;
+    __syncthreads();
+    if (kg > 0) {
+        #pragma unroll
+        for (int t = 0; t < MT; t++)
+            #pragma unroll
+            for (int r = 0; r < 16; r++) red[((kg - 1) * MT * 16 + 16 * t + r) * LANES + lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (kg == 0) {
+        #pragma unroll
+        for (int g = 1; g < KG; g++)
+            #pragma unroll
+            for (int t = 0; t < MT; t++)
+                #pragma unroll
+                for (int r = 0; r < 16; r++) acc[t][r] += red[((g - 1) * MT * 16 + 16 * t + r) * LANES + lane];
+    }
+}
+
+template <class F, int BM, int NS, int NW, int KG>
 __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], const uint8_t* W, uint32_t wrb, const uint8_t* X,
-                                        uint32_t xrb, float* Y, int count, int N, int nsb, int m0, int n0, int wave,
-                                        int l, int kb0 = 0) {
+                                        uint32_t xrb, float* Y, int count, int N, int nsb, int m0, int n0, int kg,
+                                        int wave, int l, int kb0 = 0) {
     using L = KQL<F, BM, NW>;
     constexpr int MT = L::MTW;
+    const int nst = nsb / KG;   // steps (nsb is a multiple of KG)
     // super-blocks [kb0, kb0 + nsb) of each row (kb0 even: Q6_K windows keep their parity)
     const uint32_t xk = (uint32_t)kb0 * Q8_K_BYTES, wk = (uint32_t)kb0 * F::BB;
     const i32x4v xr = make_rsrc4(X + (size_t)m0 * xrb + xk, (uint32_t)((size_t)(count - m0) * xrb) - xk);
@@ -512,11 +549,13 @@ __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], con
     kq_offsets<F, BM, NW>(off, xrb, wrb, wave, l);
     #pragma unroll
     for (int s = 0; s < NS - 1; s++)
-        if (s < nsb) kq_issue<F, BM, NW>(stages[s], xr, wr, off, s, wave);
-    for (int b = 0; b < nsb; b += NS)
-        kq_round<F, BM, NW, NS>(std::make_integer_sequence<int, NS>{}, stages, b, nsb, xr, wr, off, wave, l, acc);
+        if (s < nst) kq_issue<F, BM, NW>(stages[s] + kg * L::STAGE, xr, wr, off, KG * s + kg, wave);
+    for (int b = 0; b < nst; b += NS)
+        kq_round<F, BM, NW, NS, KG>(std::make_integer_sequence<int, NS>{}, stages, b, nst, xr, wr, off, kg, wave, l,
+                                    acc);
 
-    kq_store<F, BM, NW>(acc, Y, count, N, m0, n0, wave, l);
+    if constexpr (KG > 1) kq_reduce_groups<F, BM, NW, KG>(stages[0], acc, kg, wave, l);
+    if (kg == 0) kq_store<F, BM, NW>(acc, Y, count, N, m0, n0, wave, l);
 }
 
 // ---- grouped: one pipeline across the workgroup's tiles ------------------------
@@ -547,18 +586,24 @@ struct KQStream {
     KQOff<F, BM, NW> off;
     int wave, l;
     // load cursor
-    int lt, lb;
+    int lt, lb, lxi;
     i32x4v lxr, lwr;
     // compute cursor
     int ct, cb;
     KQTile cT;
 
+    __device__ __forceinline__ void set_load_tile(const KQTile& t) {
+        kq_tile_rsrc<F>(t, xrb, wrb, N, lxr, lwr);
+        const int rows = t.count - t.m0 < BM ? t.count - t.m0 : BM;
+        const int xi = (rows * F::XC + 63) / 64;
+        lxi = xi < KQL<F, BM, NW>::X_INSTR_ALL ? xi : KQL<F, BM, NW>::X_INSTR_ALL;
+    }
     __device__ __forceinline__ void issue_next(uint8_t* stage) {
-        kq_issue<F, BM, NW>(stage, lxr, lwr, off, lb, wave);
+        kq_issue<F, BM, NW>(stage, lxr, lwr, off, lb, wave, lxi);
         if (++lb == nsb) {
             lb = 0;
             lt += grid;
-            if (lt < total) kq_tile_rsrc<F>(decode(lt), xrb, wrb, N, lxr, lwr);
+            if (lt < total) set_load_tile(decode(lt));
         }
     }
 };
@@ -569,7 +614,8 @@ __device__ __forceinline__ void kq_stream_step(KQStream<F, BM, NW, Dec>& st, uin
     using L = KQL<F, BM, NW>;
     constexpr int MT = L::MTW;
     if (h >= G) return;
-    if (h + NS - 2 < G) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
+    // stages may skip activation loads: count only the weight loads
+    if (h + NS - 2 < G) wait_vmcnt<(NS - 2) * L::LOADS_MIN_W>();
     else wait_vmcnt<0>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -603,10 +649,10 @@ __device__ __forceinline__ void kq_grouped_stream(uint8_t* const (&stages)[KQ_MA
     const int t0 = blockIdx.x, grid = gridDim.x;
     if (t0 >= total) return;
     const int G = ((total - 1 - t0) / grid + 1) * nsb;   // this workgroup's steps
-    KQStream<F, BM, NW, Dec> st{decode, total, grid, nsb, N, xrb, wrb, {}, wave, l, t0, 0, {}, {}, t0, 0, {}};
+    KQStream<F, BM, NW, Dec> st{decode, total, grid, nsb, N, xrb, wrb, {}, wave, l, t0, 0, 0, {}, {}, t0, 0, {}};
     kq_offsets<F, BM, NW>(st.off, xrb, wrb, wave, l);
     st.cT = decode(t0);
-    kq_tile_rsrc<F>(st.cT, xrb, wrb, N, st.lxr, st.lwr);
+    st.set_load_tile(st.cT);
     #pragma unroll
     for (int s = 0; s < NS - 1; s++)
         if (s < G) st.issue_next(stages[s]);
@@ -626,23 +672,26 @@ __device__ __forceinline__ void kq_grouped_stream(uint8_t* const (&stages)[KQ_MA
 // there: every workgroup builds the per-expert tile prefix from the device
 // offsets (lane e holds expert e) and strides over the flattened
 // (expert, m-tile, mat, n-tile) list, so no host round trip is needed.
-template <class F, int BM, int NS, int NW, bool GROUPED>
-__global__ __launch_bounds__(64 * NW, 1)
+template <class F, int BM, int NS, int NW, int KG, bool GROUPED>
+__global__ __launch_bounds__(64 * NW * KG, 1)
 void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb, float* __restrict__ Y, int M,
                int N, int nsb, int tiles_m, int tiles_n, const int32_t* __restrict__ offsets, int ne, int nmat,
                size_t ymat, int ks, size_t ykstride, int xcd_order) {
     static_assert(NS >= 2 && NS <= KQ_MAX_NS, "stage count");
+    static_assert(KG == 1 || !GROUPED, "K-groups split one tile's super-blocks (ungrouped launches)");
     using L = KQL<F, BM, NW>;
+    constexpr int SB = KG * L::STAGE;
     // one array per stage (stages beyond NS are unused 16-byte stubs)
-    __shared__ __align__(16) uint8_t st0[L::STAGE];
-    __shared__ __align__(16) uint8_t st1[L::STAGE];
-    __shared__ __align__(16) uint8_t st2[L::STAGE];
-    __shared__ __align__(16) uint8_t st3[NS > 3 ? L::STAGE : 16];
-    __shared__ __align__(16) uint8_t st4[NS > 4 ? L::STAGE : 16];
-    __shared__ __align__(16) uint8_t st5[NS > 5 ? L::STAGE : 16];
+    __shared__ __align__(16) uint8_t st0[SB];
+    __shared__ __align__(16) uint8_t st1[SB];
+    __shared__ __align__(16) uint8_t st2[NS > 2 ? SB : 16];
+    __shared__ __align__(16) uint8_t st3[NS > 3 ? SB : 16];
+    __shared__ __align__(16) uint8_t st4[NS > 4 ? SB : 16];
+    __shared__ __align__(16) uint8_t st5[NS > 5 ? SB : 16];
     uint8_t* const stages[KQ_MAX_NS] = {st0, st1, st2, st3, st4, st5};
     const int l = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kg = wave_all / NW, wave = wave_all - kg * NW;
 
     if constexpr (!GROUPED) {
         // workgroup i runs on XCD i % 8: give each XCD a contiguous run of
@@ -651,7 +700,7 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
         int tile = blockIdx.x;
         if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
         const int mt = tile % tiles_m, ntile = tile / tiles_m;
-        kq_tile<F, BM, NS, NW>(stages, wt.w[0], wrb, X, xrb, Y, M, N, nsb, mt * BM, ntile * KQ_BN, wave, l);
+        kq_tile<F, BM, NS, NW, KG>(stages, wt.w[0], wrb, X, xrb, Y, M, N, nsb, mt * BM, ntile * KQ_BN, kg, wave, l);
     } else {
         int r0 = 0, cnt = 0;
         if (l < ne) {
@@ -722,7 +771,7 @@ struct KQArgs {
     size_t ykstride;
 };
 
-template <class F, int BM, int NS, int NW, bool GROUPED>
+template <class F, int BM, int NS, int NW, bool GROUPED, int KG = 1>
 static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     const int tiles_n = (a.N + KQ_BN - 1) / KQ_BN;
     int tiles_m = (a.M + BM - 1) / BM;
@@ -736,7 +785,8 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
         grid = (unsigned)(tiles < cap ? tiles : cap);
         tiles_m = 0;
     }
-    hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, GROUPED>), dim3(grid), dim3(64 * NW), 0, s, a.wt, a.wrb, a.X, a.xrb,
+    if (a.nsb % KG != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, KG, GROUPED>), dim3(grid), dim3(64 * NW * KG), 0, s, a.wt, a.wrb, a.X, a.xrb,
                        a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, a.ks, a.ykstride,
                        g_kq_xcd);
     return hipGetLastError();
@@ -744,6 +794,7 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
 
 static const int g_kq_ns = kq_env("BARQ_GEMM_NS", 0);   // stage-count override for tuning
 static const int g_kq_ks = kq_env("BARQ_GEMM_KS", 0);   // K-slice override for grouped launches (tuning)
+static const int g_kq_kg = kq_env("BARQ_GEMM_KG", 0);   // K-group override for ungrouped launches (tuning)
 
 // rows: M (ungrouped) or the expected rows per expert (grouped).  Stage
 // counts are the most that fit the 160 KiB of LDS (deeper pipelines keep
@@ -761,6 +812,19 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // 32-row tiles: two stages per workgroup and two workgroups per CU for
     // expert groups (measured best for C5), the deepest pipeline otherwise
     const int ns = g_kq_ns ? g_kq_ns : (GROUPED ? 2 : 0);
+    if constexpr (!GROUPED) {
+        // two K-groups of waves share a tile's pipeline (twice the waves per
+        // SIMD for the same LDS) when the super-block count is even
+        const int kg = g_kq_kg ? g_kq_kg : 2;
+        if (kg == 2 && a.nsb % 2 == 0) {
+            if constexpr (F::TYPE == TYPE_Q4_K) {
+                if (bm == 65) return kq_launch_t<F, 64, 2, 8, GROUPED, 2>(a, s);
+                return kq_launch_t<F, 32, 2, 4, GROUPED, 2>(a, s);
+            } else {
+                return kq_launch_t<F, 32, 2, 4, GROUPED, 2>(a, s);
+            }
+        }
+    }
     if constexpr (F::TYPE == TYPE_Q4_K) {
         if (bm == 65) return kq_launch_t<F, 64, 4, 8, GROUPED>(a, s);
         if (ns == 2) return kq_launch_t<F, 32, 2, 4, GROUPED>(a, s);
