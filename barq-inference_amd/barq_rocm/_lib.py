@@ -59,7 +59,13 @@ EXPORTS = (
     "barq_rocm_gguf_tensor", "barq_rocm_gguf_find_tensor", "barq_rocm_gguf_kv_type", "barq_rocm_gguf_kv_int",
     "barq_rocm_gguf_kv_number", "barq_rocm_gguf_kv_string", "barq_rocm_cache_create", "barq_rocm_cache_get",
     "barq_rocm_cache_bytes", "barq_rocm_cache_destroy",
+    "barq_rocm_rope", "barq_rocm_transpose_heads", "barq_rocm_kv_cache_create", "barq_rocm_kv_cache_append",
+    "barq_rocm_kv_cache_append_rope", "barq_rocm_kv_cache_size", "barq_rocm_kv_cache_layer_len",
+    "barq_rocm_kv_cache_head", "barq_rocm_kv_cache_clear", "barq_rocm_kv_cache_destroy", "barq_rocm_attention",
 )
+
+ROPE_INTERLEAVED = 0
+ROPE_SPLIT_HALF = 1
 
 
 class BarqError(RuntimeError):
@@ -120,6 +126,17 @@ def _declare(lib):
                                      ctypes.POINTER(_u64), ctypes.POINTER(_vp)]),
         "barq_rocm_cache_bytes": (_u64, [_vp]),
         "barq_rocm_cache_destroy": (_i, [_vp]),
+        "barq_rocm_rope": (_i, [_vp, _vp, _sz, _sz, _sz, _sz, ctypes.c_float, _vp, _i, _vp, _i]),
+        "barq_rocm_transpose_heads": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _i]),
+        "barq_rocm_kv_cache_create": (_i, [_vp, _sz, _sz, _sz, _sz, ctypes.POINTER(_vp)]),
+        "barq_rocm_kv_cache_append": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _i]),
+        "barq_rocm_kv_cache_append_rope": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i, _i]),
+        "barq_rocm_kv_cache_size": (_sz, [_vp]),
+        "barq_rocm_kv_cache_layer_len": (_sz, [_vp, _sz]),
+        "barq_rocm_kv_cache_head": (_i, [_vp, _sz, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
+        "barq_rocm_kv_cache_clear": (_i, [_vp]),
+        "barq_rocm_kv_cache_destroy": (_i, [_vp]),
+        "barq_rocm_attention": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _i]),
     }
     for name, (res, args) in P.items():
         fn = getattr(lib, name)

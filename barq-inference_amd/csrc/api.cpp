@@ -33,18 +33,6 @@ using barq_api::DeviceGuard;
 using barq_api::fail;
 using barq_api::ok;
 
-#define BARQ_HIP(expr)                                                                          \
-    do {                                                                                        \
-        hipError_t e_ = (expr);                                                                 \
-        if (e_ != hipSuccess) return fail(BARQ_E_BACKEND, "%s: %s", #expr, hipGetErrorString(e_)); \
-    } while (0)
-
-#define BARQ_CHECK(rc_expr)          \
-    do {                             \
-        int rc_ = (rc_expr);         \
-        if (rc_ != BARQ_OK) return rc_; \
-    } while (0)
-
 bool is_weight_type(int t) {
     return t == BARQ_TYPE_Q4_0 || t == BARQ_TYPE_Q8_0 || t == BARQ_TYPE_Q4_K || t == BARQ_TYPE_Q6_K ||
            t == BARQ_TYPE_Q4_0_BARQ;
@@ -83,8 +71,6 @@ size_t row_bytes_of(int t, size_t k) {
     return k / be * blk_bytes(t);
 }
 
-bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-
 // alignment the kernels need for a packed weight / activation buffer
 size_t weight_align(int t) {
     switch (t) {
@@ -94,7 +80,9 @@ size_t weight_align(int t) {
     }
 }
 
-int ensure_ws(barq_rocm_handle* h, size_t bytes) {
+}  // namespace
+
+int barq_api::ensure_ws(barq_rocm_handle* h, size_t bytes) {
     if (bytes <= h->ws_size) return ok();
     if (h->ws) {
         BARQ_HIP(hipStreamSynchronize(h->stream));
@@ -112,39 +100,9 @@ int ensure_ws(barq_rocm_handle* h, size_t bytes) {
     return ok();
 }
 
-size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+namespace {
 
-// Carves 256-byte aligned slices out of the workspace.
-struct Arena {
-    size_t used = 0;
-    std::vector<std::pair<size_t, size_t>> parts;  // offset, size
-    size_t add(size_t bytes) {
-        size_t off = used;
-        used = round_up(used + bytes, 256);
-        parts.push_back({off, bytes});
-        return off;
-    }
-};
-
-template <class T>
-T* at(barq_rocm_handle* h, size_t off) {
-    return reinterpret_cast<T*>(static_cast<uint8_t*>(h->ws) + off);
-}
-
-int check_handle(barq_rocm_handle* h) {
-    if (!h) return fail(BARQ_E_INVALID, "null handle");
-    return ok();
-}
-
-int check_mem(int mem) {
-    if (mem != BARQ_MEM_HOST && mem != BARQ_MEM_DEVICE) return fail(BARQ_E_INVALID, "mem must be BARQ_MEM_HOST or BARQ_MEM_DEVICE");
-    return ok();
-}
-
-int launched(hipError_t e, const char* what) {
-    if (e != hipSuccess) return fail(BARQ_E_BACKEND, "%s launch: %s", what, hipGetErrorString(e));
-    return ok();
-}
+using namespace barq_api;
 
 constexpr size_t LDS_LIMIT = 64 * 1024;
 

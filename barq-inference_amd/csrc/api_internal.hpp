@@ -1,10 +1,12 @@
-// Internals shared by the C ABI translation units (api.cpp, gguf.cpp).
+// Internals shared by the C ABI translation units (api.cpp, gguf.cpp,
+// attention.cpp).
 #pragma once
 #include "../../include/barq_rocm.h"
 
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <cstdint>
 
 struct barq_rocm_handle {
     int device = 0;
@@ -19,6 +21,55 @@ namespace barq_api {
 // Records the thread's last error message and returns code.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 inline int ok() { return BARQ_OK; }
+
+#define BARQ_HIP(expr)                                                                          \
+    do {                                                                                        \
+        hipError_t e_ = (expr);                                                                 \
+        if (e_ != hipSuccess) return barq_api::fail(BARQ_E_BACKEND, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define BARQ_CHECK(rc_expr)             \
+    do {                                \
+        int rc_ = (rc_expr);            \
+        if (rc_ != BARQ_OK) return rc_; \
+    } while (0)
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Grows the handle's device workspace to at least `bytes` (waiting for the
+// stream before a reallocation).
+int ensure_ws(barq_rocm_handle* h, size_t bytes);
+
+// Carves 256-byte aligned slices out of the workspace.
+struct Arena {
+    size_t used = 0;
+    size_t add(size_t bytes) {
+        const size_t off = used;
+        used = round_up(used + bytes, 256);
+        return off;
+    }
+};
+
+template <class T>
+T* at(barq_rocm_handle* h, size_t off) {
+    return reinterpret_cast<T*>(static_cast<uint8_t*>(h->ws) + off);
+}
+
+inline int check_handle(barq_rocm_handle* h) {
+    if (!h) return fail(BARQ_E_INVALID, "null handle");
+    return ok();
+}
+
+inline int check_mem(int mem) {
+    if (mem != BARQ_MEM_HOST && mem != BARQ_MEM_DEVICE) return fail(BARQ_E_INVALID, "mem must be BARQ_MEM_HOST or BARQ_MEM_DEVICE");
+    return ok();
+}
+
+inline int launched(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(BARQ_E_BACKEND, "%s launch: %s", what, hipGetErrorString(e));
+    return ok();
+}
 
 // Make the handle's device current for the duration of a call.
 struct DeviceGuard {

@@ -1,0 +1,314 @@
+// Attention on device: RoPE, head transpose, the KV-cache copy and the
+// attention kernel of a LlamaTransformer layer.
+//
+//   apply_rope      models/src/transformer.rs:514-562 (Interleaved / SplitHalf)
+//   transpose_heads models/src/transformer.rs:598-611
+//   compute_attention models/src/transformer.rs:301-374:
+//     kv_h = h * n_head_kv / n_head                                (:318)
+//     score_j = (q . K[j]) * (1 / sqrt(head_dim))                  (:311,327-335)
+//     score_j = -inf for j >= start_pos + i + 1                    (:337-342)
+//     p = softmax(score); out[i, h, :] = sum_j p_j V[j, :]        (:344-356)
+//
+// Layouts (the reference's): q is [n_head, q_len, head_dim] (apply_rope's
+// output); the cache holds, per layer and kv head, positions x head_dim
+// contiguous (KVCache, models/src/context.rs:245-340), here preallocated to
+// max_size positions; out is [q_len, n_head, head_dim].
+//
+// The attention kernel streams K and V rows from HBM once per kv head for all
+// the query heads that share it (GQA), split over the positions so that
+// enough workgroups run: a row of head_dim floats is read by head_dim / 8
+// lanes (two float4 each), every lane keeps its own online-softmax state
+// (running max, sum, and its 8 output dims) for each query head, and the
+// states are merged in LDS and then across splits.  Exponentials are base 2
+// on scores pre-scaled by log2(e) (v_exp_f32), so the weights agree with the
+// reference's expf to a few ulp, not bit for bit; sums run in a different
+// order from the reference's sequential ones.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace barq {
+
+// ---- RoPE / transpose ----------------------------------------------------------
+// One thread per (position, head, pair).  out[h * out_head_stride + p * hd + ...]
+// so that the rotated rows can go straight into a cache.
+template <int LAYOUT>
+__global__ __launch_bounds__(256)
+void rope_kernel(const float* __restrict__ x, float* __restrict__ out, int seq, int heads, int hd, long long start_pos,
+                 float freq_scale, const float* __restrict__ inv_freq, size_t out_head_stride) {
+    const int half = hd / 2;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)seq * heads * half) return;
+    const int i = (int)(t % half);
+    const size_t ph = t / half;
+    const int h = (int)(ph % heads), p = (int)(ph / heads);
+    // (abs_pos as f32 * rope_freq_scale) * rope_inv_freq[i]
+    const float angle = ((float)(start_pos + p) * freq_scale) * inv_freq[i];
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    const float* src = x + ((size_t)p * heads + h) * hd;
+    float* dst = out + (size_t)h * out_head_stride + (size_t)p * hd;
+    const int i0 = LAYOUT == ROPE_INTERLEAVED ? 2 * i : i;
+    const int i1 = LAYOUT == ROPE_INTERLEAVED ? 2 * i + 1 : i + half;
+    const float x0 = src[i0], x1 = src[i1];
+    dst[i0] = x0 * cs - x1 * sn;
+    dst[i1] = x0 * sn + x1 * cs;
+}
+
+__global__ __launch_bounds__(256)
+void transpose_heads_kernel(const float* __restrict__ x, float* __restrict__ out, int seq, int heads, int hd,
+                            size_t out_head_stride) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)seq * heads * hd) return;
+    const int d = (int)(t % hd);
+    const size_t ph = t / hd;
+    const int h = (int)(ph % heads), p = (int)(ph / heads);
+    out[(size_t)h * out_head_stride + (size_t)p * hd + d] = x[t];
+}
+
+hipError_t rope_launch(int layout, const float* x, float* out, size_t seq, size_t heads, size_t hd, size_t start_pos,
+                       float freq_scale, const float* inv_freq, size_t out_head_stride, hipStream_t s) {
+    const size_t n = seq * heads * (hd / 2);
+    if (n == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (layout == ROPE_INTERLEAVED)
+        hipLaunchKernelGGL(rope_kernel<ROPE_INTERLEAVED>, dim3(grid), dim3(256), 0, s, x, out, (int)seq, (int)heads,
+                           (int)hd, (long long)start_pos, freq_scale, inv_freq, out_head_stride);
+    else
+        hipLaunchKernelGGL(rope_kernel<ROPE_SPLIT_HALF>, dim3(grid), dim3(256), 0, s, x, out, (int)seq, (int)heads,
+                           (int)hd, (long long)start_pos, freq_scale, inv_freq, out_head_stride);
+    return hipGetLastError();
+}
+
+hipError_t transpose_heads_launch(const float* x, float* out, size_t seq, size_t heads, size_t hd,
+                                  size_t out_head_stride, hipStream_t s) {
+    const size_t n = seq * heads * hd;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(transpose_heads_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, out, (int)seq,
+                       (int)heads, (int)hd, out_head_stride);
+    return hipGetLastError();
+}
+
+// ---- attention -----------------------------------------------------------------
+constexpr int ATT_THREADS = 256;
+constexpr float LOG2E = 1.44269504088896340736f;
+
+// Sum over aligned groups of N lanes (N = 8, 16 or 32); every lane of the
+// group gets the sum.  Within a row of 16 lanes: quad swaps, then the
+// half-row and row mirrors; across two rows: a 16-lane xor.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    if constexpr (N >= 16)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    if constexpr (N >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Partial state of one (query row, head, split): running max m (log2 units),
+// sum l, then HD output sums.  Stored as HD + 2 floats.
+//
+// Grid: x = split, y = head group (kv head for G > 1; query head for G == 1),
+// z = query row i.  The workgroup covers positions [split * chunk, ...) of
+// the visible prefix [0, min(kv_len, start_pos + i + 1)).
+template <int HD, int G>
+__global__ __launch_bounds__(ATT_THREADS)
+void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+                 size_t layer_off, size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
+                 long long start_pos, int chunk, float score_scale, float* __restrict__ part, float* __restrict__ out) {
+    constexpr int LPR = HD / 8;              // lanes per K/V row
+    constexpr int R = ATT_THREADS / LPR;     // rows per pass
+    static_assert(LPR == 8 || LPR == 16 || LPR == 32, "head_dim 64, 128 or 256");
+    __shared__ float red_o[R][G][HD];
+    __shared__ float red_ml[R][G][2];
+
+    const int t = threadIdx.x, c = t % LPR, r = t / LPR;
+    const int split = blockIdx.x, grp = blockIdx.y, i = blockIdx.z, n_split = gridDim.x;
+    const int hk = G > 1 ? grp : (int)((long long)grp * n_head_kv / n_head);
+    const long long vis = start_pos + i + 1;
+    const int valid = (int)(vis < kv_len ? vis : kv_len);
+    const int j0 = split * chunk, j1 = min(valid, j0 + chunk);
+
+    // query rows of the group's heads (pre-scaled: score * log2e is the exponent)
+    float qv[G][8];
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int h = G > 1 ? grp * G + g : grp;
+        const float4* qp = reinterpret_cast<const float4*>(q + ((size_t)h * q_len + i) * HD + 8 * c);
+        const float4 a = qp[0], b = qp[1];
+        qv[g][0] = a.x; qv[g][1] = a.y; qv[g][2] = a.z; qv[g][3] = a.w;
+        qv[g][4] = b.x; qv[g][5] = b.y; qv[g][6] = b.z; qv[g][7] = b.w;
+    }
+    float m[G], l[G], o[G][8];
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+        #pragma unroll
+        for (int d = 0; d < 8; d++) o[g][d] = 0.0f;
+    }
+
+    const float* kh = kc + layer_off + (size_t)hk * head_stride + 8 * c;
+    const float* vh = vc + layer_off + (size_t)hk * head_stride + 8 * c;
+    for (int base = j0; base < j1; base += R) {
+        const int j = base + r;
+        const bool live = j < j1;
+        float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
+        if (live) {
+            const float4* kp = reinterpret_cast<const float4*>(kh + (size_t)j * HD);
+            const float4* vp = reinterpret_cast<const float4*>(vh + (size_t)j * HD);
+            k0 = kp[0]; k1 = kp[1];
+            v0 = vp[0]; v1 = vp[1];
+        }
+        #pragma unroll
+        for (int g = 0; g < G; g++) {
+            float dot = qv[g][0] * k0.x;
+            dot = __builtin_fmaf(qv[g][1], k0.y, dot);
+            dot = __builtin_fmaf(qv[g][2], k0.z, dot);
+            dot = __builtin_fmaf(qv[g][3], k0.w, dot);
+            dot = __builtin_fmaf(qv[g][4], k1.x, dot);
+            dot = __builtin_fmaf(qv[g][5], k1.y, dot);
+            dot = __builtin_fmaf(qv[g][6], k1.z, dot);
+            dot = __builtin_fmaf(qv[g][7], k1.w, dot);
+            dot = group_sum<LPR>(dot);
+            if (live) {
+                const float s = dot * score_scale;          // (q . k) / sqrt(hd) * log2(e)
+                const float mn = fmaxf(m[g], s);
+                const float corr = fast_exp2(m[g] - mn);     // 0 while m is -inf
+                const float p = fast_exp2(s - mn);
+                m[g] = mn;
+                l[g] = __builtin_fmaf(l[g], corr, p);
+                o[g][0] = __builtin_fmaf(o[g][0], corr, p * v0.x);
+                o[g][1] = __builtin_fmaf(o[g][1], corr, p * v0.y);
+                o[g][2] = __builtin_fmaf(o[g][2], corr, p * v0.z);
+                o[g][3] = __builtin_fmaf(o[g][3], corr, p * v0.w);
+                o[g][4] = __builtin_fmaf(o[g][4], corr, p * v1.x);
+                o[g][5] = __builtin_fmaf(o[g][5], corr, p * v1.y);
+                o[g][6] = __builtin_fmaf(o[g][6], corr, p * v1.z);
+                o[g][7] = __builtin_fmaf(o[g][7], corr, p * v1.w);
+            }
+        }
+    }
+
+    // merge the R row states of the workgroup
+    #pragma unroll
+    for (int g = 0; g < G; g++) {
+        #pragma unroll
+        for (int d = 0; d < 8; d++) red_o[r][g][8 * c + d] = o[g][d];
+        if (c == 0) {
+            red_ml[r][g][0] = m[g];
+            red_ml[r][g][1] = l[g];
+        }
+    }
+    __syncthreads();
+    for (int e = t; e < G * HD; e += ATT_THREADS) {
+        const int g = e / HD, d = e % HD;
+        float M = -INFINITY;
+        for (int rr = 0; rr < R; rr++) M = fmaxf(M, red_ml[rr][g][0]);
+        float L = 0.0f, O = 0.0f;
+        if (M != -INFINITY) {
+            for (int rr = 0; rr < R; rr++) {
+                const float w = fast_exp2(red_ml[rr][g][0] - M);
+                L = __builtin_fmaf(red_ml[rr][g][1], w, L);
+                O = __builtin_fmaf(red_o[rr][g][d], w, O);
+            }
+        }
+        const int h = G > 1 ? grp * G + g : grp;
+        if (n_split == 1) {
+            out[((size_t)i * n_head + h) * HD + d] = O / L;
+        } else {
+            float* pp = part + (((size_t)i * n_head + h) * n_split + split) * (HD + 2);
+            pp[2 + d] = O;
+            if (d == 0) {
+                pp[0] = M;
+                pp[1] = L;
+            }
+        }
+    }
+}
+
+// out[i, h, :] from the n_split partial states of (i, h): one workgroup per
+// (h, i), one thread per output dim.
+__global__ __launch_bounds__(256)
+void attn_combine_kernel(const float* __restrict__ part, int n_split, int hd, int n_head, float* __restrict__ out) {
+    const int h = blockIdx.x, i = blockIdx.y, d = threadIdx.x;
+    if (d >= hd) return;
+    const float* pp = part + ((size_t)i * n_head + h) * n_split * (hd + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_split; s++) M = fmaxf(M, pp[(size_t)s * (hd + 2)]);
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < n_split; s++) {
+        const float* ps = pp + (size_t)s * (hd + 2);
+        if (ps[0] == -INFINITY) continue;
+        const float w = fast_exp2(ps[0] - M);
+        L = __builtin_fmaf(ps[1], w, L);
+        O = __builtin_fmaf(ps[2 + d], w, O);
+    }
+    out[((size_t)i * n_head + h) * hd + d] = O / L;
+}
+
+bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
+
+size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv) {
+    int ns = 0, chunk = 0;
+    attention_plan(n_head, n_head_kv, q_len, kv_len, &ns, &chunk);
+    return ns > 1 ? (size_t)ns * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
+}
+
+// Splits: about 1024 workgroups in all, at least 64 positions each.
+void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len, int* n_split, int* chunk) {
+    const size_t g = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
+    const size_t groups = (g == 1 || g > 8 || (g & (g - 1))) ? n_head : n_head_kv;
+    const size_t wg = groups * (q_len ? q_len : 1);
+    size_t ns = (1024 + wg - 1) / wg;
+    const size_t max_ns = (kv_len + 63) / 64;
+    if (ns > max_ns) ns = max_ns;
+    if (ns < 1) ns = 1;
+    size_t ch = (kv_len + ns - 1) / ns;
+    ch = (ch + 63) / 64 * 64;
+    ns = (kv_len + ch - 1) / ch;
+    if (ns < 1) ns = 1;
+    *n_split = (int)ns;
+    *chunk = (int)ch;
+}
+
+template <int HD, int G>
+static hipError_t attn_launch_t(const AttnArgs& a, int ns, int chunk, int groups, hipStream_t s) {
+    const float scale = (1.0f / sqrtf((float)HD)) * LOG2E;
+    hipLaunchKernelGGL((attn_kernel<HD, G>), dim3(ns, groups, (unsigned)a.q_len), dim3(ATT_THREADS), 0, s, a.q, a.k,
+                       a.v, a.layer_off, a.head_stride, (int)a.n_head, (int)a.n_head_kv, (int)a.q_len, (int)a.kv_len,
+                       (long long)a.start_pos, chunk, scale, a.part, a.out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ns == 1) return e;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(HD), 0, s, a.part, ns,
+                       HD, (int)a.n_head, a.out);
+    return hipGetLastError();
+}
+
+template <int HD>
+static hipError_t attn_launch_hd(const AttnArgs& a, hipStream_t s) {
+    int ns = 0, chunk = 0;
+    attention_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len, &ns, &chunk);
+    const size_t g = (a.n_head_kv && a.n_head % a.n_head_kv == 0) ? a.n_head / a.n_head_kv : 1;
+    switch (g) {
+    case 2: return attn_launch_t<HD, 2>(a, ns, chunk, (int)a.n_head_kv, s);
+    case 4: return attn_launch_t<HD, 4>(a, ns, chunk, (int)a.n_head_kv, s);
+    case 8: return attn_launch_t<HD, 8>(a, ns, chunk, (int)a.n_head_kv, s);
+    default: return attn_launch_t<HD, 1>(a, ns, chunk, (int)a.n_head, s);
+    }
+}
+
+hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
+    if (a.q_len == 0 || a.n_head == 0) return hipSuccess;
+    switch (a.head_dim) {
+    case 64: return attn_launch_hd<64>(a, s);
+    case 128: return attn_launch_hd<128>(a, s);
+    case 256: return attn_launch_hd<256>(a, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace barq

@@ -819,6 +819,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
         if (kg == 2 && a.nsb % 2 == 0) {
             if constexpr (F::TYPE == TYPE_Q4_K) {
                 if (bm == 65) return kq_launch_t<F, 64, 2, 8, GROUPED, 2>(a, s);
+                if (bm == 64) return kq_launch_t<F, 64, 2, 4, GROUPED, 2>(a, s);
                 return kq_launch_t<F, 32, 2, 4, GROUPED, 2>(a, s);
             } else {
                 return kq_launch_t<F, 32, 2, 4, GROUPED, 2>(a, s);

@@ -92,4 +92,27 @@ hipError_t moe_scatter_launch(const float* yg, const int32_t* ids, const float* 
                               const int32_t* rowpos, size_t rows, size_t top_k, size_t hidden,
                               float* out, hipStream_t s, int parts = 1, size_t part_stride = 0);
 
+// ---- attention (attention.hip) ----
+constexpr int ROPE_INTERLEAVED = 0, ROPE_SPLIT_HALF = 1;
+// apply_rope: x [seq, heads * hd] -> out[h * out_head_stride + p * hd + d]
+hipError_t rope_launch(int layout, const float* x, float* out, size_t seq, size_t heads, size_t hd, size_t start_pos,
+                       float freq_scale, const float* inv_freq, size_t out_head_stride, hipStream_t s);
+// transpose_heads: x [seq, heads * hd] -> out[h * out_head_stride + p * hd + d]
+hipError_t transpose_heads_launch(const float* x, float* out, size_t seq, size_t heads, size_t hd,
+                                  size_t out_head_stride, hipStream_t s);
+struct AttnArgs {
+    const float* q;           // [n_head, q_len, head_dim]
+    const float* k;           // cache base: [layer][kv head][position][head_dim]
+    const float* v;
+    size_t layer_off;         // floats from the base to the layer
+    size_t head_stride;       // floats between kv heads (max_size * head_dim)
+    size_t n_head, n_head_kv, head_dim, q_len, kv_len, start_pos;
+    float* part;              // split partials (attention_workspace bytes)
+    float* out;               // [q_len, n_head, head_dim]
+};
+bool attention_supported(size_t head_dim);
+void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len, int* n_split, int* chunk);
+size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv);
+hipError_t attention_launch(const AttnArgs& a, hipStream_t s);
+
 }  // namespace barq

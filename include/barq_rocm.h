@@ -268,6 +268,70 @@ int barq_rocm_cache_get(const barq_rocm_cache* c, const char* name, int* type, u
 uint64_t barq_rocm_cache_bytes(const barq_rocm_cache* c);
 int barq_rocm_cache_destroy(barq_rocm_cache* c);
 
+/* ---- attention: RoPE, KV cache, attention ---------------------------------
+ * The attention half of LlamaTransformer::self_attention
+ * (models/src/transformer.rs:176-265) with f32 tensors, as the reference
+ * computes it.  Heads and positions use the reference's layouts:
+ *   projections x:  [seq_len, n_heads * head_dim]
+ *   RoPE'd q / k, transposed v: [n_heads, seq_len, head_dim]
+ *   attention out:  [q_len, n_head, head_dim]
+ *
+ * barq_rocm_rope = apply_rope (transformer.rs:514-562): pair i of position p
+ * of every head is rotated by angle = ((float)(start_pos + p) * freq_scale)
+ * * inv_freq[i]; inv_freq has head_dim / 2 entries (the caller's
+ * rope_inv_freq, transformer.rs:52-54) and lives where `mem` says.  layout:
+ * BARQ_ROPE_INTERLEAVED pairs (2i, 2i+1), BARQ_ROPE_SPLIT_HALF pairs
+ * (i, i + head_dim/2) (RopeLayout, :570-595).  sin/cos are the device's
+ * sincosf, so results agree with the reference's to a few ulp.
+ * barq_rocm_transpose_heads = transpose_heads (:598-611). */
+#define BARQ_ROPE_INTERLEAVED 0
+#define BARQ_ROPE_SPLIT_HALF 1
+int barq_rocm_rope(barq_rocm_handle* h, const float* x, size_t seq_len, size_t n_heads, size_t head_dim,
+                   size_t start_pos, float freq_scale, const float* inv_freq, int layout, float* out, int mem);
+int barq_rocm_transpose_heads(barq_rocm_handle* h, const float* x, size_t seq_len, size_t n_heads,
+                              size_t head_dim, float* out, int mem);
+
+/* KV cache = KVCache (models/src/context.rs:245-340): per layer and kv head,
+ * positions x head_dim f32, contiguous per head.  Preallocated in device
+ * memory for max_size positions (KVCache::new's max_size, :260).
+ * append = KVCache::append (:272-291): k and v are [n_head_kv, n_tokens,
+ * head_dim]; they go after the layer's current length; an out-of-range
+ * layer is ignored (returns BARQ_OK, as the reference returns silently); a
+ * layer 0 append advances size (:287-289).  Unlike the reference's growing
+ * vectors, appending past max_size fails with BARQ_E_INVALID.
+ * append_rope fuses apply_rope on k and transpose_heads on v into the
+ * append: k_proj and v_proj are the projections [n_tokens, n_head_kv *
+ * head_dim] (transformer.rs:222-245).
+ * head = get_k_head / get_v_head (:316-323): device pointers to the layer's
+ * positions of kv head `head` (len(layer) rows of head_dim). */
+typedef struct barq_rocm_kv_cache barq_rocm_kv_cache;
+int barq_rocm_kv_cache_create(barq_rocm_handle* h, size_t max_size, size_t n_layers, size_t n_head_kv,
+                              size_t head_dim, barq_rocm_kv_cache** out);
+int barq_rocm_kv_cache_append(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const float* k,
+                              const float* v, size_t n_tokens, size_t head_dim, int mem);
+int barq_rocm_kv_cache_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer,
+                                   const float* k_proj, const float* v_proj, size_t n_tokens,
+                                   size_t start_pos, float freq_scale, const float* inv_freq, int layout,
+                                   int mem);
+size_t barq_rocm_kv_cache_size(const barq_rocm_kv_cache* c);
+size_t barq_rocm_kv_cache_layer_len(const barq_rocm_kv_cache* c, size_t layer);
+int barq_rocm_kv_cache_head(const barq_rocm_kv_cache* c, size_t layer, size_t head, const float** k,
+                            const float** v);
+int barq_rocm_kv_cache_clear(barq_rocm_kv_cache* c);
+int barq_rocm_kv_cache_destroy(barq_rocm_kv_cache* c);
+
+/* Attention = LlamaTransformer::compute_attention (transformer.rs:301-374):
+ * q is [n_head, q_len, head_dim] (mem), K/V are the cache's layer; query
+ * head h reads kv head h * n_head_kv / n_head; query i sees positions
+ * j < min(kv_len, start_pos + i + 1) with weights softmax((q . K[j]) /
+ * sqrt(head_dim)); out[i, h, :] = sum_j p_j V[j, :].  kv_len must be at most
+ * the layer's length; head_dim 64, 128 or 256 (else BARQ_E_UNSUPPORTED).
+ * n_head_kv and head_dim must be the cache's.  Uses the handle's workspace
+ * for the partial results of long sequences. */
+int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer,
+                        size_t n_head, size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len,
+                        size_t start_pos, float* out, int mem);
+
 #ifdef __cplusplus
 }
 #endif

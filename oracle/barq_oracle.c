@@ -686,3 +686,63 @@ int orc_moe_ffn(int gate_type, const uint8_t* const* gate,
     if (act == ORC_Q8_K && (hidden % 256 || n_ff % 256)) return -1;
     return orc_moe_dispatch(x, rows, hidden, n_experts, ids, weights, k, moe_expert_ffn, &c, out);
 }
+
+/* ---- attention ------------------------------------------------------------ */
+
+void orc_rope(const float* x, size_t seq, size_t heads, size_t hd, size_t start_pos, float freq_scale,
+              const float* inv_freq, int layout, float* out) {
+    /* transformer.rs:525-559: per head, per position, per pair */
+    const size_t half = hd / 2;
+    for (size_t h = 0; h < heads; h++)
+        for (size_t pos = 0; pos < seq; pos++) {
+            const size_t src = pos * heads * hd + h * hd, dst = h * seq * hd + pos * hd;
+            const size_t abs_pos = start_pos + pos;
+            for (size_t i = 0; i < half; i++) {
+                const float angle = ((float)abs_pos * freq_scale) * inv_freq[i];
+                const float sn = sinf(angle), cs = cosf(angle);
+                const size_t i0 = layout == 0 ? 2 * i : i, i1 = layout == 0 ? 2 * i + 1 : i + half;
+                const float x0 = x[src + i0], x1 = x[src + i1];
+                const float a = x0 * cs, b = x1 * sn, c = x0 * sn, d = x1 * cs;
+                out[dst + i0] = a - b;
+                out[dst + i1] = c + d;
+            }
+        }
+}
+
+void orc_transpose_heads(const float* x, size_t seq, size_t heads, size_t hd, float* out) {
+    for (size_t h = 0; h < heads; h++)
+        for (size_t pos = 0; pos < seq; pos++)
+            memcpy(out + h * seq * hd + pos * hd, x + pos * heads * hd + h * hd, hd * sizeof(float));
+}
+
+void orc_attention(const float* q, const float* kc, const float* vc, size_t head_stride, size_t n_head,
+                   size_t n_head_kv, size_t hd, size_t q_len, size_t kv_len, size_t start_pos, float* out) {
+    const float scale = sqrtf((float)hd);            /* :311 */
+    const float inv_scale = 1.0f / scale;            /* :327 */
+    float* scores = (float*)malloc((kv_len ? kv_len : 1) * sizeof(float));
+    float* head_out = (float*)malloc(hd * sizeof(float));
+    for (size_t h = 0; h < n_head; h++) {
+        const size_t kv_h = h * n_head_kv / n_head;   /* :318 */
+        const float* q_head = q + h * q_len * hd;
+        const float* k_head = kc + kv_h * head_stride;
+        const float* v_head = vc + kv_h * head_stride;
+        for (size_t i = 0; i < q_len; i++) {
+            orc_gemv_f32(k_head, q_head + i * hd, kv_len, hd, scores);   /* :331 */
+            for (size_t j = 0; j < kv_len; j++) scores[j] *= inv_scale;
+            const size_t valid_len = start_pos + i + 1;                   /* :337-342 */
+            for (size_t j = valid_len; j < kv_len; j++) scores[j] = -INFINITY;
+            float max_s = -INFINITY;                                      /* :345, f32::max */
+            for (size_t j = 0; j < kv_len; j++) max_s = fmaxf(max_s, scores[j]);
+            float exp_sum = 0.0f;
+            for (size_t j = 0; j < kv_len; j++) {
+                scores[j] = expf(scores[j] - max_s);
+                exp_sum += scores[j];
+            }
+            for (size_t j = 0; j < kv_len; j++) scores[j] /= exp_sum;
+            orc_gemm_f32(scores, v_head, 1, kv_len, hd, head_out);        /* :355 */
+            memcpy(out + i * n_head * hd + h * hd, head_out, hd * sizeof(float));   /* :365-371 */
+        }
+    }
+    free(scores);
+    free(head_out);
+}

@@ -151,6 +151,24 @@ int orc_moe_ffn(int gate_type, const uint8_t* const* gate,
                 const float* x, size_t rows, const int32_t* ids,
                 const float* weights, size_t k, int act, float* out);
 
+/* ---- attention (transformer.rs:176-374, context.rs:245-340) ------------ */
+/* apply_rope (models/src/transformer.rs:514-562): x [seq x heads*hd] ->
+   out [heads x seq x hd]; layout 0 = Interleaved (pairs 2i, 2i+1), 1 =
+   SplitHalf (pairs i, i+hd/2); angle = ((float)(start+p) * freq_scale) *
+   inv_freq[i]; sinf / cosf as Rust's f32::sin_cos calls them. */
+void orc_rope(const float* x, size_t seq, size_t heads, size_t hd, size_t start_pos,
+              float freq_scale, const float* inv_freq, int layout, float* out);
+/* transpose_heads (transformer.rs:598-611): [seq x heads*hd] -> [heads x seq x hd] */
+void orc_transpose_heads(const float* x, size_t seq, size_t heads, size_t hd, float* out);
+/* compute_attention (transformer.rs:301-374): q [n_head x q_len x hd]; kc/vc
+   hold kv head hk's positions at kc + hk*head_stride (kv_len rows of hd);
+   out [q_len x n_head x hd].  Scores by gemv_f32 (sequential dot), times
+   1/sqrt(hd), -inf from start_pos+i+1 on, softmax (max by fold, expf,
+   sequential sum, division), then gemm_f32 of the weights with V. */
+void orc_attention(const float* q, const float* kc, const float* vc, size_t head_stride,
+                   size_t n_head, size_t n_head_kv, size_t hd, size_t q_len, size_t kv_len,
+                   size_t start_pos, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,9 @@ def lib():
             "orc_moe_batch_by_expert": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
             "orc_moe_dispatch": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
             "orc_moe_ffn": (_i, [_i, _vp, _i, _vp, _i, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp]),
+            "orc_rope": (None, [_vp, _sz, _sz, _sz, _sz, ctypes.c_float, _vp, _i, _vp]),
+            "orc_transpose_heads": (None, [_vp, _sz, _sz, _sz, _vp]),
+            "orc_attention": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
             "cpub_gemm_literal_m1": (None, [_vp, _vp, _sz, _sz, _sz, _sz, _vp]),
             "cpub_gemv_simd": (None, [_vp, _vp, _sz, _sz, _sz, _vp]),
             "cpub_gemv_simd_threaded": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _i]),
@@ -147,6 +150,37 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     y = np.empty((rows, n), dtype=np.float32)
     lib().orc_rms_norm(_p(x), _p(w), rows, n, eps, _p(y))
     return y
+
+
+def rope(x: np.ndarray, seq: int, heads: int, hd: int, start_pos: int, freq_scale: float, inv_freq: np.ndarray,
+         layout: int) -> np.ndarray:
+    """apply_rope (transformer.rs:514-562): [seq, heads*hd] -> [heads, seq, hd]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    out = np.empty((heads, seq, hd), dtype=np.float32)
+    lib().orc_rope(_p(x), seq, heads, hd, start_pos, freq_scale, _p(f), layout, _p(out))
+    return out
+
+
+def transpose_heads(x: np.ndarray, seq: int, heads: int, hd: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty((heads, seq, hd), dtype=np.float32)
+    lib().orc_transpose_heads(_p(x), seq, heads, hd, _p(out))
+    return out
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_head: int, q_len: int, kv_len: int,
+              start_pos: int) -> np.ndarray:
+    """compute_attention (transformer.rs:301-374).  q [n_head, q_len, hd];
+    k, v [n_head_kv, positions >= kv_len, hd]; returns [q_len, n_head, hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    n_head_kv, pos, hd = k.shape
+    assert v.shape == k.shape and q.shape == (n_head, q_len, hd) and kv_len <= pos
+    out = np.empty((q_len, n_head, hd), dtype=np.float32)
+    lib().orc_attention(_p(q), _p(k), _p(v), pos * hd, n_head, n_head_kv, hd, q_len, kv_len, start_pos, _p(out))
+    return out
 
 
 def gemv_f32(a: np.ndarray, x: np.ndarray, m: int, n: int) -> np.ndarray:

@@ -1,0 +1,178 @@
+"""GPU parity of RoPE, the device KV cache and attention against the oracle
+(models/src/transformer.rs:176-374, models/src/context.rs:245-340).
+
+Bars:
+  - transpose_heads, KV-cache appends and reads: bit-exact.
+  - RoPE: within 2e-6 * max|x| of the oracle (the device's sincosf against
+    glibc's sinf/cosf, a few ulp apart).
+  - attention: max |out - ref| <= 2e-5 * max|V| (outputs are convex
+    combinations of V rows; the device sums in a different order and takes
+    base-2 exponentials of pre-scaled scores).
+"""
+import numpy as np
+import pytest
+
+import barq_rocm as B
+from barq_rocm import attention as A
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def inv_freq(hd, base=500000.0):
+    return np.array([np.float32(base) ** np.float32(-2.0 * i / hd) for i in range(hd // 2)], dtype=F32)
+
+
+def rng_f32(seed, *shape):
+    return np.random.default_rng(seed).standard_normal(shape).astype(F32)
+
+
+@pytest.mark.parametrize("layout", [A.ROPE_INTERLEAVED, A.ROPE_SPLIT_HALF])
+@pytest.mark.parametrize("seq,heads,hd,start", [(1, 32, 128, 4095), (7, 8, 128, 0), (33, 4, 64, 100000),
+                                                (2, 3, 256, 17), (5, 2, 4, 1)])
+def test_rope_matches_oracle(be, orc, layout, seq, heads, hd, start):
+    x = rng_f32(seq * 31 + hd, seq, heads * hd)
+    f = inv_freq(hd)
+    ref = orc.rope(x, seq, heads, hd, start, 1.0, f, layout)
+    got = A.apply_rope(be, dev(x), seq, heads, hd, start, 1.0, dev(f), layout).cpu().numpy()
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(x))
+    host = A.apply_rope(be, x, seq, heads, hd, start, 1.0, f, layout, mem=B.MEM_HOST)
+    assert np.array_equal(host, got)
+
+
+def test_rope_reference_known_answers(be):
+    # transformer.rs:623-684 on the device
+    x = np.array([1.0, 2.0, 3.0, 4.0], dtype=F32)
+    f = np.array([1.0, np.float32(10000.0) ** np.float32(-0.5)], dtype=F32)
+    s0, c0, s1, c1 = np.sin(f[0]), np.cos(f[0]), np.sin(f[1]), np.cos(f[1])
+    r0 = A.apply_rope(be, x, 1, 1, 4, 0, 1.0, f, A.ROPE_INTERLEAVED, mem=B.MEM_HOST).ravel()
+    assert np.allclose(r0, x, atol=1e-6)
+    r = A.apply_rope(be, x, 1, 1, 4, 1, 1.0, f, A.ROPE_INTERLEAVED, mem=B.MEM_HOST).ravel()
+    assert np.allclose(r, [c0 - 2 * s0, s0 + 2 * c0, 3 * c1 - 4 * s1, 3 * s1 + 4 * c1], atol=1e-6)
+    r = A.apply_rope(be, x, 1, 1, 4, 1, 1.0, f, A.ROPE_SPLIT_HALF, mem=B.MEM_HOST).ravel()
+    assert np.allclose(r, [c0 - 3 * s0, 2 * c1 - 4 * s1, s0 + 3 * c0, 2 * s1 + 4 * c1], atol=1e-6)
+
+
+def test_transpose_heads_bit_exact(be, orc):
+    x = rng_f32(5, 9, 4 * 64)
+    got = A.transpose_heads(be, dev(x), 9, 4, 64).cpu().numpy()
+    assert np.array_equal(got, orc.transpose_heads(x, 9, 4, 64))
+    assert np.array_equal(A.transpose_heads(be, x, 9, 4, 64, mem=B.MEM_HOST), got)
+
+
+def test_kv_cache_semantics(be):
+    n_kv, hd = 2, 64
+    c = A.KVCache(be, 16, 3, n_kv, hd)
+    assert c.size() == 0
+    k0, v0 = rng_f32(1, n_kv, 5, hd), rng_f32(2, n_kv, 5, hd)
+    c.append(0, dev(k0), dev(v0), 5, hd)
+    k1, v1 = rng_f32(3, n_kv, 4, hd), rng_f32(4, n_kv, 4, hd)
+    c.append(1, k1, v1, 4, hd, mem=B.MEM_HOST)
+    assert c.size() == 5 and c.layer_len(0) == 5 and c.layer_len(1) == 4   # only layer 0 moves size
+    c.append(7, k1, v1, 4, hd, mem=B.MEM_HOST)                           # out-of-range layer: ignored
+    assert c.size() == 5
+    k2, v2 = rng_f32(5, n_kv, 3, hd), rng_f32(6, n_kv, 3, hd)
+    c.append(0, dev(k2), dev(v2), 3, hd)
+    for h in range(n_kv):
+        kh, vh = c.get_head(0, h)
+        assert np.array_equal(kh, np.concatenate([k0[h], k2[h]]))
+        assert np.array_equal(vh, np.concatenate([v0[h], v2[h]]))
+        kh, vh = c.get_head(1, h)
+        assert np.array_equal(kh, k1[h]) and np.array_equal(vh, v1[h])
+    with pytest.raises(B.BarqError) as e:
+        c.append(0, rng_f32(7, n_kv, 9, hd), rng_f32(8, n_kv, 9, hd), 9, hd, mem=B.MEM_HOST)
+    assert e.value.code == B._lib.E_INVALID
+    with pytest.raises(B.BarqError) as e:
+        c.append(0, k2, v2, 3, 32, mem=B.MEM_HOST)
+    assert e.value.code == B._lib.E_DIM
+    c.clear()
+    assert c.size() == 0 and c.layer_len(1) == 0
+    c.close()
+
+
+@pytest.mark.parametrize("layout", [A.ROPE_INTERLEAVED, A.ROPE_SPLIT_HALF])
+def test_append_rope_equals_rope_then_append(be, layout):
+    n_kv, hd, n = 4, 128, 6
+    f = inv_freq(hd)
+    kp, vp = rng_f32(11, n, n_kv * hd), rng_f32(12, n, n_kv * hd)
+    c1 = A.KVCache(be, 32, 2, n_kv, hd)
+    c2 = A.KVCache(be, 32, 2, n_kv, hd)
+    for layer in range(2):
+        c1.append_rope(layer, dev(kp), dev(vp), n, 3, 1.0, dev(f), layout)
+        kr = A.apply_rope(be, dev(kp), n, n_kv, hd, 3, 1.0, dev(f), layout)
+        vt = A.transpose_heads(be, dev(vp), n, n_kv, hd)
+        c2.append(layer, kr, vt, n, hd)
+    c1.append_rope(1, kp, vp, n, 3 + n, 1.0, f, layout, mem=B.MEM_HOST)
+    kr = A.apply_rope(be, dev(kp), n, n_kv, hd, 3 + n, 1.0, dev(f), layout)
+    c2.append(1, kr, A.transpose_heads(be, dev(vp), n, n_kv, hd), n, hd)
+    assert c1.size() == c2.size() == n and c1.layer_len(1) == 2 * n
+    for layer in range(2):
+        for h in range(n_kv):
+            a, b = c1.get_head(layer, h), c2.get_head(layer, h)
+            assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+ATTN_CASES = [
+    # n_head, n_kv, hd, q_len, kv_len, start_pos, cache positions
+    (32, 8, 128, 1, 4096, 4095, 4096),    # Llama-3-8B decode
+    (32, 8, 128, 1, 1, 0, 1),
+    (32, 8, 128, 1, 63, 62, 63),
+    (32, 8, 128, 1, 65, 64, 80),
+    (32, 8, 128, 1, 1000, 999, 1000),
+    (8, 8, 64, 1, 300, 299, 300),         # no grouping
+    (16, 2, 128, 1, 700, 699, 700),       # 8 query heads per kv head
+    (12, 6, 128, 1, 500, 499, 512),       # 2 per kv head
+    (6, 4, 128, 1, 129, 128, 129),        # irregular grouping (kv = h * 4 / 6)
+    (8, 2, 256, 1, 517, 516, 517),
+    (32, 8, 128, 7, 40, 33, 40),          # a chunk of 7 new tokens
+    (4, 2, 64, 16, 16, 0, 16),            # a prompt from position 0
+    (8, 2, 128, 3, 10, 2, 10),            # start_pos + q_len < kv_len: masked tail
+    (8, 2, 128, 1, 50, 49, 80),           # kv_len below the layer length
+]
+
+
+def fill_cache(be, n_kv, hd, pos, seed, layers=2, layer=1):
+    k = rng_f32(seed, n_kv, pos, hd)
+    v = rng_f32(seed + 1, n_kv, pos, hd)
+    c = A.KVCache(be, pos + 5, layers, n_kv, hd)
+    c.append(0, dev(k), dev(v), pos, hd)
+    c.append(layer, dev(k), dev(v), pos, hd)
+    return c, k, v
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,q_len,kv_len,start,pos", ATTN_CASES)
+def test_attention_matches_oracle(be, orc, n_head, n_kv, hd, q_len, kv_len, start, pos):
+    c, k, v = fill_cache(be, n_kv, hd, pos, n_head * 7 + kv_len)
+    q = rng_f32(kv_len + 3, n_head, q_len, hd)
+    print(f"attention case n_head={n_head} n_kv={n_kv} hd={hd} q_len={q_len} kv_len={kv_len} start={start}",
+          flush=True)
+    got = A.compute_attention(be, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start).cpu().numpy()
+    ref = orc.attention(q, k, v, n_head, q_len, kv_len, start)
+    err = np.max(np.abs(got - ref))
+    assert err <= 2e-5 * np.max(np.abs(v)), err
+    host = A.compute_attention(be, q, c, 1, n_head, n_kv, hd, q_len, kv_len, start, mem=B.MEM_HOST)
+    assert np.array_equal(host, got)
+    c.close()
+
+
+def test_attention_argument_errors(be):
+    c, k, v = fill_cache(be, 2, 128, 20, 3)
+    q = rng_f32(1, 4, 1, 128)
+    with pytest.raises(B.BarqError) as e:
+        A.compute_attention(be, q, c, 1, 4, 2, 128, 1, 21, 20, mem=B.MEM_HOST)
+    assert e.value.code == B._lib.E_DIM
+    with pytest.raises(B.BarqError) as e:
+        A.compute_attention(be, q, c, 1, 4, 4, 128, 1, 20, 19, mem=B.MEM_HOST)
+    assert e.value.code == B._lib.E_DIM
+    c.close()
+    c80 = A.KVCache(be, 8, 1, 1, 80)
+    c80.append(0, rng_f32(2, 1, 4, 80), rng_f32(3, 1, 4, 80), 4, 80, mem=B.MEM_HOST)
+    with pytest.raises(B.BarqError) as e:
+        A.compute_attention(be, rng_f32(4, 1, 1, 80), c80, 0, 1, 1, 80, 1, 4, 3, mem=B.MEM_HOST)
+    assert e.value.code == B._lib.E_UNSUPPORTED
+    c80.close()
