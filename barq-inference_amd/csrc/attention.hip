@@ -26,6 +26,8 @@
 #include "common.hpp"
 #include "launch.hpp"
 
+#include <cstdlib>
+
 namespace barq {
 
 // ---- RoPE / transpose ----------------------------------------------------------
@@ -137,8 +139,8 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     #pragma unroll
     for (int g = 0; g < G; g++) {
         const int h = G > 1 ? grp * G + g : grp;
-        const float4* qp = reinterpret_cast<const float4*>(q + ((size_t)h * q_len + i) * HD + 8 * c);
-        const float4 a = qp[0], b = qp[1];
+        const float4* qp = reinterpret_cast<const float4*>(q + ((size_t)h * q_len + i) * HD);
+        const float4 a = qp[c], b = qp[c + LPR];
         qv[g][0] = a.x; qv[g][1] = a.y; qv[g][2] = a.z; qv[g][3] = a.w;
         qv[g][4] = b.x; qv[g][5] = b.y; qv[g][6] = b.z; qv[g][7] = b.w;
     }
@@ -151,45 +153,85 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
         for (int d = 0; d < 8; d++) o[g][d] = 0.0f;
     }
 
-    const float* kh = kc + layer_off + (size_t)hk * head_stride + 8 * c;
-    const float* vh = vc + layer_off + (size_t)hk * head_stride + 8 * c;
-    for (int base = j0; base < j1; base += R) {
-        const int j = base + r;
-        const bool live = j < j1;
-        float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
-        if (live) {
-            const float4* kp = reinterpret_cast<const float4*>(kh + (size_t)j * HD);
-            const float4* vp = reinterpret_cast<const float4*>(vh + (size_t)j * HD);
-            k0 = kp[0]; k1 = kp[1];
-            v0 = vp[0]; v1 = vp[1];
+    // lane c of a row holds dims 4c..4c+3 and 4(c+LPR)..: each load
+    // instruction reads whole contiguous half-rows
+    const float* kh = kc + layer_off + (size_t)hk * head_stride;
+    const float* vh = vc + layer_off + (size_t)hk * head_stride;
+    // P passes of R rows form a block; the next block's rows are loaded
+    // while this block's are scored, so every lane keeps K/V loads in
+    // flight.  The softmax state moves once per block: all P scores first,
+    // then one rescale of the running sums by the block's new maximum.
+    constexpr int P = G <= 4 ? 2 : 1;
+    struct Rows {
+        float4 k[P][2], v[P][2];
+    };
+    auto load = [&](Rows& b, int blk) {
+        #pragma unroll
+        for (int p = 0; p < P; p++) {
+            const int j = blk + p * R + r;
+            if (j < j1) {
+                const float4* kp = reinterpret_cast<const float4*>(kh + (size_t)j * HD);
+                const float4* vp = reinterpret_cast<const float4*>(vh + (size_t)j * HD);
+                b.k[p][0] = kp[c]; b.k[p][1] = kp[c + LPR];
+                b.v[p][0] = vp[c]; b.v[p][1] = vp[c + LPR];
+            } else {
+                b.k[p][0] = b.k[p][1] = b.v[p][0] = b.v[p][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
+    };
+    auto block = [&](const Rows& b, int blk) {
         #pragma unroll
         for (int g = 0; g < G; g++) {
-            float dot = qv[g][0] * k0.x;
-            dot = __builtin_fmaf(qv[g][1], k0.y, dot);
-            dot = __builtin_fmaf(qv[g][2], k0.z, dot);
-            dot = __builtin_fmaf(qv[g][3], k0.w, dot);
-            dot = __builtin_fmaf(qv[g][4], k1.x, dot);
-            dot = __builtin_fmaf(qv[g][5], k1.y, dot);
-            dot = __builtin_fmaf(qv[g][6], k1.z, dot);
-            dot = __builtin_fmaf(qv[g][7], k1.w, dot);
-            dot = group_sum<LPR>(dot);
-            if (live) {
-                const float s = dot * score_scale;          // (q . k) / sqrt(hd) * log2(e)
-                const float mn = fmaxf(m[g], s);
-                const float corr = fast_exp2(m[g] - mn);     // 0 while m is -inf
-                const float p = fast_exp2(s - mn);
-                m[g] = mn;
-                l[g] = __builtin_fmaf(l[g], corr, p);
-                o[g][0] = __builtin_fmaf(o[g][0], corr, p * v0.x);
-                o[g][1] = __builtin_fmaf(o[g][1], corr, p * v0.y);
-                o[g][2] = __builtin_fmaf(o[g][2], corr, p * v0.z);
-                o[g][3] = __builtin_fmaf(o[g][3], corr, p * v0.w);
-                o[g][4] = __builtin_fmaf(o[g][4], corr, p * v1.x);
-                o[g][5] = __builtin_fmaf(o[g][5], corr, p * v1.y);
-                o[g][6] = __builtin_fmaf(o[g][6], corr, p * v1.z);
-                o[g][7] = __builtin_fmaf(o[g][7], corr, p * v1.w);
+            float sc[P];
+            float bm = -INFINITY;
+            #pragma unroll
+            for (int p = 0; p < P; p++) {
+                const float4 k0 = b.k[p][0], k1 = b.k[p][1];
+                float dot = qv[g][0] * k0.x;
+                dot = __builtin_fmaf(qv[g][1], k0.y, dot);
+                dot = __builtin_fmaf(qv[g][2], k0.z, dot);
+                dot = __builtin_fmaf(qv[g][3], k0.w, dot);
+                dot = __builtin_fmaf(qv[g][4], k1.x, dot);
+                dot = __builtin_fmaf(qv[g][5], k1.y, dot);
+                dot = __builtin_fmaf(qv[g][6], k1.z, dot);
+                dot = __builtin_fmaf(qv[g][7], k1.w, dot);
+                dot = group_sum<LPR>(dot);
+                // (q . k) / sqrt(hd) * log2(e); rows past the range do not count
+                sc[p] = blk + p * R + r < j1 ? dot * score_scale : -INFINITY;
+                bm = fmaxf(bm, sc[p]);
             }
+            if (bm == -INFINITY) continue;             // no live row of this lane's in the block
+            const float mn = fmaxf(m[g], bm);
+            const float corr = fast_exp2(m[g] - mn);  // 0 while m is -inf
+            m[g] = mn;
+            l[g] *= corr;
+            #pragma unroll
+            for (int d = 0; d < 8; d++) o[g][d] *= corr;
+            #pragma unroll
+            for (int p = 0; p < P; p++) {
+                const float e = fast_exp2(sc[p] - mn);  // 0 for rows past the range
+                const float4 v0 = b.v[p][0], v1 = b.v[p][1];
+                l[g] += e;
+                o[g][0] = __builtin_fmaf(e, v0.x, o[g][0]);
+                o[g][1] = __builtin_fmaf(e, v0.y, o[g][1]);
+                o[g][2] = __builtin_fmaf(e, v0.z, o[g][2]);
+                o[g][3] = __builtin_fmaf(e, v0.w, o[g][3]);
+                o[g][4] = __builtin_fmaf(e, v1.x, o[g][4]);
+                o[g][5] = __builtin_fmaf(e, v1.y, o[g][5]);
+                o[g][6] = __builtin_fmaf(e, v1.z, o[g][6]);
+                o[g][7] = __builtin_fmaf(e, v1.w, o[g][7]);
+            }
+        }
+    };
+    if (j0 < j1) {
+        Rows cur;
+        load(cur, j0);
+        for (int blk = j0; blk < j1; blk += R * P) {
+            Rows nxt;
+            const bool more = blk + R * P < j1;
+            if (more) load(nxt, blk + R * P);
+            block(cur, blk);
+            if (more) cur = nxt;
         }
     }
 
@@ -197,7 +239,10 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     #pragma unroll
     for (int g = 0; g < G; g++) {
         #pragma unroll
-        for (int d = 0; d < 8; d++) red_o[r][g][8 * c + d] = o[g][d];
+        for (int d = 0; d < 4; d++) {
+            red_o[r][g][4 * c + d] = o[g][d];
+            red_o[r][g][4 * (c + LPR) + d] = o[g][4 + d];
+        }
         if (c == 0) {
             red_ml[r][g][0] = m[g];
             red_ml[r][g][1] = l[g];
@@ -231,23 +276,71 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
 }
 
 // out[i, h, :] from the n_split partial states of (i, h): one workgroup per
-// (h, i), one thread per output dim.
-__global__ __launch_bounds__(256)
-void attn_combine_kernel(const float* __restrict__ part, int n_split, int hd, int n_head, float* __restrict__ out) {
-    const int h = blockIdx.x, i = blockIdx.y, d = threadIdx.x;
-    if (d >= hd) return;
-    const float* pp = part + ((size_t)i * n_head + h) * n_split * (hd + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_split; s++) M = fmaxf(M, pp[(size_t)s * (hd + 2)]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < n_split; s++) {
-        const float* ps = pp + (size_t)s * (hd + 2);
-        if (ps[0] == -INFINITY) continue;
-        const float w = fast_exp2(ps[0] - M);
-        L = __builtin_fmaf(ps[1], w, L);
-        O = __builtin_fmaf(ps[2 + d], w, O);
+// (h, i).  The split maxima and weights are spread over the 1024 threads;
+// the output sums over 1024 / HD thread subsets of the splits, then added in
+// LDS.
+constexpr int ATT_MAX_SPLIT = 1024;
+
+template <int HD>
+__global__ __launch_bounds__(1024)
+void attn_combine_kernel(const float* __restrict__ part, int n_split, int n_head, float* __restrict__ out) {
+    constexpr int NT = 1024, NWV = NT / 64, SUB = NT / HD, PRE = 8;
+    __shared__ float w[ATT_MAX_SPLIT];
+    __shared__ float red[SUB][HD];
+    __shared__ float wred[2][NWV];
+    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int sub = t / HD, d = t % HD;
+    const float* pp = part + ((size_t)i * n_head + h) * n_split * (HD + 2);
+    // every load of the first PRE rounds is issued before any reduction
+    float ov[PRE];
+    #pragma unroll
+    for (int u = 0; u < PRE; u++) {
+        const int s = sub + SUB * u;
+        ov[u] = s < n_split ? pp[(size_t)s * (HD + 2) + 2 + d] : 0.0f;
     }
-    out[((size_t)i * n_head + h) * hd + d] = O / L;
+    float M = -INFINITY, Ls = 0.0f, Ms = -INFINITY;
+    if (t < n_split) {
+        Ms = pp[(size_t)t * (HD + 2)];
+        Ls = pp[(size_t)t * (HD + 2) + 1];
+    }
+    for (int s = t; s < n_split; s += NT) M = fmaxf(M, pp[(size_t)s * (HD + 2)]);
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) wred[0][wave] = M;
+    __syncthreads();
+    M = wred[0][0];
+    #pragma unroll
+    for (int u = 1; u < NWV; u++) M = fmaxf(M, wred[0][u]);
+    float L = 0.0f;
+    for (int s = t; s < n_split; s += NT) {
+        const float ms = s == t ? Ms : pp[(size_t)s * (HD + 2)];
+        const float ls = s == t ? Ls : pp[(size_t)s * (HD + 2) + 1];
+        const float ws = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
+        w[s] = ws;
+        L = __builtin_fmaf(ls, ws, L);
+    }
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+    if (lane == 0) wred[1][wave] = L;
+    __syncthreads();
+    L = wred[1][0];
+    #pragma unroll
+    for (int u = 1; u < NWV; u++) L += wred[1][u];
+    float O = 0.0f;
+    #pragma unroll
+    for (int u = 0; u < PRE; u++) {
+        const int s = sub + SUB * u;
+        if (s < n_split) O = __builtin_fmaf(ov[u], w[s], O);
+    }
+    for (int s = sub + SUB * PRE; s < n_split; s += SUB) O = __builtin_fmaf(pp[(size_t)s * (HD + 2) + 2 + d], w[s], O);
+    red[sub][d] = O;
+    __syncthreads();
+    if (t < HD) {
+        float acc = red[0][t];
+        #pragma unroll
+        for (int u = 1; u < SUB; u++) acc += red[u][t];
+        out[((size_t)i * n_head + h) * HD + t] = acc / L;
+    }
 }
 
 bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
@@ -258,13 +351,22 @@ size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t 
     return ns > 1 ? (size_t)ns * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
 }
 
-// Splits: about 1024 workgroups in all, at least 64 positions each.
+static int att_env(const char* name) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : 0;
+}
+static const int g_att_wg = att_env("BARQ_ATTN_WG");   // workgroup-count target override (tuning)
+
+// Splits: about 512 workgroups in all (two per CU; measured best on MI355X
+// for 4K-32K positions), at least 64 positions each.
 void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len, int* n_split, int* chunk) {
     const size_t g = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
     const size_t groups = (g == 1 || g > 8 || (g & (g - 1))) ? n_head : n_head_kv;
     const size_t wg = groups * (q_len ? q_len : 1);
-    size_t ns = (1024 + wg - 1) / wg;
-    const size_t max_ns = (kv_len + 63) / 64;
+    const size_t target = g_att_wg > 0 ? (size_t)g_att_wg : 512;
+    size_t ns = (target + wg - 1) / wg;
+    size_t max_ns = (kv_len + 63) / 64;
+    if (max_ns > (size_t)ATT_MAX_SPLIT) max_ns = ATT_MAX_SPLIT;
     if (ns > max_ns) ns = max_ns;
     if (ns < 1) ns = 1;
     size_t ch = (kv_len + ns - 1) / ns;
@@ -283,8 +385,8 @@ static hipError_t attn_launch_t(const AttnArgs& a, int ns, int chunk, int groups
                        (long long)a.start_pos, chunk, scale, a.part, a.out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ns == 1) return e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(HD), 0, s, a.part, ns,
-                       HD, (int)a.n_head, a.out);
+    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(1024), 0, s, a.part,
+                       ns, (int)a.n_head, a.out);
     return hipGetLastError();
 }
 

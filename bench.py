@@ -51,6 +51,9 @@ def parse():
                    help="skip the two rocprofv3 --pmc child runs that measure HBM traffic per launch")
     p.add_argument("--norm", action="store_true",
                    help="time the fused RMSNorm -> Q8_K quantizer (the step before each projection) instead of a config")
+    p.add_argument("--attn", action="store_true",
+                   help="time decode attention over the device KV cache (Llama-3-8B heads) instead of a config")
+    p.add_argument("--kv-len", type=int, default=4096, help="--attn: cached positions per query")
     p.add_argument("--probe-copy", action="store_true",
                    help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -361,6 +364,90 @@ def bench_norm(args):
     return 0
 
 
+def bench_attn(args):
+    """Decode attention (compute_attention, transformer.rs:301-374) at the
+    Llama-3-8B head layout: 32 query heads, 8 kv heads, head_dim 128, one new
+    token against kv_len cached positions in f32.  HBM-bound: every call
+    reads the layer's K and V rows once (2 * 8 * kv_len * 128 * 4 bytes).
+    Calls rotate over enough cache layers (> 320 MB) that the Infinity Cache
+    cannot hold them.  The CPU leg times the oracle's restatement of
+    compute_attention (one core) on a bounded number of calls."""
+    import numpy as np
+    import torch
+
+    import barq_rocm as B
+    from barq_rocm import attention as A
+
+    be = B.Backend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    n_head, n_kv, hd, kv = 32, 8, 128, args.kv_len
+    layer_bytes = 2 * n_kv * kv * hd * 4
+    layers = max(2, -(-320 * 2**20 // layer_bytes))
+    log(f"attention: {n_head} heads / {n_kv} kv heads x {hd}, kv_len {kv}, {layers} cache layers "
+        f"({layers * layer_bytes / 2**20:.0f} MiB)")
+    cache = A.KVCache(be, kv, layers, n_kv, hd)
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    for layer in range(layers):
+        k = torch.randn((n_kv, kv, hd), generator=g, device="cuda", dtype=torch.float32)
+        v = torch.randn((n_kv, kv, hd), generator=g, device="cuda", dtype=torch.float32)
+        cache.append(layer, k, v, kv, hd)
+        del k, v
+    q = torch.randn((n_head, 1, hd), generator=g, device="cuda", dtype=torch.float32)
+    out = torch.empty((1, n_head, hd), dtype=torch.float32, device="cuda")
+    lib = be._lib
+
+    def launch(i):
+        B._lib.check(lib.barq_rocm_attention(be.h, q.data_ptr(), cache.c, i % layers, n_head, n_kv, hd, 1, kv,
+                                             kv - 1, out.data_ptr(), B.MEM_DEVICE))
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    ms, method = time_launches(launch, args.steps, args.eager)
+    ms_eager, _ = time_launches(launch, args.steps, True)
+    alg = layer_bytes + 2 * n_head * hd * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+
+    # parity of layer 0 against the oracle, and the CPU leg
+    launch(0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    kh = np.stack([cache.get_head(0, h)[0] for h in range(n_kv)])
+    vh = np.stack([cache.get_head(0, h)[1] for h in range(n_kv)])
+    qn = q.cpu().numpy()
+    from oracle import oracle as O
+    t0 = time.perf_counter()
+    ref = O.attention(qn, kh, vh, n_head, 1, kv, kv - 1)
+    calls, t_cpu = 1, time.perf_counter() - t0
+    while not args.no_cpu and t_cpu < min(args.cpu_seconds, 20.0):
+        O.attention(qn, kh, vh, n_head, 1, kv, kv - 1)
+        calls += 1
+        t_cpu = time.perf_counter() - t0
+    err = float(np.max(np.abs(got - ref)) / np.max(np.abs(vh)))
+    cpu_gbs = alg * calls / t_cpu / 1e9
+    result = {
+        "metric": f"decode attention (Llama-3-8B heads, kv_len {kv}) achieved HBM GB/s + us/call, 1 GPU",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"attention 32 q heads / 8 kv heads x 128, q_len 1, kv_len {kv}, f32 KV cache",
+                   "cache_layers_rotated": layers, "timing": method},
+        "us_per_call": round(ms * 1e3, 3), "us_per_call_eager": round(ms_eager * 1e3, 3),
+        "parity_max_err_rel_to_max_v": err,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
+                     "scope": "one call: the split kernel and the split-combine kernel"},
+        "cpu_baseline": {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": f"{calls} calls of the oracle's compute_attention restatement on layer 0",
+                         "us_per_call": round(t_cpu / calls * 1e6, 1)},
+    }
+    cache.close()
+    be.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -376,6 +463,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.norm:
         return bench_norm(args)
+    if args.attn:
+        return bench_attn(args)
     if args.config == 5:
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]
