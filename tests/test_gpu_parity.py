@@ -308,6 +308,10 @@ MOE_CASES = {
     "mixed_types": dict(ne=3, hid=512, nff=512, rows=20, k=2, gt=B.Q6_K, ut=B.Q4_K),
     "wide_tiles": dict(ne=2, hid=256, nff=512, rows=80, k=2),
     "odd_q6k_fallback": dict(ne=3, hid=256, nff=768, rows=12, k=2),
+    # more tiles than workgroups, so each workgroup streams several tiles
+    # through one pipeline: gate/up 8 x 2 x 64 tiles; down 24 x 32 tiles
+    "multi_tile_gate_up": dict(ne=8, hid=512, nff=8192, rows=16, k=2),
+    "multi_tile_down": dict(ne=24, hid=4096, nff=512, rows=24, k=2),
 }
 
 
