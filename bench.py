@@ -54,6 +54,7 @@ def parse():
     p.add_argument("--attn", action="store_true",
                    help="time decode attention over the device KV cache (Llama-3-8B heads) instead of a config")
     p.add_argument("--kv-len", type=int, default=4096, help="--attn: cached positions per query")
+    p.add_argument("--q-len", type=int, default=1, help="--attn: new tokens per call (1 = decode; > 1 = a prompt chunk)")
     p.add_argument("--probe-copy", action="store_true",
                    help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -382,7 +383,8 @@ def bench_attn(args):
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     be.set_stream(stream.cuda_stream)
-    n_head, n_kv, hd, kv = 32, 8, 128, args.kv_len
+    n_head, n_kv, hd, kv, ql = 32, 8, 128, args.kv_len, args.q_len
+    assert 1 <= ql <= kv
     layer_bytes = 2 * n_kv * kv * hd * 4
     layers = max(2, -(-320 * 2**20 // layer_bytes))
     log(f"attention: {n_head} heads / {n_kv} kv heads x {hd}, kv_len {kv}, {layers} cache layers "
@@ -394,20 +396,22 @@ def bench_attn(args):
         v = torch.randn((n_kv, kv, hd), generator=g, device="cuda", dtype=torch.float32)
         cache.append(layer, k, v, kv, hd)
         del k, v
-    q = torch.randn((n_head, 1, hd), generator=g, device="cuda", dtype=torch.float32)
-    out = torch.empty((1, n_head, hd), dtype=torch.float32, device="cuda")
+    q = torch.randn((n_head, ql, hd), generator=g, device="cuda", dtype=torch.float32)
+    out = torch.empty((ql, n_head, hd), dtype=torch.float32, device="cuda")
     lib = be._lib
 
     def launch(i):
-        B._lib.check(lib.barq_rocm_attention(be.h, q.data_ptr(), cache.c, i % layers, n_head, n_kv, hd, 1, kv,
-                                             kv - 1, out.data_ptr(), B.MEM_DEVICE))
+        B._lib.check(lib.barq_rocm_attention(be.h, q.data_ptr(), cache.c, i % layers, n_head, n_kv, hd, ql, kv,
+                                             kv - ql, out.data_ptr(), B.MEM_DEVICE))
     for i in range(args.warmup):
         launch(i)
     torch.cuda.synchronize()
     ms, method = time_launches(launch, args.steps, args.eager)
     ms_eager, _ = time_launches(launch, args.steps, True)
-    alg = layer_bytes + 2 * n_head * hd * 4
+    alg = layer_bytes + 2 * ql * n_head * hd * 4
     gbs = alg / (ms * 1e-3) / 1e9
+    # causal: query i sees kv - ql + i + 1 positions; two FMAs (q.k, p.v) per dim per visible position
+    flops = 2 * 2 * n_head * hd * sum(kv - ql + i + 1 for i in range(ql))
 
     # parity of layer 0 against the oracle, and the CPU leg
     launch(0)
@@ -418,22 +422,24 @@ def bench_attn(args):
     qn = q.cpu().numpy()
     from oracle import oracle as O
     t0 = time.perf_counter()
-    ref = O.attention(qn, kh, vh, n_head, 1, kv, kv - 1)
+    ref = O.attention(qn, kh, vh, n_head, ql, kv, kv - ql)
     calls, t_cpu = 1, time.perf_counter() - t0
     while not args.no_cpu and t_cpu < min(args.cpu_seconds, 20.0):
-        O.attention(qn, kh, vh, n_head, 1, kv, kv - 1)
+        O.attention(qn, kh, vh, n_head, ql, kv, kv - ql)
         calls += 1
         t_cpu = time.perf_counter() - t0
     err = float(np.max(np.abs(got - ref)) / np.max(np.abs(vh)))
     cpu_gbs = alg * calls / t_cpu / 1e9
     result = {
-        "metric": f"decode attention (Llama-3-8B heads, kv_len {kv}) achieved HBM GB/s + us/call, 1 GPU",
+        "metric": f"{'decode' if ql == 1 else 'prompt-chunk'} attention (Llama-3-8B heads, q_len {ql}, kv_len {kv}) "
+                  f"achieved HBM GB/s + us/call, 1 GPU",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"attention 32 q heads / 8 kv heads x 128, q_len 1, kv_len {kv}, f32 KV cache",
+        "config": {"workload": f"attention 32 q heads / 8 kv heads x 128, q_len {ql}, kv_len {kv}, f32 KV cache",
                    "cache_layers_rotated": layers, "timing": method},
         "us_per_call": round(ms * 1e3, 3), "us_per_call_eager": round(ms_eager * 1e3, 3),
+        "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
         "parity_max_err_rel_to_max_v": err,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
