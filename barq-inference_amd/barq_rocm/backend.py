@@ -210,13 +210,15 @@ class Backend:
         return ids, w
 
     def moe_ffn(self, gate_type, gates, up_type, ups, down_type, downs, hidden, n_ff, x, rows, ids, weights,
-                top_k, act, mem=L.MEM_DEVICE, sync=True):
+                top_k, act, mem=L.MEM_DEVICE, sync=True, out=None):
         ne = len(gates)
         arr = ctypes.c_void_p * ne
         g = arr(*[_ptr(t) for t in gates])
         u = arr(*[_ptr(t) for t in ups])
         d = arr(*[_ptr(t) for t in downs])
-        if mem == L.MEM_HOST:
+        if out is not None:
+            pass
+        elif mem == L.MEM_HOST:
             out = np.empty((rows, hidden), dtype=np.float32)
         else:
             import torch

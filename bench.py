@@ -41,7 +41,8 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    # untimed launches before the timed ones: enough (< 1 s) for the GPU's clocks to settle
+    p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--config", type=int, default=2, help="BASELINE.json config: 1-4 linear, 5 MoE")
     p.add_argument("--copies", type=int, default=0, help="distinct weight copies (default: >= 320 MB)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
@@ -253,21 +254,18 @@ def bench_moe(args):
     ids, wts = be.moe_route(ld, tokens, ne, top_k)
     torch.cuda.synchronize()
 
+    out = torch.empty((tokens, hidden), dtype=torch.float32, device="cuda")
+
     def launch(i):
-        return be.moe_ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, hidden, n_ff, xd, tokens, ids, wts, top_k,
-                          B.ACT_F32_Q8, sync=False)
+        be.moe_ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, hidden, n_ff, xd, tokens, ids, wts, top_k, B.ACT_F32_Q8,
+                   sync=False, out=out)
 
     for i in range(args.warmup):
-        out = launch(i)
+        launch(i)
     torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for i in range(args.steps):
-        out = launch(i)
-    ev1.record(stream)
-    ev1.synchronize()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    # the whole step (seven kernels, no host synchronisation) as one HIP graph
+    ms, method = time_launches(launch, args.steps, args.eager)
+    ms_eager, _ = time_launches(launch, args.steps, True)
     ids_h = ids.cpu().numpy()
     used = sorted(set(ids_h.reshape(-1).tolist()))
     wbytes = sum(gates[e].nbytes + ups[e].nbytes + downs[e].nbytes for e in used)
@@ -289,8 +287,9 @@ def bench_moe(args):
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
-        "config": {"workload": c["name"], "experts_used": len(used), "tokens_per_expert": counts, "timing": "eager"},
-        "us_per_step": round(ms * 1e3, 2), "parity_rel_err_4_tokens": rel,
+        "config": {"workload": c["name"], "experts_used": len(used), "tokens_per_expert": counts, "timing": method},
+        "us_per_step": round(ms * 1e3, 2), "us_per_step_eager": round(ms_eager * 1e3, 2),
+        "parity_rel_err_4_tokens": rel,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
                      "scope": "the whole step (grouping, quantizers, grouped GEMMs, scatter)"},
