@@ -351,11 +351,6 @@ size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t 
     return ns > 1 ? (size_t)ns * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
 }
 
-static int att_env(const char* name) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : 0;
-}
-static const int g_att_wg = att_env("BARQ_ATTN_WG");   // workgroup-count target override (tuning)
 
 // Splits: about 512 workgroups in all (two per CU; measured best on MI355X
 // for 4K-32K positions), at least 64 positions each.
@@ -363,7 +358,8 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
     const size_t g = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
     const size_t groups = (g == 1 || g > 8 || (g & (g - 1))) ? n_head : n_head_kv;
     const size_t wg = groups * (q_len ? q_len : 1);
-    const size_t target = g_att_wg > 0 ? (size_t)g_att_wg : 512;
+    const int wg_override = tuning_env("BARQ_ATTN_WG");   // workgroup-count target (tuning)
+    const size_t target = wg_override > 0 ? (size_t)wg_override : 512;
     size_t ns = (target + wg - 1) / wg;
     size_t max_ns = (kv_len + 63) / 64;
     if (max_ns > (size_t)ATT_MAX_SPLIT) max_ns = ATT_MAX_SPLIT;

@@ -6,8 +6,17 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace barq {
+
+// Launch-shape overrides for tuning sweeps (BARQ_GEMM_*, BARQ_GEMV_*,
+// BARQ_ATTN_*): read at every launch, so one process can compare variants;
+// unset (or 0) keeps the measured default.
+inline int tuning_env(const char* name, int def = 0) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : def;
+}
 
 // GGUF block geometry (barq_core/src/gguf.rs:168-186 block sizes; bytes
 // from gguf.rs:529-530,645,747,854 and llama.cpp block_q4_0/block_q8_K).

@@ -738,12 +738,6 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
 }
 
 // ---- launch ------------------------------------------------------------------
-static int kq_env(const char* name, int def) {
-    if (const char* e = getenv(name)) return atoi(e);
-    return def;
-}
-static const int g_kq_bm = kq_env("BARQ_GEMM_BM", 0);    // tile override for tuning: 32, 64 or 65 (64 rows, 8 waves)
-static const int g_kq_xcd = kq_env("BARQ_GEMM_XCD", 1);  // XCD-aware tile order (ungrouped)
 
 static int cu_count() {
     static int n[64] = {};
@@ -788,13 +782,13 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     if (a.nsb % KG != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, KG, GROUPED>), dim3(grid), dim3(64 * NW * KG), 0, s, a.wt, a.wrb, a.X, a.xrb,
                        a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, a.ks, a.ykstride,
-                       g_kq_xcd);
+                       tuning_env("BARQ_GEMM_XCD", 1));   // XCD-aware tile order (ungrouped)
     return hipGetLastError();
 }
 
-static const int g_kq_ns = kq_env("BARQ_GEMM_NS", 0);   // stage-count override for tuning
-static const int g_kq_ks = kq_env("BARQ_GEMM_KS", 0);   // K-slice override for grouped launches (tuning)
-static const int g_kq_kg = kq_env("BARQ_GEMM_KG", 0);   // K-group override for ungrouped launches (tuning)
+// Overrides: BARQ_GEMM_BM (16, 32, 64, or 65 = 64 rows with eight waves),
+// BARQ_GEMM_NS (stages), BARQ_GEMM_KG (K-groups, ungrouped), BARQ_GEMM_KS
+// (K slices of the MoE down projection).
 
 // rows: M (ungrouped) or the expected rows per expert (grouped).  Stage
 // counts are the most that fit the 160 KiB of LDS (deeper pipelines keep
@@ -803,6 +797,7 @@ template <class F, bool GROUPED>
 static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // measured on MI355X: 64x128 tiles with eight waves (two per SIMD) above
     // 32 rows, 32-row tiles with four waves for small expert groups
+    const int g_kq_ns = tuning_env("BARQ_GEMM_NS"), g_kq_bm = tuning_env("BARQ_GEMM_BM");
     const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 65 : 32);
     if (bm == 16) {
         if (g_kq_ns == 2) return kq_launch_t<F, 16, 2, 4, GROUPED>(a, s);
@@ -815,7 +810,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     if constexpr (!GROUPED) {
         // two K-groups of waves share a tile's pipeline (twice the waves per
         // SIMD for the same LDS) when the super-block count is even
-        const int kg = g_kq_kg ? g_kq_kg : 2;
+        const int kg = tuning_env("BARQ_GEMM_KG", 2);
         if (kg == 2 && a.nsb % 2 == 0) {
             if constexpr (F::TYPE == TYPE_Q4_K) {
                 if (bm == 65) return kq_launch_t<F, 64, 2, 8, GROUPED, 2>(a, s);
@@ -843,7 +838,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
 // Raw buffer loads use 32-bit offsets: each weight matrix and the activation
 // rows must stay below 2 GiB.  Q6_K needs row bytes that are a multiple of 4
 // (an even number of super-blocks).
-int kq_k_slices_override() { return g_kq_ks; }
+int kq_k_slices_override() { return tuning_env("BARQ_GEMM_KS"); }
 
 bool kq_supported(int w_type, size_t n_rows, size_t k, size_t m) {
     if ((w_type != TYPE_Q4_K && w_type != TYPE_Q6_K) || k % 256 != 0 || k == 0 || n_rows == 0) return false;

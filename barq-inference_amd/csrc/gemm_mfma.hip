@@ -395,11 +395,6 @@ void gemm_kq_kernel(const uint8_t* __restrict__ W, size_t w_row_bytes, const uin
 // y += dx * (d*C - dmin*Cm).
 // ---------------------------------------------------------------------------
 // ---- launch ---------------------------------------------------------------
-static int read_env_bm() {
-    if (const char* e = getenv("BARQ_GEMM_BM")) return atoi(e);
-    return 0;
-}
-static int g_bm_override = read_env_bm();
 
 template <class F, int BM>
 static hipError_t launch_kq(const uint8_t* W, size_t wrb, const uint8_t* X, size_t xrb, float* Y, int M, int N,
@@ -422,7 +417,7 @@ static hipError_t launch_kq(const uint8_t* W, size_t wrb, const uint8_t* X, size
 // Activation-tile height: the largest of 128/64/32/16 that still gives
 // every CU two workgroups, never taller than M needs.
 static int pick_bm(int M, int N) {
-    if (g_bm_override) return g_bm_override;
+    if (const int o = tuning_env("BARQ_GEMM_BM")) return o;
     const int tiles_n = (N + GM_BN - 1) / GM_BN;
     int bm = 128;
     while (bm > 16 && (bm >= 2 * ((M + 15) / 16 * 16) || (long)tiles_n * ((M + bm - 1) / bm) < 512)) bm >>= 1;
@@ -431,11 +426,6 @@ static int pick_bm(int M, int N) {
 
 // BARQ_GEMM_IMPL=0 selects this file's 16x16x64 kernel for every shape
 // (comparison runs); by default gemm_kq.hip takes every shape it supports.
-static int read_env_impl() {
-    if (const char* e = getenv("BARQ_GEMM_IMPL")) return atoi(e);
-    return 2;
-}
-static const int g_impl = read_env_impl();
 
 template <class F>
 static hipError_t dispatch_kq(const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
@@ -466,7 +456,8 @@ hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t
                                 float* y, hipStream_t s) {
     if (m == 0 || n_rows == 0) return hipSuccess;
     if (!gemm_mfma_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
-    if (g_impl != 0 && kq_supported(w_type, n_rows, k, m)) return kq_gemm_launch(w_type, W, n_rows, k, xq, m, y, s);
+    if (tuning_env("BARQ_GEMM_IMPL", 2) != 0 && kq_supported(w_type, n_rows, k, m))
+        return kq_gemm_launch(w_type, W, n_rows, k, xq, m, y, s);
     switch (w_type) {
     case TYPE_Q4_K: return dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
     case TYPE_Q6_K: return dispatch_kq<GQ6K>(W, n_rows, k, xq, m, y, s);

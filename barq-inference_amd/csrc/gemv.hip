@@ -152,14 +152,14 @@ void gemv_f32_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const floa
 struct GemvCfg { int r, waves; };
 
 // BARQ_GEMV_CFG="R,W" overrides the launch shape (used for tuning sweeps).
-static GemvCfg read_env_cfg() {
+static GemvCfg env_cfg() {
     GemvCfg c = {0, 0};
     if (const char* e = getenv("BARQ_GEMV_CFG")) {
         if (sscanf(e, "%d,%d", &c.r, &c.waves) != 2) c = {0, 0};
     }
     return c;
 }
-static GemvCfg g_cfg_override = read_env_cfg();
+static GemvCfg g_cfg_override = {0, 0};
 
 void gemv_set_config(int rows_per_wave, int waves) { g_cfg_override = {rows_per_wave, waves}; }
 
@@ -176,7 +176,8 @@ static hipError_t launch_q8(const uint8_t* W, size_t row_bytes, const uint8_t* x
 template <class F>
 static hipError_t dispatch_q8(const uint8_t* W, size_t row_bytes, const uint8_t* xq, float* y,
                               int n_rows, int k, hipStream_t s, GemvCfg def) {
-    GemvCfg c = g_cfg_override.r ? g_cfg_override : def;
+    const GemvCfg e = env_cfg();
+    const GemvCfg c = g_cfg_override.r ? g_cfg_override : e.r ? e : def;
 #define BARQ_GEMV_CASE(RR, WW) \
     if (c.r == RR && c.waves == WW) return launch_q8<F, RR, WW>(W, row_bytes, xq, y, n_rows, k, s);
     BARQ_GEMV_CASE(1, 4) BARQ_GEMV_CASE(2, 4) BARQ_GEMV_CASE(4, 4) BARQ_GEMV_CASE(8, 4)
@@ -209,18 +210,14 @@ static int dma_bit(int w_type) {
     default: return 0;
     }
 }
-static int read_env_dma_types() {
-    if (const char* e = getenv("BARQ_GEMV_DMA_TYPES")) return atoi(e);
-    return 2 | 4 | 8 | 16;
-}
-static const int g_dma_types = read_env_dma_types();
 
 hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,
                           float* y, hipStream_t s) {
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     const int n = (int)n_rows, kk = (int)k;
-    if (g_dma_types & dma_bit(w_type) && gemv_dma_supported(w_type, W, n_rows, k, xq))
+    if (tuning_env("BARQ_GEMV_DMA_TYPES", 2 | 4 | 8 | 16) & dma_bit(w_type) &&
+        gemv_dma_supported(w_type, W, n_rows, k, xq))
         return gemv_dma_launch(w_type, W, n_rows, k, xq, y, s);
     switch (w_type) {
     case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, {2, 2});

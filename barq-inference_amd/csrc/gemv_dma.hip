@@ -307,12 +307,7 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
 }
 
 // ---- launch ------------------------------------------------------------------
-static int dma_env(const char* name, int def) {
-    if (const char* e = getenv(name)) return atoi(e);
-    return def;
-}
-// tuning: W*100+R*10+D selects another launch shape (e.g. 842); -1 turns the path off
-static const int g_dma_cfg = dma_env("BARQ_GEMV_DMA", 0);
+// tuning: BARQ_GEMV_DMA = W*100+R*10+D selects another launch shape (e.g. 842); -1 turns the path off
 
 template <class P, int W, int R, int D>
 static hipError_t launch_dma(const uint8_t* Wq, uint32_t rb, size_t n_rows, int nblk, const uint8_t* xq,
@@ -345,7 +340,7 @@ static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const voi
     const uint8_t* x = static_cast<const uint8_t*>(xq);
 #define BARQ_DMA_CASE(WW, RR, DD) \
     case WW * 100 + RR * 10 + DD: return launch_dma<P, WW, RR, DD>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
-    switch (g_dma_cfg) {
+    switch (tuning_env("BARQ_GEMV_DMA")) {
     BARQ_DMA_CASE(4, 2, 2) BARQ_DMA_CASE(4, 4, 4) BARQ_DMA_CASE(4, 8, 2) BARQ_DMA_CASE(8, 2, 2)
     BARQ_DMA_CASE(8, 4, 2) BARQ_DMA_CASE(2, 2, 2) BARQ_DMA_CASE(2, 4, 2) BARQ_DMA_CASE(4, 1, 1)
     BARQ_DMA_CASE(8, 1, 1)
@@ -364,7 +359,7 @@ static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const voi
 // block pairs per lane, offsets within one wave's rows stay below 2 GiB and
 // the staged activation fits in LDS beside the slice buffers.
 bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq) {
-    if (g_dma_cfg < 0 || k == 0 || n_rows > (size_t)INT32_MAX) return false;
+    if (tuning_env("BARQ_GEMV_DMA") < 0 || k == 0 || n_rows > (size_t)INT32_MAX) return false;
     if (((uintptr_t)W & 3) || ((uintptr_t)xq & 3)) return false;
     size_t rb = 0, xch = 0;
     switch (w_type) {

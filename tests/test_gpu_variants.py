@@ -1,0 +1,124 @@
+"""Every launch-shape override the kernels accept (the BARQ_GEMM_*,
+BARQ_GEMV_* and BARQ_ATTN_* tuning variables, read at each launch) against
+the oracle, in one process: the variants that measured slower stay off by
+default but must still compute the same product.  Bars as in
+test_gpu_parity.py / test_gpu_attention.py."""
+import contextlib
+import os
+
+import numpy as np
+import pytest
+
+import barq_rocm as B
+from barq_rocm import attention as A
+from barq_rocm import synth
+from conftest import assert_close_1e3
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@contextlib.contextmanager
+def env(**kv):
+    old = {k: os.environ.get(k) for k in kv}
+    os.environ.update({k: str(v) for k, v in kv.items()})
+    try:
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+GEN = {B.Q4_K: synth.gen_q4_k, B.Q6_K: synth.gen_q6_k, B.Q4_0: synth.gen_q4_0, B.Q8_0: synth.gen_q8_0}
+
+
+def matmul_case(orc, w_type, n, k, m, seed):
+    w = GEN[w_type](n, k, seed)
+    x = synth.gen_f32(m * k, seed + 1).reshape(m, k)
+    xq = orc.quantize_act(B.Q8_PARTNER[w_type], x)
+    return w, xq, orc.matmul(w_type, w, n, k, B.Q8_PARTNER[w_type], xq, m)
+
+
+GEMM_VARIANTS = [
+    dict(BARQ_GEMM_KG=1), dict(BARQ_GEMM_KG=2), dict(BARQ_GEMM_BM=32), dict(BARQ_GEMM_BM=64),
+    dict(BARQ_GEMM_BM=65, BARQ_GEMM_KG=1), dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=2),
+    dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=2),
+    dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=3), dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=4),
+    dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1), dict(BARQ_GEMM_XCD=0), dict(BARQ_GEMM_IMPL=0),
+]
+
+
+@pytest.mark.parametrize("w_type", [B.Q4_K, B.Q6_K])
+def test_gemm_variants(be, orc, w_type):
+    n, k, m = 384, 2048, 72
+    w, xq, ref = matmul_case(orc, w_type, n, k, m, 900 + w_type)
+    wd, xd = dev(w), dev(xq)
+    for v in GEMM_VARIANTS:
+        print("gemm variant", w_type, v, flush=True)
+        with env(**v):
+            got = be.matmul(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd, m).cpu().numpy()
+        assert_close_1e3(got, ref)
+
+
+GEMV_VARIANTS = [dict(BARQ_GEMV_DMA=c) for c in (-1, 422, 444, 482, 822, 842, 222, 242, 411, 811)] + [
+    dict(BARQ_GEMV_DMA_TYPES=0), dict(BARQ_GEMV_DMA_TYPES=31)] + [
+    dict(BARQ_GEMV_DMA_TYPES=0, BARQ_GEMV_CFG=c) for c in ("1,4", "2,4", "4,4", "8,4", "1,8", "2,8", "4,8", "2,2",
+                                                          "4,2", "8,2", "4,1")]
+
+
+@pytest.mark.parametrize("w_type", [B.Q4_K, B.Q6_K, B.Q4_0, B.Q8_0])
+def test_gemv_variants(be, orc, w_type):
+    n, k = 517, 4096
+    w, xq, ref = matmul_case(orc, w_type, n, k, 1, 950 + w_type)
+    wd, xd = dev(w), dev(xq)
+    for v in GEMV_VARIANTS:
+        print("gemv variant", w_type, v, flush=True)
+        with env(**v):
+            got = be.matvec(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd).cpu().numpy()
+        assert_close_1e3(got, ref.ravel())
+
+
+MOE_VARIANTS = [dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_NS=3),
+                dict(BARQ_GEMM_NS=4), dict(BARQ_GEMM_KS=1), dict(BARQ_GEMM_KS=2), dict(BARQ_GEMM_KS=4)]
+
+
+def test_moe_variants(be, orc):
+    ne, hid, nff, rows, k = 6, 512, 2048, 40, 2
+    gates = [synth.gen_q4_k(nff, hid, 70 + e) for e in range(ne)]
+    ups = [synth.gen_q4_k(nff, hid, 80 + e) for e in range(ne)]
+    downs = [synth.gen_q6_k(hid, nff, 90 + e) for e in range(ne)]
+    x = synth.gen_f32(rows * hid, 99).reshape(rows, hid)
+    ids, w = orc.moe_select_top_k(synth.gen_f32(rows * ne, 98).reshape(rows, ne), k)
+    ids, w = np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(w, np.float32)
+    ref = orc.moe_ffn(B.Q4_K, gates, B.Q4_K, ups, B.Q6_K, downs, hid, nff, x, ids, w, orc.Q8_K)
+    gd, ud, dd = [dev(a) for a in gates], [dev(a) for a in ups], [dev(a) for a in downs]
+    for v in MOE_VARIANTS:
+        print("moe variant", v, flush=True)
+        with env(**v):
+            got = be.moe_ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, hid, nff, dev(x), rows, dev(ids), dev(w), k,
+                             B.ACT_F32_Q8).cpu().numpy()
+        assert_close_1e3(got, ref)
+
+
+def test_attention_split_variants(be, orc):
+    n_head, n_kv, hd, kv = 16, 4, 128, 1500
+    rng = np.random.default_rng(17)
+    k = rng.standard_normal((n_kv, kv, hd)).astype(np.float32)
+    v = rng.standard_normal((n_kv, kv, hd)).astype(np.float32)
+    c = A.KVCache(be, kv, 1, n_kv, hd)
+    c.append(0, k, v, kv, hd, mem=B.MEM_HOST)
+    q = rng.standard_normal((n_head, 2, hd)).astype(np.float32)
+    ref = orc.attention(q, k, v, n_head, 2, kv, kv - 2)
+    for wg in (1, 8, 64, 256, 4096):
+        print("attention workgroup target", wg, flush=True)
+        with env(BARQ_ATTN_WG=wg):
+            got = A.compute_attention(be, q, c, 0, n_head, n_kv, hd, 2, kv, kv - 2, mem=B.MEM_HOST)
+        assert np.max(np.abs(got - ref)) <= 2e-5 * np.max(np.abs(v))
+    c.close()
