@@ -253,7 +253,7 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
         const uint32_t so = (uint32_t)r * rb + (uint32_t)it * P::SLICE_BYTES;
         uint8_t* dst = bufs + (u % D) * SL;
         #pragma unroll
-        for (int q = 0; q < SI; q++) lds_load16(wr, dst + 1024 * q, voff[q] == DMA_SKIP ? DMA_SKIP : voff[q] + so, 0);
+        for (int q = 0; q < SI; q++) lds_load16_nt(wr, dst + 1024 * q, voff[q] == DMA_SKIP ? DMA_SKIP : voff[q] + so, 0);
     };
     const int U = n_it * R;   // >= R >= D
     if (live) {
