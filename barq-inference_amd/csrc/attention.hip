@@ -110,6 +110,14 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// K/V rows are streamed once per call: loaded with the non-temporal hint
+// (measured in one run: 55.1 -> 49.5 us at 32K positions, 14.1 -> 13.5 us at 4K)
+typedef float f32x4n __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ntf4(const f32x4n* p) {
+    const f32x4n v = __builtin_nontemporal_load(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // Partial state of one (query row, head, split): running max m (log2 units),
 // sum l, then HD output sums.  Stored as HD + 2 floats.
 //
@@ -170,10 +178,10 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
         for (int p = 0; p < P; p++) {
             const int j = blk + p * R + r;
             if (j < j1) {
-                const float4* kp = reinterpret_cast<const float4*>(kh + (size_t)j * HD);
-                const float4* vp = reinterpret_cast<const float4*>(vh + (size_t)j * HD);
-                b.k[p][0] = kp[c]; b.k[p][1] = kp[c + LPR];
-                b.v[p][0] = vp[c]; b.v[p][1] = vp[c + LPR];
+                const f32x4n* kp = reinterpret_cast<const f32x4n*>(kh + (size_t)j * HD);
+                const f32x4n* vp = reinterpret_cast<const f32x4n*>(vh + (size_t)j * HD);
+                b.k[p][0] = ntf4(kp + c); b.k[p][1] = ntf4(kp + c + LPR);
+                b.v[p][0] = ntf4(vp + c); b.v[p][1] = ntf4(vp + c + LPR);
             } else {
                 b.k[p][0] = b.k[p][1] = b.v[p][0] = b.v[p][1] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
