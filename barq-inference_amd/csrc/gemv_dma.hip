@@ -346,8 +346,10 @@ static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const voi
     BARQ_DMA_CASE(8, 1, 1)
     default:
         // measured on MI355X: four rows per wave for the 128256-row Q6_K head
-        // (C3), two for the 4096-row Q4_0 matrix (C1)
+        // (C3); for the 32-element formats one row per wave (more
+        // workgroups) up to 8192 rows (C1: 3.82 against 3.94 us), two above
         if constexpr (P::SLICE_BLOCKS == 16) return launch_dma<P, 4, 4, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+        else if (n_rows <= 8192) return launch_dma<P, 4, 1, 1>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
         else return launch_dma<P, 4, 2, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
     }
 #undef BARQ_DMA_CASE
