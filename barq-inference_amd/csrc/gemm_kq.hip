@@ -26,6 +26,7 @@
 #include "launch.hpp"
 #include "mfma_common.hpp"
 
+#include <atomic>
 #include <cstdlib>
 #include <utility>
 
@@ -740,15 +741,15 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
 // ---- launch ------------------------------------------------------------------
 
 static int cu_count() {
-    static int n[64] = {};
+    static std::atomic<int> n[64] = {};   // per device; racing callers store the same value
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!n[dev]) {
-        int v = 0;
+    int v = n[dev].load(std::memory_order_relaxed);
+    if (!v) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        n[dev] = v;
+        n[dev].store(v, std::memory_order_relaxed);
     }
-    return n[dev];
+    return v;
 }
 
 struct KQArgs {

@@ -402,13 +402,10 @@ static hipError_t launch_kq(const uint8_t* W, size_t wrb, const uint8_t* X, size
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + GM_BN - 1) / GM_BN;
     const int n_tiles = tiles_m * tiles_n;
     constexpr size_t lds = 2 * sizeof(Stage<F, BM>);
-    static bool attr_set = false;   // per template instance; the attribute is per device function
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kq_kernel<F, BM>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // set once per template instance (thread-safe static init)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kq_kernel<F, BM>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL((gemm_kq_kernel<F, BM>), dim3(n_tiles), dim3(256), lds, s, W, wrb, X, xrb, Y, M, N, nsb,
                        tiles_m, n_tiles);
     return hipGetLastError();

@@ -148,7 +148,7 @@ void gemv_f32_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const floa
 
 // ---- launch configuration ---------------------------------------------------
 // (rows per wave, waves per workgroup) for the integer path.  The default for
-// each format was chosen by sweeping on MI355X; gemv_set_config overrides it.
+// each format was chosen by sweeping on MI355X.
 struct GemvCfg { int r, waves; };
 
 // BARQ_GEMV_CFG="R,W" overrides the launch shape (used for tuning sweeps).
@@ -159,9 +159,7 @@ static GemvCfg env_cfg() {
     }
     return c;
 }
-static GemvCfg g_cfg_override = {0, 0};
 
-void gemv_set_config(int rows_per_wave, int waves) { g_cfg_override = {rows_per_wave, waves}; }
 
 template <class F, int R, int WAVES>
 static hipError_t launch_q8(const uint8_t* W, size_t row_bytes, const uint8_t* xq, float* y,
@@ -177,7 +175,7 @@ template <class F>
 static hipError_t dispatch_q8(const uint8_t* W, size_t row_bytes, const uint8_t* xq, float* y,
                               int n_rows, int k, hipStream_t s, GemvCfg def) {
     const GemvCfg e = env_cfg();
-    const GemvCfg c = g_cfg_override.r ? g_cfg_override : e.r ? e : def;
+    const GemvCfg c = e.r ? e : def;
 #define BARQ_GEMV_CASE(RR, WW) \
     if (c.r == RR && c.waves == WW) return launch_q8<F, RR, WW>(W, row_bytes, xq, y, n_rows, k, s);
     BARQ_GEMV_CASE(1, 4) BARQ_GEMV_CASE(2, 4) BARQ_GEMV_CASE(4, 4) BARQ_GEMV_CASE(8, 4)

@@ -314,13 +314,11 @@ static hipError_t launch_dma(const uint8_t* Wq, uint32_t rb, size_t n_rows, int 
                              uint32_t x_bytes, uint32_t x_region, float* y, hipStream_t s) {
     const size_t lds = x_region + (size_t)W * D * 1024 * P::SLICE_INSTR;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    static size_t attr = 0;   // largest dynamic LDS size enabled so far for this instance
-    if (lds > attr) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_dma_kernel<P, W, R, D>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr = lds;
-    }
+    // the whole 160 KiB enabled once per instance (thread-safe static init),
+    // so concurrent callers never lower it below their own launch
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_dma_kernel<P, W, R, D>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)((n_rows + (size_t)W * R - 1) / ((size_t)W * R));
     hipLaunchKernelGGL((gemv_dma_kernel<P, W, R, D>), dim3(grid), dim3(W * 64), lds, s, Wq, rb, xq, x_bytes, y,
                        (int)n_rows, nblk, x_region);

@@ -36,7 +36,6 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
                           float* y, hipStream_t s);
 hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
                            float* y, hipStream_t s);
-void gemv_set_config(int rows_per_wave, int waves);
 
 // gemv_dma.hip: the same GEMV streaming row slices through LDS
 bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq);
