@@ -8,12 +8,12 @@ inputs of the benchmark configurations (synth).
 """
 from . import _lib
 from ._lib import (ACT_F32, ACT_F32_Q8, BLOCK_BYTES, BLOCK_ELEMS, F16, F32, MEM_DEVICE, MEM_HOST, Q4_0,
-                   Q4_0_BARQ, Q4_K, Q6_K, Q8_0, Q8_K, Q8_PARTNER, BarqError)
+                   Q4_0_BARQ, Q4_K, Q4_K_BARQ, Q6_K, Q8_0, Q8_K, Q8_PARTNER, BarqError)
 from .backend import Backend
 
 __all__ = [
     "_lib", "Backend", "BarqError", "ACT_F32", "ACT_F32_Q8", "BLOCK_BYTES", "BLOCK_ELEMS", "F16", "F32",
-    "MEM_DEVICE", "MEM_HOST", "Q4_0", "Q4_0_BARQ", "Q4_K", "Q6_K", "Q8_0", "Q8_K", "Q8_PARTNER",
+    "MEM_DEVICE", "MEM_HOST", "Q4_0", "Q4_0_BARQ", "Q4_K", "Q4_K_BARQ", "Q6_K", "Q8_0", "Q8_K", "Q8_PARTNER",
 ]
 
 

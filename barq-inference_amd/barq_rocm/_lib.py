@@ -36,14 +36,15 @@ Q4_K = 12
 Q6_K = 14
 Q8_K = 15
 Q4_0_BARQ = 0x10002
+Q4_K_BARQ = 0x1000C   # the quant crate's own Q4_K (quant/src/q4_k.rs), not GGUF
 ACT_F32 = 0
 ACT_F32_Q8 = 0x20000
 
 MEM_HOST = 0
 MEM_DEVICE = 1
 
-BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_0_BARQ: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
-BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q4_0_BARQ: 20, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_0_BARQ: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256, Q4_K_BARQ: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q4_0_BARQ: 20, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292, Q4_K_BARQ: 136}
 Q8_PARTNER = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_0_BARQ: Q8_0, Q4_K: Q8_K, Q6_K: Q8_K}
 
 # every symbol include/barq_rocm.h declares
@@ -54,7 +55,8 @@ EXPORTS = (
     "barq_rocm_dequantize", "barq_rocm_quantize_act", "barq_rocm_rms_norm", "barq_rocm_rms_norm_quantize",
     "barq_rocm_matvec", "barq_rocm_matmul",
     "barq_rocm_gemm_f32", "barq_rocm_gemv_f32", "barq_rocm_dequantize_split",
-    "barq_rocm_quantized_matmul_split", "barq_rocm_quantize_q4_0_barq", "barq_rocm_moe_route",
+    "barq_rocm_quantized_matmul_split", "barq_rocm_quantize_q4_0_barq", "barq_rocm_quantize_q4_k_barq",
+    "barq_rocm_q4_k_barq_bytes", "barq_rocm_moe_route",
     "barq_rocm_moe_ffn", "barq_rocm_gguf_open", "barq_rocm_gguf_close", "barq_rocm_gguf_info",
     "barq_rocm_gguf_tensor", "barq_rocm_gguf_find_tensor", "barq_rocm_gguf_kv_type", "barq_rocm_gguf_kv_int",
     "barq_rocm_gguf_kv_number", "barq_rocm_gguf_kv_string", "barq_rocm_cache_create", "barq_rocm_cache_get",
@@ -106,6 +108,8 @@ def _declare(lib):
         "barq_rocm_dequantize_split": (_i, [_vp, _i, _vp, _sz, _vp, _sz, _sz, _vp, _sz, _i]),
         "barq_rocm_quantized_matmul_split": (_i, [_vp, _vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _i, _sz, _i]),
         "barq_rocm_quantize_q4_0_barq": (_i, [_vp, _vp, _sz, _vp, _i]),
+        "barq_rocm_quantize_q4_k_barq": (_i, [_vp, _vp, _sz, _vp, _i]),
+        "barq_rocm_q4_k_barq_bytes": (_sz, [_sz]),
         "barq_rocm_moe_route": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i]),
         "barq_rocm_moe_ffn": (_i, [_vp, _sz, _i, _vp, _i, _vp, _i, _vp, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp, _i]),
         "barq_rocm_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),

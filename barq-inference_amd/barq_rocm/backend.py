@@ -195,6 +195,20 @@ class Backend:
             self.sync()
         return out
 
+    def quantize_q4_k_barq(self, x, mem=L.MEM_DEVICE):
+        """quant::Q4_K::quantize (quant/src/q4_k.rs:23-73)."""
+        n = x.size if mem == L.MEM_HOST else x.numel()
+        nbytes = self._lib.barq_rocm_q4_k_barq_bytes(n)
+        if mem == L.MEM_HOST:
+            out = np.empty(nbytes, dtype=np.uint8)
+        else:
+            import torch
+            out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        L.check(self._lib.barq_rocm_quantize_q4_k_barq(self.h, _ptr(x), n, _ptr(out), mem))
+        if mem == L.MEM_DEVICE:
+            self.sync()
+        return out
+
     def moe_route(self, logits, rows, n_experts, top_k, mem=L.MEM_DEVICE):
         k = max(1, min(top_k, n_experts))
         if mem == L.MEM_HOST:

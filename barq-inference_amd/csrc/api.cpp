@@ -46,7 +46,7 @@ size_t blk_elems(int t) {
     switch (t) {
     case BARQ_TYPE_F32: case BARQ_TYPE_F16: return 1;
     case BARQ_TYPE_Q4_0: case BARQ_TYPE_Q8_0: case BARQ_TYPE_Q4_0_BARQ: return 32;
-    case BARQ_TYPE_Q4_K: case BARQ_TYPE_Q6_K: case BARQ_TYPE_Q8_K: return 256;
+    case BARQ_TYPE_Q4_K: case BARQ_TYPE_Q6_K: case BARQ_TYPE_Q8_K: case BARQ_TYPE_Q4_K_BARQ: return 256;
     default: return 0;
     }
 }
@@ -57,6 +57,7 @@ size_t blk_bytes(int t) {
     case BARQ_TYPE_F16: return 2;
     case BARQ_TYPE_Q4_0: return 18;
     case BARQ_TYPE_Q4_0_BARQ: return 20;
+    case BARQ_TYPE_Q4_K_BARQ: return 136;
     case BARQ_TYPE_Q8_0: return 34;
     case BARQ_TYPE_Q4_K: return 144;
     case BARQ_TYPE_Q6_K: return 210;
@@ -75,7 +76,7 @@ size_t row_bytes_of(int t, size_t k) {
 size_t weight_align(int t) {
     switch (t) {
     case BARQ_TYPE_Q4_K: return 16;
-    case BARQ_TYPE_Q4_0_BARQ: case BARQ_TYPE_Q8_K: case BARQ_TYPE_F32: return 4;
+    case BARQ_TYPE_Q4_0_BARQ: case BARQ_TYPE_Q4_K_BARQ: case BARQ_TYPE_Q8_K: case BARQ_TYPE_F32: return 4;
     default: return 2;
     }
 }
@@ -510,6 +511,30 @@ int barq_rocm_quantize_q4_0_barq(barq_rocm_handle* h, const float* x, size_t n, 
     BARQ_HIP(hipStreamSynchronize(h->stream));
     return ok();
 }
+
+int barq_rocm_quantize_q4_k_barq(barq_rocm_handle* h, const float* x, size_t n, uint8_t* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (n == 0) return ok();
+    if (!x || !out) return fail(BARQ_E_INVALID, "quantize_q4_k_barq: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h->device);
+    const size_t ob_bytes = barq_rocm_q4_k_barq_bytes(n);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(out, 4)) return fail(BARQ_E_INVALID, "quantize_q4_k_barq: out must be 4-byte aligned");
+        return launched(barq::quantize_q4_k_barq_launch(x, n, out, h->stream), "quantize_q4_k_barq");
+    }
+    Arena a;
+    size_t ox = a.add(n * 4), oo = a.add(ob_bytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::quantize_q4_k_barq_launch(at<float>(h, ox), n, at<uint8_t>(h, oo), h->stream),
+                        "quantize_q4_k_barq"));
+    BARQ_HIP(hipMemcpyAsync(out, at<uint8_t>(h, oo), ob_bytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+size_t barq_rocm_q4_k_barq_bytes(size_t n) { return n / 256 * 136 + (n % 256 ? 8 + (n % 256 + 1) / 2 : 0); }
 
 // ---------------------------------------------------------------------------
 // MoE

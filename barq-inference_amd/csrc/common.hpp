@@ -22,12 +22,13 @@ inline int tuning_env(const char* name, int def = 0) {
 // from gguf.rs:529-530,645,747,854 and llama.cpp block_q4_0/block_q8_K).
 constexpr int QK4_0 = 32, Q4_0_BYTES = 18;
 constexpr int Q4_0_BARQ_BYTES = 20;
+constexpr int Q4_K_BARQ_BYTES = 136;   // the quant crate's own Q4_K (quant/src/q4_k.rs)
 constexpr int QK8_0 = 32, Q8_0_BYTES = 34;
 constexpr int QK_K = 256, Q4_K_BYTES = 144, Q6_K_BYTES = 210, Q8_K_BYTES = 292;
 
 constexpr int TYPE_F32 = 0, TYPE_F16 = 1, TYPE_Q4_0 = 2, TYPE_Q8_0 = 8,
               TYPE_Q4_K = 12, TYPE_Q6_K = 14, TYPE_Q8_K = 15,
-              TYPE_Q4_0_BARQ = 0x10002;
+              TYPE_Q4_0_BARQ = 0x10002, TYPE_Q4_K_BARQ = 0x1000C;
 
 constexpr int WAVE = 64;
 

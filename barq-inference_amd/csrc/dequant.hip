@@ -37,6 +37,17 @@ __device__ __forceinline__ void deq4_at(const uint8_t* __restrict__ src, size_t 
             int qs = n >= 8 ? n - 16 : n;
             v[j] = (float)qs * scale;
         }
+    } else if constexpr (TYPE == TYPE_Q4_K_BARQ) {
+        // quant/src/q4_k.rs:76-132: f32 scale_min, f32 scale_max (the range),
+        // 128 nibble bytes (element i: low nibble of byte i/2 if i is even);
+        // y = scale_min + (q / 15) * scale_max
+        const uint8_t* p = src + (e / 256) * Q4_K_BARQ_BYTES;
+        const int i = (int)(e % 256);
+        const float smin = *reinterpret_cast<const float*>(p);
+        const float srange = *reinterpret_cast<const float*>(p + 4);
+        const uint32_t q = ld_u16(p + 8 + i / 2);
+        #pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = smin + ((float)((q >> (4 * j)) & 15u) / 15.0f) * srange;
     } else if constexpr (TYPE == TYPE_Q8_0) {
         // gguf.rs:658-676: (q as i8) as f32 * scale
         const uint8_t* p = src + (e / 32) * 34;
@@ -134,6 +145,7 @@ hipError_t dequant_launch(int type, const void* blocks, size_t n_elems, float* o
     switch (type) {
     case TYPE_Q4_0: hipLaunchKernelGGL(dequant_kernel<TYPE_Q4_0>, g, b, 0, s, src, o, n4); break;
     case TYPE_Q4_0_BARQ: hipLaunchKernelGGL(dequant_kernel<TYPE_Q4_0_BARQ>, g, b, 0, s, src, o, n4); break;
+    case TYPE_Q4_K_BARQ: hipLaunchKernelGGL(dequant_kernel<TYPE_Q4_K_BARQ>, g, b, 0, s, src, o, n4); break;
     case TYPE_Q8_0: hipLaunchKernelGGL(dequant_kernel<TYPE_Q8_0>, g, b, 0, s, src, o, n4); break;
     case TYPE_Q4_K: hipLaunchKernelGGL(dequant_kernel<TYPE_Q4_K>, g, b, 0, s, src, o, n4); break;
     case TYPE_Q6_K: hipLaunchKernelGGL(dequant_kernel<TYPE_Q6_K>, g, b, 0, s, src, o, n4); break;

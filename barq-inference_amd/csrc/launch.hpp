@@ -17,6 +17,8 @@ hipError_t dequant_split_launch(int kind_q8_0, const uint8_t* quants, size_t n_q
 hipError_t quantize_q8_0_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s);
 hipError_t quantize_q8_k_launch(const float* x, size_t n_rows, size_t k, void* out, hipStream_t s);
 hipError_t quantize_q4_0_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s);
+// quant::Q4_K::quantize (quant/src/q4_k.rs:23-73): 136-byte blocks, a shorter last one
+hipError_t quantize_q4_k_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s);
 // Q8_K rows of x[rows_idx[i] * k ..] for i < n_rows (gather fused in)
 hipError_t quantize_q8_k_gather_launch(const float* x, const int32_t* rows_idx, size_t n_rows, size_t k, void* out,
                                        hipStream_t s);

@@ -177,6 +177,61 @@ hipError_t swiglu_q8_k_launch(const float* g, const float* u, size_t n_rows, siz
     return hipGetLastError();
 }
 
+// quant::Q4_K::quantize (quant/src/q4_k.rs:23-73), the quant crate's own
+// 4-bit format: blocks of 256 (the last one may be shorter); per block the
+// f32 min and max (folds that skip NaN), scale_max = max - min,
+// q = clamp(round((x - min) / scale_max * 15), 0, 15) (7.5 -> 8 when
+// scale_max is 0; Rust's half-away-from-zero round, NaN -> 0 as `as u8`
+// does), two per byte, low nibble first.  A block is 8 + ceil(len/2) bytes.
+// One wave per block, four elements per lane.
+__global__ __launch_bounds__(256) void quantize_q4_k_barq_kernel(const float* __restrict__ x, size_t n,
+                                                                 uint8_t* __restrict__ out, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;
+    const int lane = threadIdx.x & 63;
+    const size_t e0 = b * 256;
+    const int len = (int)(n - e0 < 256 ? n - e0 : 256);
+    float v[4];
+    float mn = INFINITY, mx = -INFINITY;
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = 4 * lane + j;
+        v[j] = i < len ? x[e0 + i] : 0.0f;
+        if (i < len) {
+            mn = fminf(mn, v[j]);
+            mx = fmaxf(mx, v[j]);
+        }
+    }
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off));
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    const float range = mx - mn;
+    uint32_t q[4];
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float t = range == 0.0f ? 7.5f : (v[j] - mn) / range * 15.0f;
+        const float r = fminf(fmaxf(roundf(t), 0.0f), 15.0f);
+        q[j] = (r == r && 4 * lane + j < len) ? (uint32_t)r : 0u;   // NaN -> 0; past the block: 0
+    }
+    uint8_t* p = out + b * Q4_K_BARQ_BYTES;
+    if (lane == 0) {
+        reinterpret_cast<float*>(p)[0] = mn;
+        reinterpret_cast<float*>(p)[1] = range;
+    }
+    const int nbytes = (len + 1) / 2;
+    if (2 * lane < nbytes) p[8 + 2 * lane] = (uint8_t)(q[0] | (q[1] << 4));
+    if (2 * lane + 1 < nbytes) p[9 + 2 * lane] = (uint8_t)(q[2] | (q[3] << 4));
+}
+
+hipError_t quantize_q4_k_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s) {
+    const size_t nb = (n + 255) / 256;
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q4_k_barq_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, x, n, out, nb);
+    return hipGetLastError();
+}
+
 hipError_t quantize_q4_0_barq_launch(const float* x, size_t n, uint8_t* out, hipStream_t s) {
     const size_t nb = n / 32;
     if (nb == 0) return hipSuccess;

@@ -63,7 +63,9 @@ typedef enum {
     BARQ_TYPE_Q4_K = 12,       /* f16 d, f16 dmin, 12 B 6-bit scales/mins, 128 B nibbles; 256 elems */
     BARQ_TYPE_Q6_K = 14,       /* 128 B ql, 64 B qh, 16 x i8 scales, f16 d; 256 elems */
     BARQ_TYPE_Q8_K = 15,       /* f32 d, 256 x i8, 16 x i16 bsums (activations) */
-    BARQ_TYPE_Q4_0_BARQ = 0x10002 /* f32 scale + 16 B; elem i in byte i/2 (low if even), sign-extended */
+    BARQ_TYPE_Q4_0_BARQ = 0x10002, /* f32 scale + 16 B; elem i in byte i/2 (low if even), sign-extended */
+    BARQ_TYPE_Q4_K_BARQ = 0x1000C  /* the quant crate's own Q4_K (quant/src/q4_k.rs:7-133, not GGUF):
+                                      f32 min, f32 range, 128 B nibbles (low first); 136 B per 256 */
 } barq_type;
 
 /* Activation mode for matvec/matmul.  BARQ_ACT_F32 keeps x in f32 and
@@ -193,6 +195,18 @@ int barq_rocm_quantized_matmul_split(barq_rocm_handle* h, const float* a,
  * BARQ_TYPE_Q4_0_BARQ blocks, bit-identical.  n must be a multiple of 32. */
 int barq_rocm_quantize_q4_0_barq(barq_rocm_handle* h, const float* x, size_t n,
                                  uint8_t* out, int mem);
+
+/* quant::Q4_K (quant/src/q4_k.rs:7-133), the quant crate's own 4-bit format
+ * (never produced by the GGUF loader): quantize = Q4_K::quantize (:23-73):
+ * per block of 256 (the last may be shorter) f32 scale_min = min, f32
+ * scale_max = max - min, q = clamp(round((x - min) / scale_max * 15), 0, 15)
+ * (7.5 rounded when scale_max is 0), two per byte low nibble first; a block
+ * of len elements is 8 + ceil(len/2) bytes (barq_rocm_q4_k_barq_bytes(n)
+ * for n elements).  Dequantize with barq_rocm_dequantize(BARQ_TYPE_Q4_K_BARQ)
+ * = Q4_K::dequantize (:75-133) on whole 136-byte blocks:
+ * y = scale_min + (q / 15) * scale_max. */
+size_t barq_rocm_q4_k_barq_bytes(size_t n);
+int barq_rocm_quantize_q4_k_barq(barq_rocm_handle* h, const float* x, size_t n, uint8_t* out, int mem);
 
 /* ---- fused MoE ---------------------------------------------------------
  * MoEFusedOps (models/src/moe_fused.rs:41-309).

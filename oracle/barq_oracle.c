@@ -687,6 +687,59 @@ int orc_moe_ffn(int gate_type, const uint8_t* const* gate,
     return orc_moe_dispatch(x, rows, hidden, n_experts, ids, weights, k, moe_expert_ffn, &c, out);
 }
 
+/* ---- the quant crate's own Q4_K ------------------------------------------- */
+
+size_t orc_q4_k_barq_quantize(const float* x, size_t n, uint8_t* out) {
+    size_t o = 0;
+    for (size_t start = 0; start < n; start += 256) {             /* :27-33 */
+        const size_t end = start + 256 < n ? start + 256 : n, len = end - start;
+        float mn = INFINITY, mx = -INFINITY;                        /* :39-40, f32::min / f32::max folds */
+        for (size_t i = start; i < end; i++) {
+            mn = fminf(mn, x[i]);
+            mx = fmaxf(mx, x[i]);
+        }
+        const float scale_min = mn, scale_max = mx - mn;            /* :43-44 */
+        const size_t nq = (len + 1) / 2;
+        uint8_t* q = out + o + 8;
+        memset(q, 0, nq);
+        for (size_t i = 0; i < len; i++) {                          /* :49-62 */
+            const float normalized = scale_max == 0.0f ? 7.5f : (x[start + i] - scale_min) / scale_max * 15.0f;
+            float r = roundf(normalized);                           /* f32::round: half away from zero */
+            if (r < 0.0f) r = 0.0f;                                 /* f32::clamp(0, 15) */
+            if (r > 15.0f) r = 15.0f;
+            const uint8_t qv = r != r ? 0 : (uint8_t)r;            /* `as u8`: NaN -> 0 */
+            q[i / 2] |= (uint8_t)(qv << (i % 2 ? 4 : 0));
+        }
+        memcpy(out + o, &scale_min, 4);                             /* :64-68, little-endian */
+        memcpy(out + o + 4, &scale_max, 4);
+        o += 8 + nq;
+    }
+    return o;
+}
+
+size_t orc_q4_k_barq_dequantize(const uint8_t* in, size_t in_len, size_t output_size, float* out) {
+    const size_t n_blocks = (output_size + 255) / 256;
+    size_t off = 0, w = 0;
+    for (size_t b = 0; b < n_blocks; b++) {
+        if (off + 8 > in_len) break;                                /* :86-88 */
+        float scale_min, scale_max;
+        memcpy(&scale_min, in + off, 4);
+        memcpy(&scale_max, in + off + 4, 4);
+        off += 8;
+        if (off + 128 > in_len) break;                              /* :108-111 */
+        const uint8_t* quants = in + off;
+        off += 128;
+        for (size_t i = 0; i < 256; i++) {                          /* :117-127 */
+            const uint8_t q = (uint8_t)((quants[i / 2] >> (i % 2 ? 4 : 0)) & 0x0F);
+            const float t = (float)q / 15.0f;
+            const float u = t * scale_max;
+            if (w < output_size) out[w] = scale_min + u;
+            w++;
+        }
+    }
+    return w < output_size ? w : output_size;                       /* :130 truncate */
+}
+
 /* ---- attention ------------------------------------------------------------ */
 
 void orc_rope(const float* x, size_t seq, size_t heads, size_t hd, size_t start_pos, float freq_scale,

@@ -151,6 +151,15 @@ int orc_moe_ffn(int gate_type, const uint8_t* const* gate,
                 const float* x, size_t rows, const int32_t* ids,
                 const float* weights, size_t k, int act, float* out);
 
+/* ---- the quant crate's own Q4_K (quant/src/q4_k.rs, not GGUF) --------- */
+/* Q4_K::quantize (:23-73): blocks of 256, the last may be shorter; per
+   block f32 scale_min, f32 scale_max (= max - min), ceil(len/2) nibble
+   bytes.  Returns the bytes written. */
+size_t orc_q4_k_barq_quantize(const float* x, size_t n, uint8_t* out);
+/* Q4_K::dequantize (:75-133): whole 136-byte blocks while the input lasts,
+   truncated to output_size.  Returns the number of values written. */
+size_t orc_q4_k_barq_dequantize(const uint8_t* in, size_t in_len, size_t output_size, float* out);
+
 /* ---- attention (transformer.rs:176-374, context.rs:245-340) ------------ */
 /* apply_rope (models/src/transformer.rs:514-562): x [seq x heads*hd] ->
    out [heads x seq x hd]; layout 0 = Interleaved (pairs 2i, 2i+1), 1 =

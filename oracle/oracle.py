@@ -51,6 +51,8 @@ def lib():
             "orc_moe_batch_by_expert": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
             "orc_moe_dispatch": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
             "orc_moe_ffn": (_i, [_i, _vp, _i, _vp, _i, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp]),
+            "orc_q4_k_barq_quantize": (_sz, [_vp, _sz, _vp]),
+            "orc_q4_k_barq_dequantize": (_sz, [_vp, _sz, _sz, _vp]),
             "orc_rope": (None, [_vp, _sz, _sz, _sz, _sz, ctypes.c_float, _vp, _i, _vp]),
             "orc_transpose_heads": (None, [_vp, _sz, _sz, _sz, _vp]),
             "orc_attention": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
@@ -150,6 +152,25 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     y = np.empty((rows, n), dtype=np.float32)
     lib().orc_rms_norm(_p(x), _p(w), rows, n, eps, _p(y))
     return y
+
+
+def q4_k_barq_quantize(x: np.ndarray) -> np.ndarray:
+    """quant::Q4_K::quantize (quant/src/q4_k.rs:23-73)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    n = x.size
+    out = np.zeros(n // 256 * 136 + (8 + (n % 256 + 1) // 2 if n % 256 else 0), dtype=np.uint8)
+    got = lib().orc_q4_k_barq_quantize(_p(x), n, _p(out))
+    assert got == out.size
+    return out
+
+
+def q4_k_barq_dequantize(data: np.ndarray, output_size: int) -> np.ndarray:
+    """quant::Q4_K::dequantize (quant/src/q4_k.rs:75-133); may return fewer
+    than output_size values, as the reference does."""
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.zeros(max(output_size, 1), dtype=np.float32)
+    w = lib().orc_q4_k_barq_dequantize(_p(data), data.size, output_size, _p(out))
+    return out[:w]
 
 
 def rope(x: np.ndarray, seq: int, heads: int, hd: int, start_pos: int, freq_scale: float, inv_freq: np.ndarray,

@@ -332,3 +332,18 @@ def test_moe_ffn_grouped_cases(be, orc, name):
                      dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
     ref = orc.moe_ffn(gt, gates, ut, ups, dt, downs, hid, nff, x, ids, w, orc.Q8_K)
     assert_close_1e3(host(out), ref)
+
+
+# ---- the quant crate's own Q4_K (quant/src/q4_k.rs): encode and decode bit-exact ----
+@pytest.mark.parametrize("n", [256, 256 * 37, 256 * 5 + 37, 100, 1])
+def test_q4_k_barq_quantize_and_dequantize_bit_exact(be, orc, n):
+    x = synth.gen_f32(n, 600 + n)
+    x[::97] *= 40.0
+    ref = orc.q4_k_barq_quantize(x)
+    got = be.quantize_q4_k_barq(dev(x)).cpu().numpy()
+    assert np.array_equal(got, ref)
+    assert np.array_equal(be.quantize_q4_k_barq(x, mem=B.MEM_HOST), ref)
+    whole = n // 256 * 256
+    if whole:
+        deq = be.dequantize(B.Q4_K_BARQ, dev(ref[:whole // 256 * 136]), whole).cpu().numpy()
+        assert_bits_equal(deq, orc.q4_k_barq_dequantize(ref, whole))

@@ -312,3 +312,44 @@ def test_block_geometry(orc):
     for t, e, nb in [(orc.Q4_0, 32, 18), (orc.Q4_0_BARQ, 32, 20), (orc.Q8_0, 32, 34), (orc.Q4_K, 256, 144),
                      (orc.Q6_K, 256, 210), (orc.Q8_K, 256, 292)]:
         assert orc.block_elems(t) == e and orc.block_bytes(t) == nb
+
+
+# ---- the quant crate's own Q4_K (quant/src/q4_k.rs; not the GGUF format) --------------
+def test_q4_k_barq_reference_roundtrip(orc):
+    # quant/src/q4_k.rs:166-180: 0..256 round trip keeps the length, no NaN
+    x = np.arange(256, dtype=np.float32)
+    q = orc.q4_k_barq_quantize(x)
+    assert q.size == 136
+    y = orc.q4_k_barq_dequantize(q, 256)
+    assert y.size == 256 and not np.isnan(y).any()
+    # and for 0..255 every value is within half a step (255/15/2) of its input
+    assert np.max(np.abs(y - x)) <= 255.0 / 30.0 + 1e-4
+
+
+def test_q4_k_barq_layout_and_closed_forms(orc):
+    x = np.array([3.0, -1.0, 7.0, 1.0] * 64, dtype=np.float32)
+    q = orc.q4_k_barq_quantize(x)
+    smin, srange = np.frombuffer(q[:8].tobytes(), dtype=np.float32)
+    assert smin == -1.0 and srange == 8.0
+    # (x - min) / range * 15: 3 -> 7.5 -> 8 (half away from zero), -1 -> 0, 7 -> 15, 1 -> 3.75 -> 4
+    assert q[8] == (8 | (0 << 4)) and q[9] == (15 | (4 << 4))
+    y = orc.q4_k_barq_dequantize(q, 256)
+    assert y[1] == -1.0 and y[2] == np.float32(-1.0) + np.float32(np.float32(15) / np.float32(15)) * np.float32(8.0)
+    # a constant block: range 0, every q = round(7.5) = 8, decodes to the constant
+    c = orc.q4_k_barq_quantize(np.full(256, 2.5, dtype=np.float32))
+    assert np.all(c[8:] == 0x88) and np.all(orc.q4_k_barq_dequantize(c, 256) == 2.5)
+
+
+def test_q4_k_barq_partial_block_and_truncation(orc):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(256 + 37).astype(np.float32)
+    q = orc.q4_k_barq_quantize(x)
+    assert q.size == 136 + 8 + 19          # the last block: 8 + ceil(37 / 2) bytes, odd length -> high nibble 0
+    assert q[-1] >> 4 == 0
+    # the reference's dequantize reads whole 136-byte blocks only: the short block is dropped
+    y = orc.q4_k_barq_dequantize(q, x.size)
+    assert y.size == 256
+    step = (x[:256].max() - x[:256].min()) / 15.0
+    assert np.max(np.abs(y - x[:256])) <= step / 2 * (1 + 1e-5)
+    # a decoder that read the short block's nibbles anyway would return 293 values
+    assert orc.q4_k_barq_dequantize(q, x.size + 1000).size == 256
