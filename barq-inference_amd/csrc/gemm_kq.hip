@@ -787,7 +787,8 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Overrides: BARQ_GEMM_BM (16, 32, 64, or 65 = 64 rows with eight waves),
+// Overrides: BARQ_GEMM_BM (16, 32, 64, or 65 = 64 rows with eight waves of
+// 32 x 32 per K-group),
 // BARQ_GEMM_NS (stages), BARQ_GEMM_KG (K-groups, ungrouped), BARQ_GEMM_KS
 // (K slices of the MoE down projection).
 
@@ -796,10 +797,13 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
 // more HBM requests in flight per CU).
 template <class F, bool GROUPED>
 static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
-    // measured on MI355X: 64x128 tiles with eight waves (two per SIMD) above
-    // 32 rows, 32-row tiles with four waves for small expert groups
+    // measured on MI355X: 64x128 tiles above 32 rows, 32-row tiles with four
+    // waves for small expert groups.  With two K-groups, each wave of a 64-row
+    // tile covers both 32-row halves of its 32 columns (bm 64: the weight
+    // fragment is decoded once for two MFMA row tiles; 26.5-27.1 against
+    // 27.6-29.0 us at C4 for eight waves of 32 x 32, bm 65)
     const int g_kq_ns = tuning_env("BARQ_GEMM_NS"), g_kq_bm = tuning_env("BARQ_GEMM_BM");
-    const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 65 : 32);
+    const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 64 : 32);
     if (bm == 16) {
         if (g_kq_ns == 2) return kq_launch_t<F, 16, 2, 4, GROUPED>(a, s);
         if (g_kq_ns == 4) return kq_launch_t<F, 16, 4, 4, GROUPED>(a, s);
@@ -823,13 +827,13 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
         }
     }
     if constexpr (F::TYPE == TYPE_Q4_K) {
-        if (bm == 65) return kq_launch_t<F, 64, 4, 8, GROUPED>(a, s);
+        if (bm >= 64) return kq_launch_t<F, 64, 4, 8, GROUPED>(a, s);
         if (ns == 2) return kq_launch_t<F, 32, 2, 4, GROUPED>(a, s);
         if (ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
         if (ns == 4) return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);
         return kq_launch_t<F, 32, 5, 4, GROUPED>(a, s);
     } else {
-        if (bm == 65) return kq_launch_t<F, 64, 3, 8, GROUPED>(a, s);
+        if (bm >= 64) return kq_launch_t<F, 64, 3, 8, GROUPED>(a, s);
         if (ns == 2) return kq_launch_t<F, 32, 2, 4, GROUPED>(a, s);
         if (ns == 3) return kq_launch_t<F, 32, 3, 4, GROUPED>(a, s);
         return kq_launch_t<F, 32, 4, 4, GROUPED>(a, s);

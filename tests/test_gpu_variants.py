@@ -48,7 +48,7 @@ def matmul_case(orc, w_type, n, k, m, seed):
 
 GEMM_VARIANTS = [
     dict(BARQ_GEMM_KG=1), dict(BARQ_GEMM_KG=2), dict(BARQ_GEMM_BM=32), dict(BARQ_GEMM_BM=64),
-    dict(BARQ_GEMM_BM=65, BARQ_GEMM_KG=1), dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=2),
+    dict(BARQ_GEMM_BM=65), dict(BARQ_GEMM_BM=65, BARQ_GEMM_KG=1), dict(BARQ_GEMM_BM=64, BARQ_GEMM_KG=1), dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=2),
     dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=2),
     dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=3), dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=4),
     dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1), dict(BARQ_GEMM_XCD=0), dict(BARQ_GEMM_IMPL=0),
