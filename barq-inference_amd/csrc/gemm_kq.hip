@@ -22,7 +22,8 @@
 // barrier per super-block.  Activation rows are stored with a 16-byte pad
 // (272-byte rows: conflict-free fragment reads); Q6_K blocks are copied as the
 // dword-aligned 224-byte window around each 210-byte block (the kernel needs
-// an even number of super-blocks per row so that window offset is uniform).
+// an even number of super-blocks per row so that window offset is uniform),
+// placed 240 bytes apart for the same reason.
 #include "launch.hpp"
 #include "mfma_common.hpp"
 
@@ -41,13 +42,19 @@ struct KQWeights {
 
 // XC: 16-byte chunks per staged activation row: the 256 quants, for Q4_K the
 // 16 bsums (sub-block sums for the mins), and one pad chunk that keeps rows
-// of a 32-row fragment read on distinct LDS banks.
+// of a 32-row fragment read on distinct LDS banks.  A staged weight row is
+// PIECES 16-byte chunks (RS bytes), of which the first WP come from memory.
+// Q6_K rows carry one pad chunk (a second copy of chunk 13): at the 224-byte
+// stride lanes n and n + 4 of a fragment read start on the same bank, which
+// measured as LDS bank conflicts in 69 % of the grouped down projection's LDS
+// cycles; 240 bytes (60 dwords) puts the eight lanes of each read phase on
+// distinct banks.
 struct KQ4 {
-    static constexpr int TYPE = TYPE_Q4_K, BB = Q4_K_BYTES, RS = 144, PIECES = 9, XC = 19, XRS = 16 * XC;
+    static constexpr int TYPE = TYPE_Q4_K, BB = Q4_K_BYTES, RS = 144, PIECES = 9, WP = 9, XC = 19, XRS = 16 * XC;
     static __device__ __forceinline__ uint32_t soff(int b) { return (uint32_t)b * 144u; }
 };
 struct KQ6 {
-    static constexpr int TYPE = TYPE_Q6_K, BB = Q6_K_BYTES, RS = 224, PIECES = 14, XC = 17, XRS = 16 * XC;
+    static constexpr int TYPE = TYPE_Q6_K, BB = Q6_K_BYTES, RS = 240, PIECES = 15, WP = 14, XC = 17, XRS = 16 * XC;
     // the dword-aligned start of block b's window (row bytes are a multiple of 4)
     static __device__ __forceinline__ uint32_t soff(int b) { return (uint32_t)b * 210u & ~3u; }
 };
@@ -70,6 +77,7 @@ struct KQL {
     // 32x32 MFMA row tiles per wave; 16-row tiles use the 16x16 path (two column blocks per wave)
     static constexpr int MTW = BM >= 32 ? BM / 32 / (NW / 4) : 1;
     static_assert(KQ_BN * F::PIECES % 64 == 0, "weight tile is whole load instructions");
+    static_assert(F::RS == 16 * F::PIECES, "weight rows are whole chunks");
 };
 
 template <class F, int BM, int NW>
@@ -91,7 +99,7 @@ __device__ __forceinline__ void kq_offsets(KQOff<F, BM, NW>& o, uint32_t xrb, ui
     #pragma unroll
     for (int q = 0; q < L::W_INSTR; q++) {
         const int p = (q * NW + wave) * 64 + l, row = p / F::PIECES, piece = p - row * F::PIECES;
-        o.w[q] = (uint32_t)row * wrb + 16u * (uint32_t)piece;
+        o.w[q] = (uint32_t)row * wrb + 16u * (uint32_t)(piece < F::WP ? piece : F::WP - 1);
     }
     o.xd = (uint32_t)(64 * wave + l) * xrb;
 }
@@ -411,8 +419,22 @@ __device__ __forceinline__ void kq6_compute16(const uint8_t* st, int wave, int l
 }
 
 // ---- pipeline ----------------------------------------------------------------
-// Super-block b of the tile from one LDS stage into the accumulators (b's
-// parity places the Q6_K windows).
+// Super-block b (32-row MFMA tiles) from its weight rows ws, activation rows
+// xs and activation scales xd in LDS into the accumulators (b's parity places
+// the Q6_K windows).
+template <class F, int BM, int NW>
+__device__ __forceinline__ void kq_compute_parts(const uint8_t* ws, const uint8_t* xs, const uint8_t* xd, int b,
+                                                 int wave, int l, float (&acc)[KQL<F, BM, NW>::MTW][16]) {
+    constexpr int MT = KQL<F, BM, NW>::MTW;
+    const int n = l & 31, g2 = l >> 5;
+    const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
+    const uint8_t* wrow = ws + (32 * slice + n) * F::RS;
+    const uint8_t* xrow = xs + (mbase + n) * F::XRS + 16 * g2;
+    if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute<MT>(wrow, xrow, xd, mbase, g2, acc);
+    else kq6_compute<MT>(wrow, xrow, xd, mbase, g2, b, acc);
+}
+
+// Super-block b of the tile from one LDS stage into the accumulators.
 template <class F, int BM, int NW>
 __device__ __forceinline__ void kq_compute(const uint8_t* st, int b, int wave, int l,
                                            float (&acc)[KQL<F, BM, NW>::MTW][16]) {
@@ -422,12 +444,7 @@ __device__ __forceinline__ void kq_compute(const uint8_t* st, int b, int wave, i
         if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute16(st, wave, l, acc);
         else kq6_compute16(st, wave, l, b, acc);
     } else {
-        const int n = l & 31, g2 = l >> 5;
-        const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);   // eight waves: two per column slice
-        const uint8_t* wrow = st + L::W + (32 * slice + n) * F::RS;
-        const uint8_t* xrow = st + L::XQ + (mbase + n) * F::XRS + 16 * g2;
-        if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, acc);
-        else kq6_compute<MT>(wrow, xrow, st + L::XD, mbase, g2, b, acc);
+        kq_compute_parts<F, BM, NW>(st + L::W, st + L::XQ, st + L::XD, b, wave, l, acc);
     }
 }
 
@@ -666,6 +683,56 @@ __device__ __forceinline__ void kq_grouped_stream(uint8_t* const (&stages)[KQ_MA
         kq_stream_round<F, BM, NW, NS>(std::make_integer_sequence<int, NS>{}, st, stages, g, G, acc);
 }
 
+// The flattened (expert, m-tile, mat, K slice, n-tile) list of a grouped
+// launch: every wave builds the per-expert m-tile prefix from the device
+// offsets (lane e holds expert e); operator() maps a list index to its tile.
+template <int BM>
+struct KQExperts {
+    const KQWeights& wt;
+    const uint8_t* X;
+    uint32_t xrb;
+    float* Y;
+    int N, tiles_n, ne, nmat, ks, nsb_k, total;
+    size_t ymat, ykstride;
+    int r0, cnt, nt, inc;
+
+    __device__ __forceinline__ KQExperts(const KQWeights& wt_, const uint8_t* X_, uint32_t xrb_, float* Y_, int N_,
+                                         int nsb, int tiles_n_, const int32_t* __restrict__ offsets, int ne_,
+                                         int nmat_, size_t ymat_, int ks_, size_t ykstride_, int l)
+        : wt(wt_), X(X_), xrb(xrb_), Y(Y_), N(N_), tiles_n(tiles_n_), ne(ne_), nmat(nmat_), ks(ks_),
+          nsb_k(nsb / ks_), total(0), ymat(ymat_), ykstride(ykstride_), r0(0), cnt(0) {
+        if (l < ne) {
+            r0 = offsets[l];
+            cnt = offsets[l + 1] - r0;
+        }
+        nt = (cnt + BM - 1) / BM;
+        inc = nt;   // inclusive prefix of m-tiles over experts
+        #pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(inc, o);
+            if (l >= o) inc += v;
+        }
+        total = __builtin_amdgcn_readfirstlane(__shfl(inc, 63)) * nmat * ks * tiles_n;
+    }
+
+    __device__ __forceinline__ KQTile operator()(int t) const {
+        const int ntile = t % tiles_n, rk = t / tiles_n, ksl = rk % ks, r = rk / ks, mat = r % nmat, s = r / nmat;
+        // expert of m-slot s: the number of experts whose tiles all lie before it
+        const int e = __builtin_amdgcn_readfirstlane(__popcll(__ballot(inc <= s)));
+        const int mt = s - __builtin_amdgcn_readfirstlane(__shfl(inc - nt, e));
+        const int row0 = __builtin_amdgcn_readfirstlane(__shfl(r0, e));
+        KQTile T;
+        T.W = wt.w[mat * ne + e];
+        T.X = X + (size_t)row0 * xrb;
+        T.Y = Y + (size_t)mat * ymat + (size_t)ksl * ykstride + (size_t)row0 * N;
+        T.count = __builtin_amdgcn_readfirstlane(__shfl(cnt, e));
+        T.m0 = mt * BM;
+        T.n0 = ntile * KQ_BN;
+        T.kb0 = ksl * nsb_k;
+        return T;
+    }
+};
+
 // Ungrouped: one tile per workgroup of the M x N product with weights wt.w[0].
 // GROUPED: nmat weight sets of ne experts each; expert e's activation and
 // output rows are [offsets[e], offsets[e+1]) of X and of Y + mat * ymat, and
@@ -703,38 +770,8 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
         const int mt = tile % tiles_m, ntile = tile / tiles_m;
         kq_tile<F, BM, NS, NW, KG>(stages, wt.w[0], wrb, X, xrb, Y, M, N, nsb, mt * BM, ntile * KQ_BN, kg, wave, l);
     } else {
-        int r0 = 0, cnt = 0;
-        if (l < ne) {
-            r0 = offsets[l];
-            cnt = offsets[l + 1] - r0;
-        }
-        const int nt = (cnt + BM - 1) / BM;
-        int inc = nt;   // inclusive prefix of m-tiles over experts
-        #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(inc, o);
-            if (l >= o) inc += v;
-        }
-        const int s_total = __builtin_amdgcn_readfirstlane(__shfl(inc, 63));
-        const int total = s_total * nmat * ks * tiles_n;
-        const int nsb_k = nsb / ks;
-        auto decode = [&](int t) {
-            const int ntile = t % tiles_n, rk = t / tiles_n, ksl = rk % ks, r = rk / ks, mat = r % nmat, s = r / nmat;
-            // expert of m-slot s: the number of experts whose tiles all lie before it
-            const int e = __builtin_amdgcn_readfirstlane(__popcll(__ballot(inc <= s)));
-            const int mt = s - __builtin_amdgcn_readfirstlane(__shfl(inc - nt, e));
-            const int row0 = __builtin_amdgcn_readfirstlane(__shfl(r0, e));
-            KQTile T;
-            T.W = wt.w[mat * ne + e];
-            T.X = X + (size_t)row0 * xrb;
-            T.Y = Y + (size_t)mat * ymat + (size_t)ksl * ykstride + (size_t)row0 * N;
-            T.count = __builtin_amdgcn_readfirstlane(__shfl(cnt, e));
-            T.m0 = mt * BM;
-            T.n0 = ntile * KQ_BN;
-            T.kb0 = ksl * nsb_k;
-            return T;
-        };
-        kq_grouped_stream<F, BM, NS, NW>(stages, decode, total, nsb_k, xrb, wrb, N, wave, l);
+        const KQExperts<BM> ex(wt, X, xrb, Y, N, nsb, tiles_n, offsets, ne, nmat, ymat, ks, ykstride, l);
+        kq_grouped_stream<F, BM, NS, NW>(stages, ex, ex.total, ex.nsb_k, xrb, wrb, N, wave, l);
     }
 }
 
