@@ -12,10 +12,11 @@
 //   Q4_K: s*q with s = 8*s1 + s0 (s1, s0 in [0, 7]): s1*q and s0*q are <= 105
 //         and come from one packed 16-bit multiply per four weights; the mins
 //         are a third pass against m_j broadcast over the sub-block.
-//   Q6_K: w' = s*(q - 32) in [-4064, 4096] = 128*h + l, l in [0, 127].
+//   Q6_K: w = s*(q - 32) in [-4064, 4096] = 256*h + l, h in [-16, 16] and l in
+//         [-128, 127]: the two bytes of w + 128, the low one less 128.
 // The integer results per super-block are exact; the f32 epilogue is
 //   Q4_K: y += dx * (d * (8*Ch + Cl) - dmin * Cm)
-//   Q6_K: y += dx * d * (128*Ch + Cl)
+//   Q6_K: y += dx * d * (256*Ch + Cl)
 //
 // Data movement: NS LDS stages, each one super-block of the tile, filled by
 // buffer->LDS direct loads NS-1 super-blocks ahead of the MFMAs with one
@@ -230,16 +231,17 @@ __device__ __forceinline__ uint4 lds16_sh(const uint8_t* p, uint32_t sh) {
                       __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh));
 }
 
-// four 6-bit quants q (bytes of q4) -> bytes of h and l with s*(q-32) = 128*h + l
+// Four 6-bit quants q (bytes of q4) -> bytes of h and l with s*(q-32) = 256*h + l.
+// Each 16-bit lane holds w' = s*(q-32) + 128 (off = 128 - 32 s; |w'| < 2^15, so
+// the packed multiply-add's low 16 bits are exact): h is its high byte (w' >> 8),
+// l its low byte less 128 (the byte with the top bit flipped, read as int8).
 __device__ __forceinline__ void q6_split4(uint32_t q4, uint32_t scv, uint32_t off, int& h, int& l) {
     const uint32_t a = mul_u16x2(__builtin_amdgcn_perm(0u, q4, 0x0c010c00u), scv);
     const uint32_t c = mul_u16x2(__builtin_amdgcn_perm(0u, q4, 0x0c030c02u), scv);
-    const s16x2 wa = __builtin_bit_cast(s16x2, a) + __builtin_bit_cast(s16x2, off);
-    const s16x2 wc = __builtin_bit_cast(s16x2, c) + __builtin_bit_cast(s16x2, off);
-    const s16x2 ha = wa >> (short)7, hc = wc >> (short)7;
-    const s16x2 la = wa & (short)127, lc = wc & (short)127;
-    h = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hc), __builtin_bit_cast(uint32_t, ha), 0x06040200u);
-    l = (int)__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, lc), __builtin_bit_cast(uint32_t, la), 0x06040200u);
+    const uint32_t wa = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, a) + __builtin_bit_cast(s16x2, off));
+    const uint32_t wc = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, c) + __builtin_bit_cast(s16x2, off));
+    h = (int)__builtin_amdgcn_perm(wc, wa, 0x07050301u);
+    l = (int)(__builtin_amdgcn_perm(wc, wa, 0x06040200u) ^ 0x80808080u);
 }
 
 template <int MT>
@@ -263,7 +265,7 @@ __device__ __forceinline__ void kq6_compute(const uint8_t* wrow, const uint8_t* 
                 const int qd = 2 * hi + odd, j = 4 * half + qd;
                 const int sc = (int)(int8_t)wrow[sh + 192 + 8 * half + g2 + 2 * qd];
                 const uint32_t scv = ((uint32_t)sc & 0xFFFFu) * 0x00010001u;
-                const uint32_t off = ((uint32_t)(-32 * sc) & 0xFFFFu) * 0x00010001u;
+                const uint32_t off = ((uint32_t)(128 - 32 * sc) & 0xFFFFu) * 0x00010001u;
                 const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w}, qhw[4] = {qh.x, qh.y, qh.z, qh.w};
                 int hv[4], lv[4];
                 #pragma unroll
@@ -288,7 +290,7 @@ __device__ __forceinline__ void kq6_compute(const uint8_t* wrow, const uint8_t* 
     for (int t = 0; t < MT; t++)
         #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int c = (ch[t][r] << 7) + cl[t][r];
+            const int c = (ch[t][r] << 8) + cl[t][r];
             acc[t][r] = __builtin_fmaf(dx[t][r], d * (float)c, acc[t][r]);
         }
 }
@@ -397,7 +399,7 @@ __device__ __forceinline__ void kq6_compute16(const uint8_t* st, int wave, int l
             const uint4 qh = lds16_sh(wrow + 128 + 32 * half + 16 * (g4 & 1), sh);
             const int sc = (int)(int8_t)wrow[sh + 192 + 8 * half + (g4 & 1) + 2 * qd];
             const uint32_t scv = ((uint32_t)sc & 0xFFFFu) * 0x00010001u;
-            const uint32_t off = ((uint32_t)(-32 * sc) & 0xFFFFu) * 0x00010001u;
+            const uint32_t off = ((uint32_t)(128 - 32 * sc) & 0xFFFFu) * 0x00010001u;
             const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w}, qhw[4] = {qh.x, qh.y, qh.z, qh.w};
             const int lsh = 4 * (t & 1), hsh = 2 * qd;
             int hv[4], lv[4];
@@ -412,7 +414,7 @@ __device__ __forceinline__ void kq6_compute16(const uint8_t* st, int wave, int l
         }
         #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int c = (ch[r] << 7) + cl[r];
+            const int c = (ch[r] << 8) + cl[r];
             acc[0][4 * cb + r] = __builtin_fmaf(dx[r], d * (float)c, acc[0][4 * cb + r]);
         }
     }
