@@ -306,6 +306,15 @@ size_t act_row_bytes(int act_type, int w_type, size_t k) {
     return row_bytes_of(act_type, k);
 }
 
+// Workspace bytes matmul_dev uses from offset 0: the dequantized weights of
+// the literal f32 matmul, or the rows quantized here followed by the
+// repacked rows of the 32-element-block GEMM.
+size_t matmul_scratch(int w_type, size_t n_rows, size_t k, int act_type, size_t m) {
+    if (act_type == BARQ_ACT_F32) return m > 1 ? n_rows * k * 4 : 0;
+    const size_t q = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(q8_partner(w_type), k), 256) : 0;
+    return q + (m >= 16 && barq::b32_supported(w_type, n_rows, k, m) ? barq::b32_workspace(m, k) : 0);
+}
+
 // Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).
 int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
                const void* x, size_t m, float* y) {
@@ -326,16 +335,22 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     }
     const int aq = q8_partner(w_type);
     const uint8_t* xq = static_cast<const uint8_t*>(x);
+    // workspace: the quantized rows (when quantized here), then the repacked
+    // rows of the 32-element-block GEMM
+    // the MFMA GEMMs copy weight rows with 4-byte buffer->LDS loads
+    const bool w4 = aligned(w, 4);
+    const bool b32 = m >= 16 && w4 && barq::b32_supported(w_type, n_rows, k, m);
+    const size_t qbytes = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(aq, k), 256) : 0;
+    if (const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m)) BARQ_CHECK(ensure_ws(h, need));
     if (act_type == BARQ_ACT_F32_Q8) {
         if (!aligned(x, 16)) return fail(BARQ_E_INVALID, "f32 activations must be 16-byte aligned");
-        const size_t qbytes = m * row_bytes_of(aq, k);
-        BARQ_CHECK(ensure_ws(h, qbytes));
         BARQ_CHECK(launched(quantize_act_dev(aq, static_cast<const float*>(x), m, k, h->ws, s), "quantize_act"));
         xq = static_cast<const uint8_t*>(h->ws);
     } else if (!aligned(x, aq == BARQ_TYPE_Q8_K ? 4 : 2)) {
         return fail(BARQ_E_INVALID, "activation blocks misaligned");
     }
-    if (m >= 16 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
+    if (b32) return launched(barq::b32_gemm_launch(w_type, w, n_rows, k, xq, m, at<uint8_t>(h, qbytes), y, s), "gemm_b32");
+    if (m >= 16 && w4 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
         return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, y, s), "gemm_mfma");
     const size_t xrb = row_bytes_of(aq, k);
     for (size_t r = 0; r < m; r++)
@@ -357,11 +372,8 @@ int matmul_any(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     const size_t wbytes = n_rows * row_bytes_of(w_type, k);
     const size_t xbytes = m * act_row_bytes(act_type, w_type, k);
     const size_t ybytes = m * n_rows * 4;
-    const size_t scratch = act_type == BARQ_ACT_F32 && m > 1 ? n_rows * k * 4
-                           : act_type == BARQ_ACT_F32_Q8        ? m * row_bytes_of(q8_partner(w_type), k)
-                                                                : 0;
     Arena a;
-    a.add(scratch);
+    a.add(matmul_scratch(w_type, n_rows, k, act_type, m));
     size_t ow = a.add(wbytes), ox = a.add(xbytes), oy = a.add(ybytes);
     BARQ_CHECK(ensure_ws(h, a.used));
     BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ow), w, wbytes, hipMemcpyHostToDevice, h->stream));

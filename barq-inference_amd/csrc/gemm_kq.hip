@@ -441,7 +441,6 @@ template <class F, int BM, int NW>
 __device__ __forceinline__ void kq_compute(const uint8_t* st, int b, int wave, int l,
                                            float (&acc)[KQL<F, BM, NW>::MTW][16]) {
     using L = KQL<F, BM, NW>;
-    constexpr int MT = L::MTW;
     if constexpr (BM == 16) {
         if constexpr (F::TYPE == TYPE_Q4_K) kq4_compute16(st, wave, l, acc);
         else kq6_compute16(st, wave, l, b, acc);
