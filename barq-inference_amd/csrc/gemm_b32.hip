@@ -28,16 +28,24 @@ namespace barq {
 
 // ---- activation repack ---------------------------------------------------------
 // Q8_0 block b of row r -> 32 int8 at xr[r * k + 32 b], f32 scale at dx[b * m + r].
+// A workgroup takes 16 rows x 16 blocks: thread t reads block t % 16 of row
+// t / 16 (each row's blocks contiguous), and the scales go out through LDS as
+// 16 runs of 16 consecutive rows.
 __global__ __launch_bounds__(256) void q8_0_repack_kernel(const uint8_t* __restrict__ xq, size_t m, size_t nblk,
                                                           int8_t* __restrict__ xr, float* __restrict__ dx) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= m * nblk) return;
-    const size_t r = i / nblk, b = i - r * nblk;
-    const uint8_t* blk = xq + i * Q8_0_BYTES;
-    dx[b * m + r] = f16_bits_to_f32(ld_u16(blk));
-    uint4* dst = reinterpret_cast<uint4*>(xr + r * nblk * 32 + 32 * b);
-    dst[0] = ld16_a2(blk + 2);
-    dst[1] = ld16_a2(blk + 18);
+    __shared__ float sd[16][17];
+    const int t = threadIdx.x;
+    const size_t r = (size_t)blockIdx.y * 16 + t / 16, b = (size_t)blockIdx.x * 16 + (t & 15);
+    if (r < m && b < nblk) {
+        const uint8_t* blk = xq + (r * nblk + b) * Q8_0_BYTES;
+        sd[t & 15][t / 16] = f16_bits_to_f32(ld_u16(blk));
+        uint4* dst = reinterpret_cast<uint4*>(xr + (r * nblk + b) * 32);
+        dst[0] = ld16_a2(blk + 2);
+        dst[1] = ld16_a2(blk + 18);
+    }
+    __syncthreads();
+    const size_t r2 = (size_t)blockIdx.y * 16 + (t & 15), b2 = (size_t)blockIdx.x * 16 + t / 16;
+    if (r2 < m && b2 < nblk) dx[b2 * m + r2] = sd[t / 16][t & 15];
 }
 
 // ---- formats -----------------------------------------------------------------
@@ -370,7 +378,7 @@ hipError_t b32_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, c
     const size_t nblk = k / 32;
     int8_t* xr = static_cast<int8_t*>(ws);
     float* dx = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + m * k);
-    hipLaunchKernelGGL(q8_0_repack_kernel, dim3((unsigned)((m * nblk + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(q8_0_repack_kernel, dim3((unsigned)((nblk + 15) / 16), (unsigned)((m + 15) / 16)), dim3(256), 0, s,
                        static_cast<const uint8_t*>(xq), m, nblk, xr, dx);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

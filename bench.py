@@ -44,6 +44,8 @@ def parse():
     # untimed launches before the timed ones: enough (< 1 s) for the GPU's clocks to settle
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--config", type=int, default=2, help="BASELINE.json config: 1-4 linear, 5 MoE")
+    p.add_argument("--w-type", default=None, choices=["Q4_0", "Q8_0", "Q4_0_BARQ", "Q4_K", "Q6_K"],
+                   help="configs 1-4: another weight format at the same shape (e.g. --config 4 --w-type Q4_0)")
     p.add_argument("--copies", type=int, default=0, help="distinct weight copies (default: >= 320 MB)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     p.add_argument("--no-cpu", action="store_true")
@@ -102,9 +104,15 @@ def time_launches(launch, K, eager):
 # dominant kernel of each config (config 5: every kernel of the MoE step)
 KERNEL_OF_CONFIG = {1: "gemv_dma_kernel<barq::DQ40", 2: "gemv_q8_kernel<barq::FmtQ4K",
                     3: "gemv_dma_kernel<barq::DQ6K", 4: "kq_kernel<barq::KQ4, 64", 5: "barq::"}
+# with --w-type: (GEMV, GEMM) kernel of each format
+KERNEL_OF_TYPE = {"Q4_0": ("gemv_dma_kernel<barq::DQ40", "b32_gemm_kernel<barq::B40,"),
+                  "Q8_0": ("gemv_dma_kernel<barq::DQ80", "b32_gemm_kernel<barq::B80,"),
+                  "Q4_0_BARQ": ("gemv_dma_kernel<barq::DQ40B", "b32_gemm_kernel<barq::B40Barq"),
+                  "Q4_K": ("gemv_q8_kernel<barq::FmtQ4K", "kq_kernel<barq::KQ4, 64"),
+                  "Q6_K": ("gemv_dma_kernel<barq::DQ6K", "kq_kernel<barq::KQ6")}
 
 
-def measure_traffic(config):
+def measure_traffic(config, w_type_name=None):
     """HBM bytes per launch of the config's dominant kernel: two rocprofv3
     child runs of this script (FETCH_SIZE, then WRITE_SIZE, in KiB per
     dispatch), each scaled by what the same counter reads for a 256 MiB
@@ -118,13 +126,17 @@ def measure_traffic(config):
     if not shutil.which("rocprofv3"):
         return None, "rocprofv3 not found"
     name = KERNEL_OF_CONFIG[config]
+    extra = []
+    if w_type_name:
+        name = KERNEL_OF_TYPE[w_type_name][1 if config == 4 else 0]
+        extra = ["--w-type", w_type_name]
     vals = {}
     tmp = tempfile.mkdtemp(prefix="barq_pmc_")
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         out = os.path.join(tmp, counter)
         cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "t", "--",
                sys.executable, os.path.abspath(__file__), "--config", str(config), "--steps", "10", "--warmup", "2",
-               "--no-cpu", "--no-traffic", "--probe-copy"]
+               "--no-cpu", "--no-traffic", "--probe-copy"] + extra
         try:
             r = subprocess.run(cmd, cwd=tmp, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, timeout=180)
         except subprocess.TimeoutExpired:
@@ -474,8 +486,16 @@ def main():
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]
     w_type, n, k, m = cfg["w_type"], cfg["n_rows"], cfg["k"], cfg["m"]
+    workload = cfg["name"]
     log(f"generating {cfg['name']}")
     t, w, x = synth.linear_inputs(args.config)
+    if args.w_type:
+        # the same shape and activation with weights of another format
+        w_type = getattr(B, args.w_type)
+        w = synth.gen_weights(w_type, n, k, synth.sub_seed(synth.config_seed(args.config), 10))
+        act_name = "Q8_K" if B.Q8_PARTNER[w_type] == B.Q8_K else "Q8_0"
+        workload = (f"C{args.config} shape with {args.w_type} weights: {n}x{k}, "
+                    + (f"batch 1, x->{act_name}" if m == 1 else f"M={m}, X->{act_name}"))
     at = B.Q8_PARTNER[w_type]
     wbytes = w.nbytes
     copies = args.copies or max(2, -(-320 * 2 ** 20 // wbytes))
@@ -526,8 +546,8 @@ def main():
     except Exception as e:
         log(f"parity check skipped: {e}")
 
-    fmt_name = {B.Q4_0: "Q4_0", B.Q8_0: "Q8_0", B.Q4_K: "Q4_K", B.Q6_K: "Q6_K"}.get(w_type, "quantized")
-    metric = METRIC if args.config == 2 else f"{fmt_name} GEMV achieved HBM GB/s (% of peak) + µs/call, 1 GPU"
+    fmt_name = {B.Q4_0: "Q4_0", B.Q8_0: "Q8_0", B.Q4_K: "Q4_K", B.Q6_K: "Q6_K", B.Q4_0_BARQ: "Q4_0_BARQ"}.get(w_type, "quantized")
+    metric = METRIC if args.config == 2 and not args.w_type else f"{fmt_name} GEMV achieved HBM GB/s (% of peak) + µs/call, 1 GPU"
     result = {
         "metric": metric,
         "value": round(gbs, 2),
@@ -541,7 +561,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": cfg["name"], "n_rows": n, "k": k, "batch": m, "weight_copies": copies,
+        "config": {"workload": workload, "n_rows": n, "k": k, "batch": m, "weight_copies": copies,
                    "weight_bytes_per_copy": wbytes, "timing": method},
         "us_per_call": round(us, 3),
         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
@@ -556,7 +576,7 @@ def main():
         # the batched path is bound by int8 MFMA: 2*M*N*K ops per launch
         ops = 2.0 * m * n * k
         tops = ops / (ms * 1e-3) / 1e12
-        result["metric"] = "Q4_K batched GEMM int8 TOP/s (% of dense int8 MFMA peak), 1 GPU"
+        result["metric"] = f"{fmt_name} batched GEMM int8 TOP/s (% of dense int8 MFMA peak), 1 GPU"
         result["value"] = round(tops, 2)
         result["unit"] = "TOP/s"
         result["roofline"] = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
@@ -572,7 +592,7 @@ def main():
         log("copy probe: 5 x 256 MiB device copies")
     if not args.no_traffic:
         log("measuring HBM traffic per launch (rocprofv3 --pmc child runs)")
-        traffic, detail = measure_traffic(args.config)
+        traffic, detail = measure_traffic(args.config, args.w_type)
         result["roofline"]["traffic"] = round(traffic) if traffic else None
         result["roofline"]["traffic_detail"] = detail
     if not args.no_cpu:
