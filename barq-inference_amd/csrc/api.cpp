@@ -312,7 +312,7 @@ size_t act_row_bytes(int act_type, int w_type, size_t k) {
 size_t matmul_scratch(int w_type, size_t n_rows, size_t k, int act_type, size_t m) {
     if (act_type == BARQ_ACT_F32) return m > 1 ? n_rows * k * 4 : 0;
     const size_t q = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(q8_partner(w_type), k), 256) : 0;
-    return q + (m >= 16 && barq::b32_supported(w_type, n_rows, k, m) ? barq::b32_workspace(m, k) : 0);
+    return q + (m >= 16 && barq::b32_supported(w_type, n_rows, k, m) ? barq::b32_workspace(m, n_rows, k) : 0);
 }
 
 // Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).

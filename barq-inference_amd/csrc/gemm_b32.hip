@@ -230,12 +230,14 @@ __device__ __forceinline__ void b32_compute(const uint8_t* st, int s, int wave, 
 // ... from its own part of each LDS stage (one barrier per KG steps), and the
 // groups' partial sums are added through LDS at the end.  More waves per tile
 // for the same LDS: small M has few tiles, and each tile's steps then run in
-// parallel.
+// parallel.  With KS > 1 K slices the grid has KS workgroups per tile, slice
+// i taking steps [i, i + 1) * steps / KS and writing its partial product to
+// Y + i * M * N (b32_reduce_kernel adds the slices in order).
 template <class F, int BM, int NS, int KG>
 __global__ __launch_bounds__(256 * KG, 1)
 void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* __restrict__ X,
                      const float* __restrict__ DXT, float* __restrict__ Y, int M, int N, int K, int tiles_m,
-                     int xcd_order) {
+                     int ks, int xcd_order) {
     using L = B32L<F, BM>;
     constexpr int MT = L::MT, SB = KG * L::STAGE;
     static_assert(NS >= 2 && NS <= 4, "stage count");
@@ -250,7 +252,8 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
     const int kg = wave_all >> 2, wave = wave_all & 3;
     // workgroup i runs on XCD i % 8: each XCD takes a contiguous run of tiles
     const int n_tiles = tiles_m * ((N + B32_BN - 1) / B32_BN);
-    int tile = blockIdx.x;
+    const int slice = blockIdx.x / n_tiles;
+    int tile = blockIdx.x - slice * n_tiles;
     if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
     const int mt = tile % tiles_m, nt = tile / tiles_m;
     const int m0 = mt * BM, n0 = nt * B32_BN;
@@ -260,7 +263,8 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
     const i32x4v dr = make_rsrc4(DXT + m0, (uint32_t)(((size_t)(K / 32) * M - m0) * 4));
     B32Off<F, BM> off;
     b32_offsets<F, BM>(off, k, wrb, m, wave, l);
-    const int nst = K / (32 * B32_SB * KG);   // steps per group (the host checks divisibility)
+    const int nst = K / (32 * B32_SB * KG * ks);   // steps per group (the host checks divisibility)
+    const int s0 = slice * nst * KG;                // this slice's first step
     const int sub = kg * L::STAGE;
 
     float acc[MT][16];
@@ -271,7 +275,7 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
 
     #pragma unroll
     for (int s = 0; s < NS - 1; s++)
-        if (s < nst) b32_issue<F, BM>(stage(s) + sub, xr, wr, dr, off, KG * s + kg, m, wave);
+        if (s < nst) b32_issue<F, BM>(stage(s) + sub, xr, wr, dr, off, s0 + KG * s + kg, m, wave);
     for (int s = 0; s < nst; s++) {
         // this thread's loads of step s are done once at most the later
         // steps' loads are outstanding; every thread's after the barrier
@@ -286,8 +290,8 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (s + NS - 1 < nst)
-            b32_issue<F, BM>(stage((s + NS - 1) % NS) + sub, xr, wr, dr, off, KG * (s + NS - 1) + kg, m, wave);
-        b32_compute<F, BM>(stage(s % NS) + sub, KG * s + kg, wave, l, acc);
+            b32_issue<F, BM>(stage((s + NS - 1) % NS) + sub, xr, wr, dr, off, s0 + KG * (s + NS - 1) + kg, m, wave);
+        b32_compute<F, BM>(stage(s % NS) + sub, s0 + KG * s + kg, wave, l, acc);
     }
 
     if constexpr (KG > 1) {
@@ -315,6 +319,7 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
         }
         if (kg > 0) return;
     }
+    float* const out = Y + (size_t)slice * M * N;
     const int col = n0 + 32 * wave + (l & 31), g2 = l >> 5;
     if (col < N) {
         #pragma unroll
@@ -322,47 +327,81 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
             #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (row < M) Y[(size_t)row * N + col] = acc[t][r];
+                if (row < M) out[(size_t)row * N + col] = acc[t][r];
             }
     }
+}
+
+// Y[i] = sum over the ks slices of P[slice * n + i], in slice order
+__global__ __launch_bounds__(256) void b32_reduce_kernel(const float* __restrict__ P, int ks, size_t n,
+                                                         float* __restrict__ Y) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float a = P[i];
+    for (int sl = 1; sl < ks; sl++) a += P[(size_t)sl * n + i];
+    Y[i] = a;
 }
 
 // ---- launch ------------------------------------------------------------------
 
 template <class F, int BM, int NS, int KG>
 static hipError_t b32_launch_t(const void* W, size_t n_rows, size_t k, const int8_t* xr, const float* dx, size_t m,
-                               float* y, hipStream_t s) {
+                               float* y, int ks, hipStream_t s) {
     const int tiles_m = (int)((m + BM - 1) / BM), tiles_n = (int)((n_rows + B32_BN - 1) / B32_BN);
     const uint32_t wrb = (uint32_t)(k / 32 * F::BB);
-    if ((k / (32 * B32_SB)) % KG != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((b32_gemm_kernel<F, BM, NS, KG>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256 * KG), 0, s,
-                       static_cast<const uint8_t*>(W), wrb, xr, dx, y, (int)m, (int)n_rows, (int)k, tiles_m,
+    if ((k / (32 * B32_SB)) % (KG * ks) != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((b32_gemm_kernel<F, BM, NS, KG>), dim3((unsigned)(tiles_m * tiles_n * ks)), dim3(256 * KG), 0, s,
+                       static_cast<const uint8_t*>(W), wrb, xr, dx, y, (int)m, (int)n_rows, (int)k, tiles_m, ks,
                        tuning_env("BARQ_GEMM_XCD", 1));
     return hipGetLastError();
 }
 
+static int b32_bm(size_t m) {
+    const int bm = tuning_env("BARQ_GEMM_BM", m > 32 ? 64 : 32);
+    return bm == 32 ? 32 : 64;
+}
+
+// K slices across workgroups when the tiles alone would leave most CUs idle:
+// doubled while the grid stays within 256 workgroups and every slice keeps
+// an even number of steps.  BARQ_GEMM_KS overrides.
+static int b32_k_slices(size_t m, size_t n_rows, size_t k) {
+    const int bm = b32_bm(m);
+    const size_t tiles = (m + bm - 1) / bm * ((n_rows + B32_BN - 1) / B32_BN), steps = k / (32 * B32_SB);
+    int ks = 1;
+    while (ks < 16 && tiles * ks * 2 <= 256 && steps % (size_t)(ks * 4) == 0) ks *= 2;
+    const int ovr = tuning_env("BARQ_GEMM_KS");
+    if (ovr > 0 && (ovr & (ovr - 1)) == 0 && ovr <= 16 && steps % (size_t)(2 * ovr) == 0) ks = ovr;
+    return ks;
+}
+
 // Tile rows and K-groups: 64-row tiles above 32 rows; four K-groups when
-// there are fewer tiles than CUs (and the step count allows), else two.
-// BARQ_GEMM_BM (32, 64) and BARQ_GEMM_KG (1, 2, 4) override.
+// there are fewer tiles than CUs and the step count allows, else two (two
+// with K slices).  BARQ_GEMM_BM (32, 64) and BARQ_GEMM_KG (1, 2, 4) override.
 template <class F>
 static hipError_t b32_dispatch(const void* W, size_t n_rows, size_t k, const int8_t* xr, const float* dx, size_t m,
-                               float* y, hipStream_t s) {
-    const int bm = tuning_env("BARQ_GEMM_BM", m > 32 ? 64 : 32);
+                               float* y, int ks, hipStream_t s) {
+    const int bm = b32_bm(m);
     const size_t tiles = (m + bm - 1) / bm * ((n_rows + B32_BN - 1) / B32_BN);
-    const size_t steps = k / (32 * B32_SB);
-    int kg = tuning_env("BARQ_GEMM_KG", tiles < 256 && steps % 4 == 0 ? 4 : 2);
+    const size_t steps = k / (32 * B32_SB) / ks;   // per slice
+    int kg = tuning_env("BARQ_GEMM_KG", ks == 1 && tiles < 256 && steps % 4 == 0 ? 4 : 2);
     if (kg != 1 && kg != 2 && kg != 4) kg = 2;
     if (kg > F::KG_MAX) kg = F::KG_MAX;   // LDS: Q8_0 weight rows are twice as long
     if (steps % kg != 0) kg = steps % 2 == 0 ? 2 : 1;
 #define B32_CASE(BMV, KGV) \
     if constexpr (KGV <= F::KG_MAX) \
-        if (bm == BMV && kg == KGV) return b32_launch_t<F, BMV, (KGV == 4 ? 2 : F::NS), KGV>(W, n_rows, k, xr, dx, m, y, s);
+        if (bm == BMV && kg == KGV) return b32_launch_t<F, BMV, (KGV == 4 ? 2 : F::NS), KGV>(W, n_rows, k, xr, dx, m, y, ks, s);
     B32_CASE(32, 1) B32_CASE(32, 2) B32_CASE(32, 4) B32_CASE(64, 1) B32_CASE(64, 2) B32_CASE(64, 4)
 #undef B32_CASE
-    return b32_launch_t<F, 64, F::NS, 2>(W, n_rows, k, xr, dx, m, y, s);
+    return b32_launch_t<F, 64, F::NS, 2>(W, n_rows, k, xr, dx, m, y, ks, s);
 }
 
-size_t b32_workspace(size_t m, size_t k) { return m * k + m * (k / 32) * 4; }
+// int8 rows, the scale table, then (with K slices) the partial products
+static size_t b32_parts_offset(size_t m, size_t k) { return (m * k + m * (k / 32) * 4 + 255) / 256 * 256; }
+
+size_t b32_workspace(size_t m, size_t n_rows, size_t k) {
+    const int ks = b32_k_slices(m, n_rows, k);
+    return b32_parts_offset(m, k) + (ks > 1 ? (size_t)ks * m * n_rows * 4 : 0);
+}
 
 bool b32_supported(int w_type, size_t n_rows, size_t k, size_t m) {
     if (w_type != TYPE_Q4_0 && w_type != TYPE_Q8_0 && w_type != TYPE_Q4_0_BARQ) return false;
@@ -382,11 +421,17 @@ hipError_t b32_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, c
                        static_cast<const uint8_t*>(xq), m, nblk, xr, dx);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const int ks = b32_k_slices(m, n_rows, k);
+    float* parts = ks > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + b32_parts_offset(m, k)) : y;
     switch (w_type) {
-    case TYPE_Q4_0: return b32_dispatch<B40>(W, n_rows, k, xr, dx, m, y, s);
-    case TYPE_Q8_0: return b32_dispatch<B80>(W, n_rows, k, xr, dx, m, y, s);
-    default: return b32_dispatch<B40Barq>(W, n_rows, k, xr, dx, m, y, s);
+    case TYPE_Q4_0: e = b32_dispatch<B40>(W, n_rows, k, xr, dx, m, parts, ks, s); break;
+    case TYPE_Q8_0: e = b32_dispatch<B80>(W, n_rows, k, xr, dx, m, parts, ks, s); break;
+    default: e = b32_dispatch<B40Barq>(W, n_rows, k, xr, dx, m, parts, ks, s); break;
     }
+    if (e != hipSuccess || ks == 1) return e;
+    const size_t n = m * n_rows;
+    hipLaunchKernelGGL(b32_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, parts, ks, n, y);
+    return hipGetLastError();
 }
 
 }  // namespace barq

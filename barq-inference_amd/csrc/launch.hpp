@@ -50,10 +50,11 @@ hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t
 bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m);
 
 // gemm_b32.hip: Y[m x n] = X W^T for Q4_0, Q8_0 and Q4_0_BARQ weights against
-// Q8_0 rows xq (k % 256 == 0); ws holds b32_workspace(m, k) bytes (the
-// activation repacked into int8 rows and an f32 scale table)
+// Q8_0 rows xq (k % 256 == 0); ws holds b32_workspace(m, n_rows, k) bytes
+// (the activation repacked into int8 rows, an f32 scale table and, when few
+// tiles split K across workgroups, the slices' partial products)
 bool b32_supported(int w_type, size_t n_rows, size_t k, size_t m);
-size_t b32_workspace(size_t m, size_t k);
+size_t b32_workspace(size_t m, size_t n_rows, size_t k);
 hipError_t b32_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, void* ws,
                            float* y, hipStream_t s);
 

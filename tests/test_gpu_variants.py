@@ -58,15 +58,19 @@ GEMM_VARIANTS = [
 @pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_gemm_32_element_blocks(be, orc, name):
     """Batched GEMM for the 32-element block formats (int8 MFMA, one block per
-    MFMA): ragged tiles in M and N, 32- and 64-row tiles, the host-buffer path,
-    and k not a multiple of 256 (per-row GEMV fallback)."""
+    MFMA): ragged tiles in M and N, 32- and 64-row tiles, K split across
+    workgroups (the default for few tiles, and each override), the
+    host-buffer path, and k not a multiple of 256 (per-row GEMV fallback)."""
     import torch
     t = getattr(B, name)
     at = B.Q8_PARTNER[t]
     for n, k, m, env_v in [(300, 512, 16, {}), (128, 1024, 40, {}), (257, 768, 97, {}), (64, 256, 33, dict(BARQ_GEMM_BM=32)),
                            (200, 512, 70, dict(BARQ_GEMM_BM=64)), (130, 512, 18, dict(BARQ_GEMM_XCD=0)), (96, 288, 20, {}),
                            (160, 1024, 50, dict(BARQ_GEMM_KG=1)), (160, 1024, 50, dict(BARQ_GEMM_KG=2)),
-                           (160, 1024, 50, dict(BARQ_GEMM_KG=4)), (160, 768, 20, dict(BARQ_GEMM_KG=4, BARQ_GEMM_BM=32))]:
+                           (160, 1024, 50, dict(BARQ_GEMM_KG=4)), (160, 768, 20, dict(BARQ_GEMM_KG=4, BARQ_GEMM_BM=32)),
+                           (257, 2048, 17, {}), (160, 1024, 50, dict(BARQ_GEMM_KS=1)), (160, 1024, 50, dict(BARQ_GEMM_KS=4)),
+                           (160, 1024, 50, dict(BARQ_GEMM_KS=2, BARQ_GEMM_KG=4)), (131, 1024, 19, dict(BARQ_GEMM_KS=4, BARQ_GEMM_KG=1)),
+                           (1100, 512, 33, dict(BARQ_GEMM_KS=2))]:
         w = synth.gen_weights(t, n, k, 900 + n + k)
         x = synth.gen_f32(m * k, 901 + m).reshape(m, k)
         xq = orc.quantize_act(at, x)
