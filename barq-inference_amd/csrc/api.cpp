@@ -308,17 +308,25 @@ size_t act_row_bytes(int act_type, int w_type, size_t k) {
 
 // Workspace bytes matmul_dev uses from offset 0: the dequantized weights of
 // the literal f32 matmul, or the rows quantized here followed by the
-// repacked rows of the 32-element-block GEMM.
+// repacked rows of the 32-element-block GEMM or the K slices' partial
+// products of either MFMA GEMM.
 size_t matmul_scratch(int w_type, size_t n_rows, size_t k, int act_type, size_t m) {
     if (act_type == BARQ_ACT_F32) return m > 1 ? n_rows * k * 4 : 0;
     const size_t q = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(q8_partner(w_type), k), 256) : 0;
-    return q + (m >= 16 && barq::b32_supported(w_type, n_rows, k, m) ? barq::b32_workspace(m, n_rows, k) : 0);
+    if (m < 16) return q;
+    if (barq::b32_supported(w_type, n_rows, k, m)) return q + barq::b32_workspace(m, n_rows, k);
+    if (barq::gemm_mfma_supported(w_type, n_rows, k, m)) return q + barq::gemm_mfma_workspace(w_type, n_rows, k, m);
+    return q;
 }
 
-// Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).
+// Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).  With
+// use_ws false the call leaves the workspace alone (its caller keeps data
+// there): Q8 activations only, no 32-element-block GEMM, no K slices.
 int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
-               const void* x, size_t m, float* y) {
+               const void* x, size_t m, float* y, bool use_ws = true) {
     hipStream_t s = h->stream;
+    if (!use_ws && (act_type == BARQ_ACT_F32 || act_type == BARQ_ACT_F32_Q8))
+        return fail(BARQ_E_INVALID, "matmul without workspace takes quantized activations");
     if (!aligned(w, weight_align(w_type))) return fail(BARQ_E_INVALID, "weights must be %zu-byte aligned", weight_align(w_type));
     if (!aligned(y, 4)) return fail(BARQ_E_INVALID, "output must be 4-byte aligned");
     if (act_type == BARQ_ACT_F32) {
@@ -339,9 +347,10 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     // rows of the 32-element-block GEMM
     // the MFMA GEMMs copy weight rows with 4-byte buffer->LDS loads
     const bool w4 = aligned(w, 4);
-    const bool b32 = m >= 16 && w4 && barq::b32_supported(w_type, n_rows, k, m);
+    const bool b32 = use_ws && m >= 16 && w4 && barq::b32_supported(w_type, n_rows, k, m);
     const size_t qbytes = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(aq, k), 256) : 0;
-    if (const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m)) BARQ_CHECK(ensure_ws(h, need));
+    if (use_ws)
+        if (const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m)) BARQ_CHECK(ensure_ws(h, need));
     if (act_type == BARQ_ACT_F32_Q8) {
         if (!aligned(x, 16)) return fail(BARQ_E_INVALID, "f32 activations must be 16-byte aligned");
         BARQ_CHECK(launched(quantize_act_dev(aq, static_cast<const float*>(x), m, k, h->ws, s), "quantize_act"));
@@ -351,7 +360,8 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     }
     if (b32) return launched(barq::b32_gemm_launch(w_type, w, n_rows, k, xq, m, at<uint8_t>(h, qbytes), y, s), "gemm_b32");
     if (m >= 16 && w4 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
-        return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, y, s), "gemm_mfma");
+        return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, use_ws ? at<uint8_t>(h, qbytes) : nullptr,
+                                                   y, s), "gemm_mfma");
     const size_t xrb = row_bytes_of(aq, k);
     for (size_t r = 0; r < m; r++)
         BARQ_CHECK(launched(barq::gemv_q8_launch(w_type, w, n_rows, k, xq + r * xrb, y + r * n_rows, s), "gemv_q8"));
@@ -683,8 +693,9 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
         const size_t r0 = (size_t)off[e], c = (size_t)off[e + 1] - r0;
         if (!c) continue;
         if (q8) {
-            BARQ_CHECK(matmul_dev(h, gt, gate[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, gb + r0 * n_ff));
-            BARQ_CHECK(matmul_dev(h, ut, up[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, ub + r0 * n_ff));
+            // the arena holds this call's data from offset `base`: no workspace
+            BARQ_CHECK(matmul_dev(h, gt, gate[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, gb + r0 * n_ff, false));
+            BARQ_CHECK(matmul_dev(h, ut, up[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, ub + r0 * n_ff, false));
         } else {
             float* wf = at<float>(h, o_wf);
             BARQ_CHECK(launched(barq::dequant_launch(gt, gate[e], n_ff * hidden, wf, s), "dequantize"));
@@ -701,7 +712,7 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
         const size_t r0 = (size_t)off[e], c = (size_t)off[e + 1] - r0;
         if (!c) continue;
         if (q8) {
-            BARQ_CHECK(matmul_dev(h, dt, down[e], hidden, n_ff, in_act, hin + r0 * hq_row, c, yg + r0 * hidden));
+            BARQ_CHECK(matmul_dev(h, dt, down[e], hidden, n_ff, in_act, hin + r0 * hq_row, c, yg + r0 * hidden, false));
         } else {
             float* wf = at<float>(h, o_wf);
             BARQ_CHECK(launched(barq::dequant_launch(dt, down[e], hidden * n_ff, wf, s), "dequantize"));

@@ -232,7 +232,7 @@ __device__ __forceinline__ void b32_compute(const uint8_t* st, int s, int wave, 
 // for the same LDS: small M has few tiles, and each tile's steps then run in
 // parallel.  With KS > 1 K slices the grid has KS workgroups per tile, slice
 // i taking steps [i, i + 1) * steps / KS and writing its partial product to
-// Y + i * M * N (b32_reduce_kernel adds the slices in order).
+// Y + i * M * N (slice_sum_kernel adds the slices in order).
 template <class F, int BM, int NS, int KG>
 __global__ __launch_bounds__(256 * KG, 1)
 void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* __restrict__ X,
@@ -333,8 +333,8 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
 }
 
 // Y[i] = sum over the ks slices of P[slice * n + i], in slice order
-__global__ __launch_bounds__(256) void b32_reduce_kernel(const float* __restrict__ P, int ks, size_t n,
-                                                         float* __restrict__ Y) {
+__global__ __launch_bounds__(256) void slice_sum_kernel(const float* __restrict__ P, int ks, size_t n,
+                                                        float* __restrict__ Y) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     float a = P[i];
@@ -429,8 +429,12 @@ hipError_t b32_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, c
     default: e = b32_dispatch<B40Barq>(W, n_rows, k, xr, dx, m, parts, ks, s); break;
     }
     if (e != hipSuccess || ks == 1) return e;
-    const size_t n = m * n_rows;
-    hipLaunchKernelGGL(b32_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, parts, ks, n, y);
+    return slice_sum_launch(parts, ks, m * n_rows, y, s);
+}
+
+hipError_t slice_sum_launch(const float* parts, int ks, size_t n, float* y, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(slice_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, parts, ks, n, y);
     return hipGetLastError();
 }
 

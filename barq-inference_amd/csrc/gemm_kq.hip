@@ -765,11 +765,15 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
     if constexpr (!GROUPED) {
         // workgroup i runs on XCD i % 8: give each XCD a contiguous run of
         // tiles so neighbouring weight tiles share its L2
+        // with ks K slices, slice i of a tile takes super-blocks
+        // [i, i + 1) * nsb / ks and writes its partial product to Y + i M N
         const int n_tiles = tiles_m * tiles_n;
-        int tile = blockIdx.x;
+        const int slice = blockIdx.x / n_tiles, nsb_k = nsb / ks;
+        int tile = blockIdx.x - slice * n_tiles;
         if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
         const int mt = tile % tiles_m, ntile = tile / tiles_m;
-        kq_tile<F, BM, NS, NW, KG>(stages, wt.w[0], wrb, X, xrb, Y, M, N, nsb, mt * BM, ntile * KQ_BN, kg, wave, l);
+        kq_tile<F, BM, NS, NW, KG>(stages, wt.w[0], wrb, X, xrb, Y + (size_t)slice * M * N, M, N, nsb_k, mt * BM,
+                                   ntile * KQ_BN, kg, wave, l, slice * nsb_k);
     } else {
         const KQExperts<BM> ex(wt, X, xrb, Y, N, nsb, tiles_n, offsets, ne, nmat, ymat, ks, ykstride, l);
         kq_grouped_stream<F, BM, NS, NW>(stages, ex, ex.total, ex.nsb_k, xrb, wrb, N, wave, l);
@@ -800,7 +804,7 @@ struct KQArgs {
     int ne, nmat;        // grouped: experts per weight set, weight sets
     size_t total_rows;   // grouped: rows over all experts
     size_t ymat;
-    int ks;              // grouped: K slices, each writing its partial product
+    int ks;              // K slices, each writing its partial product
     size_t ykstride;
 };
 
@@ -808,7 +812,7 @@ template <class F, int BM, int NS, int NW, bool GROUPED, int KG = 1>
 static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     const int tiles_n = (a.N + KQ_BN - 1) / KQ_BN;
     int tiles_m = (a.M + BM - 1) / BM;
-    unsigned grid = (unsigned)(tiles_m * tiles_n);
+    unsigned grid = (unsigned)(tiles_m * tiles_n * a.ks);
     if constexpr (GROUPED) {
         // m-tiles over all experts: sum of ceil(c_e / BM) <= (total + ne (BM - 1)) / BM
         const size_t slots = (a.total_rows + (size_t)a.ne * (BM - 1)) / BM;
@@ -818,7 +822,9 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
         grid = (unsigned)(tiles < cap ? tiles : cap);
         tiles_m = 0;
     }
-    if (a.nsb % KG != 0) return hipErrorInvalidValue;
+    // ungrouped K slices: whole K-group steps, even first super-blocks
+    if (!GROUPED && (a.nsb % a.ks != 0 || (a.ks > 1 && (a.nsb / a.ks) % 2 != 0))) return hipErrorInvalidValue;
+    if ((GROUPED ? a.nsb : a.nsb / a.ks) % KG != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, KG, GROUPED>), dim3(grid), dim3(64 * NW * KG), 0, s, a.wt, a.wrb, a.X, a.xrb,
                        a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, a.ks, a.ykstride,
                        tuning_env("BARQ_GEMM_XCD", 1));   // XCD-aware tile order (ungrouped)
@@ -828,7 +834,7 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
 // Overrides: BARQ_GEMM_BM (16, 32, 64, or 65 = 64 rows with eight waves of
 // 32 x 32 per K-group),
 // BARQ_GEMM_NS (stages), BARQ_GEMM_KG (K-groups, ungrouped), BARQ_GEMM_KS
-// (K slices of the MoE down projection).
+// (K slices: the MoE down projection, and ungrouped launches).
 
 // rows: M (ungrouped) or the expected rows per expert (grouped).  Stage
 // counts are the most that fit the 160 KiB of LDS (deeper pipelines keep
@@ -854,7 +860,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
         // two K-groups of waves share a tile's pipeline (twice the waves per
         // SIMD for the same LDS) when the super-block count is even
         const int kg = tuning_env("BARQ_GEMM_KG", 2);
-        if (kg == 2 && a.nsb % 2 == 0) {
+        if (kg == 2 && (a.nsb / a.ks) % 2 == 0) {
             if constexpr (F::TYPE == TYPE_Q4_K) {
                 if (bm == 65) return kq_launch_t<F, 64, 2, 8, GROUPED, 2>(a, s);
                 if (bm == 64) return kq_launch_t<F, 64, 2, 4, GROUPED, 2>(a, s);
@@ -904,14 +910,47 @@ static KQArgs kq_args(int w_type, size_t n_rows, size_t k, const void* xq, float
     return a;
 }
 
-hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
-                          hipStream_t s) {
+// K slices of an ungrouped launch when the tiles alone would leave most CUs
+// idle: doubled while the grid stays within 256 workgroups and every slice
+// keeps an even number of super-blocks (two K-groups; Q6_K windows keep
+// their parity).  BARQ_GEMM_KS overrides (a power of two up to 16).
+// The tile height kq_dispatch picks (for an even super-block count per slice).
+static size_t kq_tile_rows(int w_type, size_t m) {
+    const int bm_env = tuning_env("BARQ_GEMM_BM");
+    const int bm = bm_env ? bm_env : (m > 32 ? 64 : 32);
+    if (bm == 16) return 16;
+    if (tuning_env("BARQ_GEMM_KG", 2) == 2) return w_type == TYPE_Q4_K && (bm == 64 || bm == 65) ? 64 : 32;
+    return bm >= 64 ? 64 : 32;
+}
+
+int kq_k_slices(int w_type, size_t m, size_t n_rows, size_t k) {
+    const size_t bm = kq_tile_rows(w_type, m);
+    const size_t tiles = (m + bm - 1) / bm * ((n_rows + KQ_BN - 1) / KQ_BN), nsb = k / 256;
+    int ks = 1;
+    while (ks < 16 && tiles * ks * 2 <= 256 && nsb % (size_t)(ks * 4) == 0) ks *= 2;
+    const int ovr = tuning_env("BARQ_GEMM_KS");
+    if (ovr > 0 && (ovr & (ovr - 1)) == 0 && ovr <= 16 && nsb % (size_t)(2 * ovr) == 0) ks = ovr;
+    return ks;
+}
+
+size_t kq_workspace(int w_type, size_t m, size_t n_rows, size_t k) {
+    const int ks = kq_k_slices(w_type, m, n_rows, k);
+    return ks > 1 ? (size_t)ks * m * n_rows * 4 : 0;
+}
+
+hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, void* ws,
+                          float* y, hipStream_t s) {
     if (m == 0 || n_rows == 0) return hipSuccess;
     if (!kq_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
-    KQArgs a = kq_args(w_type, n_rows, k, xq, y);
+    const int ks = ws ? kq_k_slices(w_type, m, n_rows, k) : 1;   // no workspace: one slice
+    float* parts = ks > 1 ? static_cast<float*>(ws) : y;
+    KQArgs a = kq_args(w_type, n_rows, k, xq, parts);
     a.wt.w[0] = static_cast<const uint8_t*>(W);
     a.M = (int)m;
-    return w_type == TYPE_Q4_K ? kq_dispatch<KQ4, false>(a, m, s) : kq_dispatch<KQ6, false>(a, m, s);
+    a.ks = ks;
+    hipError_t e = w_type == TYPE_Q4_K ? kq_dispatch<KQ4, false>(a, m, s) : kq_dispatch<KQ6, false>(a, m, s);
+    if (e != hipSuccess || ks == 1) return e;
+    return slice_sum_launch(parts, ks, m * n_rows, y, s);
 }
 
 hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,

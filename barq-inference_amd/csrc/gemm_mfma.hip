@@ -449,12 +449,19 @@ bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m) {
     return wbytes < (1ull << 31) && xbytes < (1ull << 31);
 }
 
+static bool use_kq(int w_type, size_t n_rows, size_t k, size_t m) {
+    return tuning_env("BARQ_GEMM_IMPL", 2) != 0 && kq_supported(w_type, n_rows, k, m);
+}
+
+size_t gemm_mfma_workspace(int w_type, size_t n_rows, size_t k, size_t m) {
+    return use_kq(w_type, n_rows, k, m) ? kq_workspace(w_type, m, n_rows, k) : 0;
+}
+
 hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,
-                                float* y, hipStream_t s) {
+                                void* ws, float* y, hipStream_t s) {
     if (m == 0 || n_rows == 0) return hipSuccess;
     if (!gemm_mfma_supported(w_type, n_rows, k, m)) return hipErrorInvalidValue;
-    if (tuning_env("BARQ_GEMM_IMPL", 2) != 0 && kq_supported(w_type, n_rows, k, m))
-        return kq_gemm_launch(w_type, W, n_rows, k, xq, m, y, s);
+    if (use_kq(w_type, n_rows, k, m)) return kq_gemm_launch(w_type, W, n_rows, k, xq, m, ws, y, s);
     switch (w_type) {
     case TYPE_Q4_K: return dispatch_kq<GQ4K>(W, n_rows, k, xq, m, y, s);
     case TYPE_Q6_K: return dispatch_kq<GQ6K>(W, n_rows, k, xq, m, y, s);

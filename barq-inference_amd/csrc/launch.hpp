@@ -44,10 +44,12 @@ bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, cons
 hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, float* y,
                            hipStream_t s);
 
-// gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows)
+// gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows); ws holds
+// gemm_mfma_workspace(...) bytes (K slices' partial products, often none)
 hipError_t gemm_q8k_mfma_launch(int w_type, const void* W, size_t n_rows, size_t k,
-                                const void* xq, size_t m, float* y, hipStream_t s);
+                                const void* xq, size_t m, void* ws, float* y, hipStream_t s);
 bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m);
+size_t gemm_mfma_workspace(int w_type, size_t n_rows, size_t k, size_t m);
 
 // gemm_b32.hip: Y[m x n] = X W^T for Q4_0, Q8_0 and Q4_0_BARQ weights against
 // Q8_0 rows xq (k % 256 == 0); ws holds b32_workspace(m, n_rows, k) bytes
@@ -55,14 +57,20 @@ bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m);
 // tiles split K across workgroups, the slices' partial products)
 bool b32_supported(int w_type, size_t n_rows, size_t k, size_t m);
 size_t b32_workspace(size_t m, size_t n_rows, size_t k);
+// y[i] = sum over ks slices of parts[slice * n + i], in slice order
+hipError_t slice_sum_launch(const float* parts, int ks, size_t n, float* y, hipStream_t s);
 hipError_t b32_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, void* ws,
                            float* y, hipStream_t s);
 
 // gemm_kq.hip: the same product with 32x32x32 int8 MFMA tiles fed by
 // buffer->LDS loads; Q4_K any k % 256 == 0, Q6_K an even number of super-blocks.
 bool kq_supported(int w_type, size_t n_rows, size_t k, size_t m);
-hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, float* y,
-                          hipStream_t s);
+// ws holds kq_workspace(w_type, m, n_rows, k) bytes: with few tiles K is split across
+// workgroups, whose partial products slice_sum_launch adds (ws null: one slice)
+hipError_t kq_gemm_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m, void* ws,
+                          float* y, hipStream_t s);
+int kq_k_slices(int w_type, size_t m, size_t n_rows, size_t k);
+size_t kq_workspace(int w_type, size_t m, size_t n_rows, size_t k);
 // Expert-grouped form: rows [offsets[e], offsets[e+1]) of xq, and of
 // y + mat * y_mat_stride, use weights W[mat * n_experts + e] (offsets on the
 // device; n_experts * n_mats <= 64).  total_rows bounds offsets[n_experts].

@@ -52,6 +52,8 @@ GEMM_VARIANTS = [
     dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=2),
     dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=3), dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1, BARQ_GEMM_NS=4),
     dict(BARQ_GEMM_BM=32, BARQ_GEMM_KG=1), dict(BARQ_GEMM_XCD=0), dict(BARQ_GEMM_IMPL=0),
+    dict(BARQ_GEMM_KS=1), dict(BARQ_GEMM_KS=2), dict(BARQ_GEMM_KS=4, BARQ_GEMM_KG=1),
+    dict(BARQ_GEMM_KS=2, BARQ_GEMM_BM=16), dict(BARQ_GEMM_KS=2, BARQ_GEMM_BM=65), dict(BARQ_GEMM_KS=4, BARQ_GEMM_BM=32),
 ]
 
 
@@ -97,6 +99,26 @@ def test_gemm_variants(be, orc, w_type):
         with env(**v):
             got = be.matmul(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd, m).cpu().numpy()
         assert_close_1e3(got, ref)
+
+
+@pytest.mark.parametrize("w_type", [B.Q4_K, B.Q6_K])
+def test_gemm_k_slices(be, orc, w_type):
+    """Few tiles split K across workgroups (the slices' partial products are
+    added in order): ragged M and N at the slice counts the automatic choice
+    makes (one to eight), device and host buffers, and f32 activations
+    quantized in the call (the quantized rows and the partials share the
+    workspace)."""
+    for n, k, m in [(1000, 4096, 16), (130, 2048, 17), (300, 1024, 40), (4100, 512, 33), (129, 4096, 100)]:
+        w, xq, ref = matmul_case(orc, w_type, n, k, m, 700 + n + m)
+        print(f"k slices {w_type} n={n} k={k} m={m}", flush=True)
+        got = be.matmul(w_type, dev(w), n, k, B.Q8_PARTNER[w_type], dev(xq), m).cpu().numpy()
+        assert_close_1e3(got, ref)
+        y = np.empty((m, n), np.float32)
+        be.matmul_raw(w_type, w, n, k, B.Q8_PARTNER[w_type], xq, m, y, B.MEM_HOST)
+        assert_close_1e3(y, ref)
+        x = synth.gen_f32(m * k, 700 + n + m + 1).reshape(m, k)   # the rows matmul_case quantized
+        got_f = be.matmul(w_type, dev(w), n, k, B.ACT_F32_Q8, dev(x), m).cpu().numpy()
+        assert_close_1e3(got_f, ref)
 
 
 GEMV_VARIANTS = [dict(BARQ_GEMV_DMA=c) for c in (-1, 422, 444, 482, 822, 842, 222, 242, 411, 811)] + [
