@@ -41,7 +41,9 @@ __device__ __forceinline__ int wg_rows_remap(int id, int G) {
 // shared by all rows), then the weight slices of all R rows are issued before
 // any arithmetic (the scheduling barrier keeps the compiler from sinking them
 // next to their uses), so each wave has R rows of HBM traffic in flight.
-template <class F, int R, int WAVES>
+// ONE: k <= 4096, a single 4096-element chunk (no loop: fewer VGPRs, so more
+// waves per SIMD; C2's 7168 waves of two rows are then all resident at once).
+template <class F, int R, int WAVES, bool ONE>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
                     float* __restrict__ y, int n_rows, int k) {
@@ -51,7 +53,7 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
     if (row0 >= n_rows) return;
     const typename F::Lane c = F::lane(l);
     const int nblk = k / F::ROW_BLOCK_ELEMS;
-    const int n_it = (k + 4095) / 4096;
+    const int n_it = ONE ? 1 : (k + 4095) / 4096;
     const int last = n_rows - 1 - row0;
     const uint8_t* wrow = W + (size_t)row0 * row_bytes;
 
@@ -166,8 +168,12 @@ static hipError_t launch_q8(const uint8_t* W, size_t row_bytes, const uint8_t* x
                             int n_rows, int k, hipStream_t s) {
     const int rows_per_block = R * WAVES;
     const unsigned grid = (unsigned)((n_rows + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL((gemv_q8_kernel<F, R, WAVES>), dim3(grid), dim3(WAVES * 64), 0, s,
-                       W, row_bytes, xq, y, n_rows, k);
+    if (k <= 4096)
+        hipLaunchKernelGGL((gemv_q8_kernel<F, R, WAVES, true>), dim3(grid), dim3(WAVES * 64), 0, s,
+                           W, row_bytes, xq, y, n_rows, k);
+    else
+        hipLaunchKernelGGL((gemv_q8_kernel<F, R, WAVES, false>), dim3(grid), dim3(WAVES * 64), 0, s,
+                           W, row_bytes, xq, y, n_rows, k);
     return hipGetLastError();
 }
 
@@ -218,7 +224,7 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
         gemv_dma_supported(w_type, W, n_rows, k, xq))
         return gemv_dma_launch(w_type, W, n_rows, k, xq, y, s);
     switch (w_type) {
-    case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, {2, 2});
+    case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, kk <= 4096 ? GemvCfg{2, 4} : GemvCfg{2, 2});
     case TYPE_Q6_K: return dispatch_q8<FmtQ6K>(w, k / 256 * 210, x, y, n, kk, s, {1, 8});
     case TYPE_Q4_0: return dispatch_q8<FmtQ40>(w, k / 32 * 18, x, y, n, kk, s, {1, 4});
     case TYPE_Q8_0: return dispatch_q8<FmtQ80>(w, k / 32 * 34, x, y, n, kk, s, {1, 4});

@@ -8,10 +8,10 @@ enough distinct copies (> 300 MB) that the 256 MB Infinity Cache cannot
 hold them, activations are quantized once beforehand (their kernel is timed
 on its own line) and all inputs are resident in HBM before timing starts.
 
-The K timed launches are captured into a HIP graph and replayed, so the
-per-launch time measured with HIP events on the launch stream is the
-kernel's own duration rather than host launch overhead; the eager
-back-to-back rate is reported beside it.
+The K timed launches are captured into a HIP graph and replayed five
+times, so the per-launch time measured with HIP events on the launch stream
+(the median of the five replays) is the kernel's own duration rather than
+host launch overhead; the eager back-to-back rate is reported beside it.
 
 The CPU baseline times the reference's per-call CPU arithmetic (an f32
 GEMV over weights dequantized at load, barq_core/src/blas.rs) as restated in
@@ -81,13 +81,17 @@ def time_launches(launch, K, eager):
                     launch(i)
             g.replay()
             torch.cuda.synchronize()
-            t0 = torch.cuda.Event(enable_timing=True)
-            t1 = torch.cuda.Event(enable_timing=True)
-            t0.record(s)
-            g.replay()
-            t1.record(s)
-            t1.synchronize()
-            return t0.elapsed_time(t1) / K, "hip-graph replay"
+            # the median of five timed replays (a single replay varies by a few %)
+            times = []
+            for _ in range(5):
+                t0 = torch.cuda.Event(enable_timing=True)
+                t1 = torch.cuda.Event(enable_timing=True)
+                t0.record(s)
+                g.replay()
+                t1.record(s)
+                t1.synchronize()
+                times.append(t0.elapsed_time(t1) / K)
+            return sorted(times)[2], "hip-graph replay (median of 5)"
         except Exception as e:  # graph capture unavailable: eager launches
             log(f"graph capture failed ({e}); timing eager launches")
     torch.cuda.synchronize()
