@@ -595,6 +595,8 @@ struct MoeArena {
 
 // K slices of the grouped down projection (each writes a partial product)
 constexpr size_t MOE_DOWN_KS = 2;
+// assignments (rows * k) up to which grouping and gather-quantize share a launch
+constexpr size_t MOE_FUSED_GROUP_MAX = 2048;
 
 MoeArena moe_arena(size_t base, size_t ne, size_t hidden, size_t n_ff, size_t na, bool q8) {
     Arena a;
@@ -637,14 +639,23 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
     float* yg = at<float>(h, o_yg);
     uint8_t* qb = at<uint8_t>(h, o_q);
 
-    BARQ_CHECK(launched(barq::moe_group_launch(ids, weights, rows, k, ne, offsets, tokens, wts, rowpos, s), "moe_group"));
-    if (q8 && q8_partner(gt) == BARQ_TYPE_Q8_K && q8_partner(ut) == BARQ_TYPE_Q8_K && q8_partner(dt) == BARQ_TYPE_Q8_K &&
-        barq::kq_supported(gt, n_ff, hidden, na) && barq::kq_supported(ut, n_ff, hidden, na) &&
-        barq::kq_supported(dt, hidden, n_ff, na)) {
+    const bool device_only = q8 && q8_partner(gt) == BARQ_TYPE_Q8_K && q8_partner(ut) == BARQ_TYPE_Q8_K &&
+                             q8_partner(dt) == BARQ_TYPE_Q8_K && barq::kq_supported(gt, n_ff, hidden, na) &&
+                             barq::kq_supported(ut, n_ff, hidden, na) && barq::kq_supported(dt, hidden, n_ff, na);
+    const bool fused_group = device_only && na <= MOE_FUSED_GROUP_MAX && barq::moe_fused_group_enabled();
+    if (fused_group) {
+        // grouping and the gather-quantize of the expert rows in one launch
+        BARQ_CHECK(launched(barq::moe_group_gather_q8k_launch(ids, weights, rows, k, ne, x, hidden, qb, offsets, tokens,
+                                                              wts, rowpos, s), "moe_group_gather"));
+    } else {
+        BARQ_CHECK(launched(barq::moe_group_launch(ids, weights, rows, k, ne, offsets, tokens, wts, rowpos, s), "moe_group"));
+    }
+    if (device_only) {
         // Device-only schedule: every kernel reads the expert row ranges from
         // `offsets`, so nothing waits for the host.  Rows past the last
         // assignment are gathered from token 0 and never read back.
-        BARQ_CHECK(launched(barq::quantize_q8_k_gather_launch(x, tokens, na, hidden, qb, s), "quantize_act"));
+        if (!fused_group)
+            BARQ_CHECK(launched(barq::quantize_q8_k_gather_launch(x, tokens, na, hidden, qb, s), "quantize_act"));
         const size_t chunk = gt == ut ? 32 : 64;   // expert weight pointers per grouped launch
         std::vector<const void*> wp;
         for (size_t e0 = 0; e0 < ne; e0 += chunk) {

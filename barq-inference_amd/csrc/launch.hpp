@@ -98,6 +98,13 @@ hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, 
 hipError_t moe_group_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
                             size_t n_experts, int32_t* offsets, int32_t* tokens, float* wts,
                             int32_t* rowpos, hipStream_t s);
+// moe_group_launch followed by quantize_q8_k_gather_launch(x, tokens) in one
+// launch (rows * top_k <= 2048, hidden % 256 == 0); the second reports the
+// BARQ_MOE_FUSED_GROUP tuning switch (0: two launches)
+int moe_fused_group_enabled();
+hipError_t moe_group_gather_q8k_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
+                                       size_t n_experts, const float* x, size_t hidden, void* out, int32_t* offsets,
+                                       int32_t* tokens, float* wts, int32_t* rowpos, hipStream_t s);
 // xg[i] = x[tokens[i]] for i < n_assign
 hipError_t moe_gather_launch(const float* x, const int32_t* tokens, size_t n_assign, size_t hidden,
                              float* xg, hipStream_t s);

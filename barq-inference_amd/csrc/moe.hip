@@ -4,11 +4,13 @@
 // MFMA kernels.
 #include "common.hpp"
 #include "launch.hpp"
+#include "q8k_block.hpp"
 
 namespace barq {
 
 constexpr int MOE_MAX_EXPERTS = 256;
 constexpr int MOE_MAX_TOPK = 64;
+constexpr int MOE_FUSED_MAX = 2048;   // assignments the fused grouping + gather handles
 constexpr float F32_EPSILON = 1.1920929e-7f;
 
 // select_top_k_experts (moe_fused.rs:95-144), one thread per row: a stable
@@ -177,6 +179,124 @@ hipError_t swiglu_launch(const float* g, const float* u, size_t n, float* h, hip
     size_t grid = (n + 255) / 256;
     if (grid > 16384) grid = 16384;
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)grid), dim3(256), 0, s, g, u, n, h);
+    return hipGetLastError();
+}
+
+// moe_group_kernel and quantize_q8_k_gather_kernel in one launch, for at
+// most MOE_FUSED_MAX assignments: every workgroup groups the assignments
+// itself in LDS (counts, prefix, then each 256-assignment chunk ranked per
+// wave with ballots: one round per distinct expert in the wave), so it knows
+// the token of each grouped row it quantizes; workgroup 0 also writes the
+// offsets / tokens / wts / rowpos arrays that the later kernels read.  The
+// positions are the ones moe_group_kernel assigns (rank among the earlier
+// assignments of the same expert).
+__global__ __launch_bounds__(256) void moe_group_gather_q8k_kernel(
+    const int32_t* __restrict__ ids, const float* __restrict__ weights, int rows, int k, int ne,
+    const float* __restrict__ x, int nbr, uint8_t* __restrict__ out, int nb, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ tokens, float* __restrict__ wts, int32_t* __restrict__ rowpos) {
+    __shared__ int start[MOE_MAX_EXPERTS + 1];
+    __shared__ int wcnt[4][MOE_MAX_EXPERTS];
+    __shared__ int tokl[MOE_FUSED_MAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool writer = blockIdx.x == 0;
+    const int n = rows * k;
+    for (int e = tid; e <= ne; e += 256) start[e] = 0;
+    for (int i = tid; i < 4 * MOE_MAX_EXPERTS; i += 256) (&wcnt[0][0])[i] = 0;
+    __syncthreads();
+    for (int a = tid; a < n; a += 256) {
+        const int e = ids[a];
+        if (e >= 0 && e < ne) atomicAdd(&start[e + 1], 1);
+    }
+    __syncthreads();
+    // exclusive prefix: start[e] <- first grouped row of expert e (one wave, four entries per lane)
+    if (tid < 64) {
+        int v[4], run = 0;
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = 4 * tid + i + 1;
+            v[i] = idx <= ne ? start[idx] : 0;
+            run += v[i];
+        }
+        int inc = run;
+        #pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(inc, o);
+            if (tid >= o) inc += t;
+        }
+        int p = inc - run;
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = 4 * tid + i + 1;
+            p += v[i];
+            if (idx <= ne) start[idx] = p;
+        }
+    }
+    __syncthreads();
+    if (writer)
+        for (int e = tid; e <= ne; e += 256) offsets[e] = start[e];
+    const int total = start[ne];
+    for (int c0 = 0; c0 < n; c0 += 256) {
+        const int a = c0 + tid;
+        int e = a < n ? ids[a] : -1;
+        if (e >= ne) e = -1;
+        int rank = 0;
+        uint64_t todo = __ballot(e >= 0);
+        while (todo) {   // wave-uniform: one round per distinct expert in the wave
+            const int leader = __ffsll((unsigned long long)todo) - 1;
+            const int el = __shfl(e, leader);
+            const uint64_t m = __ballot(e == el);
+            if (e == el) rank = __popcll(m & ((1ull << lane) - 1ull));
+            if (lane == leader) wcnt[wave][el] = __popcll(m);
+            todo &= ~m;
+        }
+        __syncthreads();
+        if (e >= 0) {
+            int pos = start[e] + rank;
+            for (int w = 0; w < wave; w++) pos += wcnt[w][e];
+            tokl[pos] = a;
+            if (writer) {
+                tokens[pos] = a / k;
+                wts[pos] = weights[a];
+                rowpos[a] = pos;
+            }
+        } else if (a < n && writer) {
+            rowpos[a] = -1;
+        }
+        __syncthreads();
+        for (int e2 = tid; e2 < ne; e2 += 256) {
+            start[e2] += wcnt[0][e2] + wcnt[1][e2] + wcnt[2][e2] + wcnt[3][e2];
+            wcnt[0][e2] = wcnt[1][e2] = wcnt[2][e2] = wcnt[3][e2] = 0;
+        }
+        __syncthreads();
+    }
+    // rows past the last assignment (skipped ids) point at token 0
+    if (writer)
+        for (int p = total + tid; p < n; p += 256) {
+            tokens[p] = 0;
+            wts[p] = 0.0f;
+        }
+    const int b = blockIdx.x * 4 + wave;
+    if (b >= nb) return;   // whole waves
+    const int i = b / nbr, cb = b - i * nbr;
+    const int tok = i < total ? tokl[i] / k : 0;
+    const float4 v = reinterpret_cast<const float4*>(x + ((size_t)tok * nbr + cb) * 256)[lane];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    q8_k_block(vv, lane, out + (size_t)b * 292);
+}
+
+// BARQ_MOE_FUSED_GROUP=0 keeps grouping and gather-quantize in two launches
+int moe_fused_group_enabled() { return tuning_env("BARQ_MOE_FUSED_GROUP", 1); }
+
+hipError_t moe_group_gather_q8k_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
+                                       size_t n_experts, const float* x, size_t hidden, void* out, int32_t* offsets,
+                                       int32_t* tokens, float* wts, int32_t* rowpos, hipStream_t s) {
+    const size_t n = rows * top_k, nbr = hidden / 256, nb = n * nbr;
+    if (n == 0 || n > (size_t)MOE_FUSED_MAX || n_experts == 0 || n_experts > (size_t)MOE_MAX_EXPERTS ||
+        hidden % 256 != 0 || nb > (size_t)INT32_MAX)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_group_gather_q8k_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, ids, weights,
+                       (int)rows, (int)top_k, (int)n_experts, x, (int)nbr, static_cast<uint8_t*>(out), (int)nb, offsets,
+                       tokens, wts, rowpos);
     return hipGetLastError();
 }
 

@@ -5,6 +5,8 @@ matmul outputs within 1e-3 (relative L2 and max-abs relative to max |y|),
 the tolerance the north star states.  The oracle for the Q8 paths runs on
 the same quantized activations the GPU produced (after checking those are
 bit-exact with the oracle's own quantization)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -312,6 +314,9 @@ MOE_CASES = {
     # through one pipeline: gate/up 8 x 2 x 64 tiles; down 24 x 32 tiles
     "multi_tile_gate_up": dict(ne=8, hid=512, nff=8192, rows=16, k=2),
     "multi_tile_down": dict(ne=24, hid=4096, nff=512, rows=24, k=2),
+    # grouping fused with the gather-quantize over several 256-assignment
+    # chunks (with skipped ids)
+    "many_chunks": dict(ne=6, hid=256, nff=256, rows=700, k=2),
 }
 
 
@@ -328,10 +333,23 @@ def test_moe_ffn_grouped_cases(be, orc, name):
         ids[5, 1] = -1          # skipped ids
         ids[6, 1] = ne
         ids[7, :] = [2, 2]      # a repeated expert
+    if name == "many_chunks":
+        ids[::37, 1] = -1       # skipped ids spread over the chunks
+        ids[300, :] = [5, 5]
     out = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs], hid, nff,
                      dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
     ref = orc.moe_ffn(gt, gates, ut, ups, dt, downs, hid, nff, x, ids, w, orc.Q8_K)
     assert_close_1e3(host(out), ref)
+    if name == "many_chunks":
+        # grouping in its own launch (the path above 2048 assignments, or with
+        # BARQ_MOE_FUSED_GROUP=0) gives the same rows in the same order
+        os.environ["BARQ_MOE_FUSED_GROUP"] = "0"
+        try:
+            out2 = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs], hid,
+                              nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
+        finally:
+            os.environ.pop("BARQ_MOE_FUSED_GROUP", None)
+        assert np.array_equal(host(out2), host(out))
 
 
 # ---- the quant crate's own Q4_K (quant/src/q4_k.rs): encode and decode bit-exact ----
