@@ -279,7 +279,7 @@ def bench_moe(args):
     for i in range(args.warmup):
         launch(i)
     torch.cuda.synchronize()
-    # the whole step (six kernels, no host synchronisation) as one HIP graph
+    # the whole step (five kernels, no host synchronisation) as one HIP graph
     ms, method = time_launches(launch, args.steps, args.eager)
     ms_eager, _ = time_launches(launch, args.steps, True)
     ids_h = ids.cpu().numpy()
