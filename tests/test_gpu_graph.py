@@ -61,6 +61,26 @@ def test_matvec_and_matmul_graph_replays(be):
     replays_match(be, lambda: be.matmul_raw(B.Q4_K, w, n, k, B.Q8_K, xq, m, ym, B.MEM_DEVICE), ym, noise)
 
 
+@pytest.mark.parametrize("w_type,m", [(B.Q4_0, 16), (B.Q8_0, 40), (B.Q6_K, 24)])
+def test_small_m_matmul_graph_replays(be, w_type, m):
+    """Few tiles: K split across workgroups (partial products in the
+    workspace, then the ordered slice sum), and for the 32-element formats the
+    activation repack, all inside the captured graph."""
+    import torch
+    n, k = 1000, 4096
+    w = dev(synth.gen_weights(w_type, n, k, 13))
+    x = dev(synth.gen_f32(m * k, 14).reshape(m, k))
+    at = B.Q8_PARTNER[w_type]
+    xq = be.quantize_act(at, x)
+    ym = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    other = torch.randn(1 << 20, device="cuda")
+
+    def noise():
+        be.matmul_raw(w_type, w, n, k, at, xq, m, torch.empty_like(ym), B.MEM_DEVICE)   # same workspace
+        other.mul_(1.0001)
+    replays_match(be, lambda: be.matmul_raw(w_type, w, n, k, at, xq, m, ym, B.MEM_DEVICE), ym, noise)
+
+
 def test_moe_step_graph_replays(be, orc):
     import torch
     ne, hid, nff, rows, k = 4, 512, 1024, 24, 2

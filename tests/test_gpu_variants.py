@@ -72,7 +72,7 @@ def test_gemm_32_element_blocks(be, orc, name):
                            (160, 1024, 50, dict(BARQ_GEMM_KG=4)), (160, 768, 20, dict(BARQ_GEMM_KG=4, BARQ_GEMM_BM=32)),
                            (257, 2048, 17, {}), (160, 1024, 50, dict(BARQ_GEMM_KS=1)), (160, 1024, 50, dict(BARQ_GEMM_KS=4)),
                            (160, 1024, 50, dict(BARQ_GEMM_KS=2, BARQ_GEMM_KG=4)), (131, 1024, 19, dict(BARQ_GEMM_KS=4, BARQ_GEMM_KG=1)),
-                           (1100, 512, 33, dict(BARQ_GEMM_KS=2))]:
+                           (1100, 512, 33, dict(BARQ_GEMM_KS=2)), (500, 4096, 16, {})]:   # the last: 16 K slices
         w = synth.gen_weights(t, n, k, 900 + n + k)
         x = synth.gen_f32(m * k, 901 + m).reshape(m, k)
         xq = orc.quantize_act(at, x)
