@@ -313,7 +313,7 @@ size_t act_row_bytes(int act_type, int w_type, size_t k) {
 size_t matmul_scratch(int w_type, size_t n_rows, size_t k, int act_type, size_t m) {
     if (act_type == BARQ_ACT_F32) return m > 1 ? n_rows * k * 4 : 0;
     const size_t q = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(q8_partner(w_type), k), 256) : 0;
-    if (m < 16) return q;
+    if (m < (size_t)barq::gemm_min_rows(w_type)) return q;
     if (barq::b32_supported(w_type, n_rows, k, m)) return q + barq::b32_workspace(m, n_rows, k);
     if (barq::gemm_mfma_supported(w_type, n_rows, k, m)) return q + barq::gemm_mfma_workspace(w_type, n_rows, k, m);
     return q;
@@ -347,7 +347,8 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     // rows of the 32-element-block GEMM
     // the MFMA GEMMs copy weight rows with 4-byte buffer->LDS loads
     const bool w4 = aligned(w, 4);
-    const bool b32 = use_ws && m >= 16 && w4 && barq::b32_supported(w_type, n_rows, k, m);
+    const bool gemm = m >= (size_t)barq::gemm_min_rows(w_type);
+    const bool b32 = use_ws && gemm && w4 && barq::b32_supported(w_type, n_rows, k, m);
     const size_t qbytes = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(aq, k), 256) : 0;
     if (use_ws)
         if (const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m)) BARQ_CHECK(ensure_ws(h, need));
@@ -359,7 +360,7 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
         return fail(BARQ_E_INVALID, "activation blocks misaligned");
     }
     if (b32) return launched(barq::b32_gemm_launch(w_type, w, n_rows, k, xq, m, at<uint8_t>(h, qbytes), y, s), "gemm_b32");
-    if (m >= 16 && w4 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
+    if (gemm && w4 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
         return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, use_ws ? at<uint8_t>(h, qbytes) : nullptr,
                                                    y, s), "gemm_mfma");
     const size_t xrb = row_bytes_of(aq, k);

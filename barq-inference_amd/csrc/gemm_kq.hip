@@ -889,6 +889,18 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
 // (an even number of super-blocks).
 int kq_k_slices_override() { return tuning_env("BARQ_GEMM_KS"); }
 
+// Activation rows from which matmul runs the MFMA GEMMs instead of one GEMV
+// per row (BARQ_GEMM_MIN_M overrides; at least 2).  Measured on MI355X at
+// 4096 x 4096, 14336 x 4096 and 4096 x 14336 (K slices spread the few tiles):
+// the K-quant and Q8_0 GEMMs beat three GEMVs, and the Q4_0 GEMM four (Q4_K
+// 4096 x 4096: 9.5 us against 9.3 / 12.1 us for three / four GEMVs; Q4_0
+// 12.8 against 10.2 / 13.4).
+int gemm_min_rows(int w_type) {
+    const int def = w_type == TYPE_Q4_0 || w_type == TYPE_Q4_0_BARQ ? 4 : 3;
+    const int v = tuning_env("BARQ_GEMM_MIN_M", def);
+    return v < 2 ? 2 : v;
+}
+
 bool kq_supported(int w_type, size_t n_rows, size_t k, size_t m) {
     if ((w_type != TYPE_Q4_K && w_type != TYPE_Q6_K) || k % 256 != 0 || k == 0 || n_rows == 0) return false;
     const size_t nsb = k / 256;

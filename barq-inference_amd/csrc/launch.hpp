@@ -80,6 +80,8 @@ hipError_t kq_grouped_launch(int w_type, const void* const* W, size_t n_experts,
                              size_t total_rows, size_t n_rows, size_t k, const void* xq, float* y, size_t y_mat_stride,
                              size_t k_slices, size_t y_k_stride, hipStream_t s);
 int kq_k_slices_override();
+// rows from which matmul takes the MFMA GEMMs (BARQ_GEMM_MIN_M overrides)
+int gemm_min_rows(int w_type);
 
 // f32blas.hip
 hipError_t gemm_f32_launch(const float* a, const float* b, size_t m, size_t k, size_t n, float* c,

@@ -121,6 +121,30 @@ def test_gemm_k_slices(be, orc, w_type):
         assert_close_1e3(got_f, ref)
 
 
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q4_0", "Q8_0", "Q4_0_BARQ"])
+def test_matmul_small_m(be, orc, name):
+    """A few activation rows: the MFMA GEMMs from 3 rows (4 for Q4_0), one
+    GEMV per row below; each M also with both paths forced
+    (BARQ_GEMM_MIN_M=2: always the GEMM; 16: GEMVs up to 15 rows), device and
+    host buffers."""
+    t = getattr(B, name)
+    at = B.Q8_PARTNER[t]
+    n, k = 300, 1024
+    w = synth.gen_weights(t, n, k, 820)
+    wd = dev(w)
+    for m in (2, 3, 4, 7, 15):
+        x = synth.gen_f32(m * k, 821 + m).reshape(m, k)
+        xq = orc.quantize_act(at, x)
+        ref = orc.matmul(t, w, n, k, at, xq, m)
+        for env_v in ({}, dict(BARQ_GEMM_MIN_M=2), dict(BARQ_GEMM_MIN_M=16)):
+            print(f"small m {name} m={m} {env_v}", flush=True)
+            with env(**env_v):
+                assert_close_1e3(be.matmul(t, wd, n, k, at, dev(xq), m).cpu().numpy(), ref)
+                y = np.empty((m, n), np.float32)
+                be.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
+                assert_close_1e3(y, ref)
+
+
 GEMV_VARIANTS = [dict(BARQ_GEMV_DMA=c) for c in (-1, 422, 444, 482, 822, 842, 222, 242, 411, 811)] + [
     dict(BARQ_GEMV_DMA_TYPES=0), dict(BARQ_GEMV_DMA_TYPES=31)] + [
     dict(BARQ_GEMV_DMA_TYPES=0, BARQ_GEMV_CFG=c) for c in ("1,4", "2,4", "4,4", "8,4", "1,8", "2,8", "4,8", "2,2",
