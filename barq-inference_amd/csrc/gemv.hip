@@ -85,6 +85,57 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
     }
 }
 
+// A few activation rows (2-4 tokens of a small decode batch): each wave's
+// weight slices are loaded once per chunk and dotted with every row's
+// activation slice, so the weights are read once instead of once per token.
+// y is [NX x n_rows] (row-major, token-major).
+template <class F, int R, int WAVES, int NX>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q8_multi_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
+                          size_t x_row_bytes, float* __restrict__ y, int n_rows, int k) {
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
+    if (row0 >= n_rows) return;
+    const typename F::Lane c = F::lane(l);
+    const int nblk = k / F::ROW_BLOCK_ELEMS;
+    const int n_it = (k + 4095) / 4096;
+    const int last = n_rows - 1 - row0;
+    const uint8_t* wrow = W + (size_t)row0 * row_bytes;
+    constexpr int NA = NX * R;   // sums per lane: token j, weight row r at j * R + r
+
+    float acc[NA];
+    #pragma unroll
+    for (int i = 0; i < NA; i++) acc[i] = 0.0f;
+
+    for (int it = 0; it < n_it; it++) {
+        if (F::active(it, c, nblk)) {
+            typename F::X xs[NX];
+            #pragma unroll
+            for (int j = 0; j < NX; j++) F::load_x(xs[j], xq + (size_t)j * x_row_bytes, it, c, nblk);
+            typename F::Wt w[R];
+            #pragma unroll
+            for (int r = 0; r < R; r++) F::load_w(w[r], wrow + (size_t)min(r, last) * row_bytes, it, c, nblk);
+            __builtin_amdgcn_sched_barrier(0);
+            #pragma unroll
+            for (int j = 0; j < NX; j++)
+                #pragma unroll
+                for (int r = 0; r < R; r++) acc[j * R + r] += F::dot(w[r], xs[j], c);
+        }
+    }
+
+    #pragma unroll
+    for (int g = 0; g < NA; g += 4) {
+        const float v = reduce4(acc[g], g + 1 < NA ? acc[g + 1] : 0.0f, g + 2 < NA ? acc[g + 2] : 0.0f,
+                                g + 3 < NA ? acc[g + 3] : 0.0f);
+        if ((l & 15) == 0) {
+            const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+            const int j = f / R, rr = f - j * R;
+            if (f < NA && rr <= last) y[(size_t)j * n_rows + row0 + rr] = v;
+        }
+    }
+}
+
 // Literal path: x (f32) staged in LDS, weights dequantized in registers.
 template <class F, int R, int WAVES>
 __global__ __launch_bounds__(WAVES * 64)
@@ -200,6 +251,37 @@ static hipError_t launch_f32(const uint8_t* W, size_t row_bytes, const float* x,
     hipLaunchKernelGGL((gemv_f32_kernel<F, R, WAVES>), dim3(grid), dim3(WAVES * 64), lds, s,
                        W, row_bytes, x, y, n_rows, k);
     return hipGetLastError();
+}
+
+template <class F, int R, int WAVES, int NX>
+static hipError_t launch_q8_multi(const uint8_t* W, size_t row_bytes, const uint8_t* xq, size_t x_row_bytes,
+                                  float* y, int n_rows, int k, hipStream_t s) {
+    const int rows_per_block = R * WAVES;
+    const unsigned grid = (unsigned)((n_rows + rows_per_block - 1) / rows_per_block);
+    hipLaunchKernelGGL((gemv_q8_multi_kernel<F, R, WAVES, NX>), dim3(grid), dim3(WAVES * 64), 0, s,
+                       W, row_bytes, xq, x_row_bytes, y, n_rows, k);
+    return hipGetLastError();
+}
+
+// Tokens up to which a Q4_K matmul runs the multi-row GEMV (BARQ_GEMV_MULTI_MAX
+// overrides, 0 turns it off; at most 4).
+bool gemv_multi_supported(int w_type, size_t m) {
+    const int mx = tuning_env("BARQ_GEMV_MULTI_MAX", 4);
+    return w_type == TYPE_Q4_K && m >= 2 && (int)m <= (mx < 4 ? mx : 4);
+}
+
+hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,
+                                float* y, hipStream_t s) {
+    if (!gemv_multi_supported(w_type, m) || k % 256 != 0 || n_rows > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+    const size_t rb = k / 256 * 144, xrb = k / 256 * 292;
+    const int n = (int)n_rows, kk = (int)k;
+    switch (m) {
+    case 2: return launch_q8_multi<FmtQ4K, 2, 4, 2>(w, rb, x, xrb, y, n, kk, s);
+    case 3: return launch_q8_multi<FmtQ4K, 2, 4, 3>(w, rb, x, xrb, y, n, kk, s);
+    default: return launch_q8_multi<FmtQ4K, 2, 4, 4>(w, rb, x, xrb, y, n, kk, s);
+    }
 }
 
 // Formats that take the LDS-streaming GEMV (gemv_dma.hip) when its layout

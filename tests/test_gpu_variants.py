@@ -123,26 +123,29 @@ def test_gemm_k_slices(be, orc, w_type):
 
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_matmul_small_m(be, orc, name):
-    """A few activation rows: the MFMA GEMMs from 3 rows (4 for Q4_0), one
-    GEMV per row below; each M also with both paths forced
-    (BARQ_GEMM_MIN_M=2: always the GEMM; 16: GEMVs up to 15 rows), device and
-    host buffers."""
+    """A few activation rows: Q4_K runs 2-4 rows on the multi-row GEMV
+    (k = 5120 also: a second, partial 4096-element chunk); otherwise the MFMA
+    GEMMs from 3 rows (4 for Q4_0) and one GEMV per row below; each M also
+    with the GEMM and the per-row GEMVs forced (BARQ_GEMM_MIN_M=2 or 16, the
+    multi-row GEMV off), device and host buffers."""
     t = getattr(B, name)
     at = B.Q8_PARTNER[t]
-    n, k = 300, 1024
-    w = synth.gen_weights(t, n, k, 820)
-    wd = dev(w)
-    for m in (2, 3, 4, 7, 15):
-        x = synth.gen_f32(m * k, 821 + m).reshape(m, k)
-        xq = orc.quantize_act(at, x)
-        ref = orc.matmul(t, w, n, k, at, xq, m)
-        for env_v in ({}, dict(BARQ_GEMM_MIN_M=2), dict(BARQ_GEMM_MIN_M=16)):
-            print(f"small m {name} m={m} {env_v}", flush=True)
-            with env(**env_v):
-                assert_close_1e3(be.matmul(t, wd, n, k, at, dev(xq), m).cpu().numpy(), ref)
-                y = np.empty((m, n), np.float32)
-                be.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
-                assert_close_1e3(y, ref)
+    shapes = [(300, 1024)] + ([(77, 5120)] if t == B.Q4_K else [])   # Q4_K: 2-4 rows take the multi-row GEMV
+    variants = [{}, dict(BARQ_GEMM_MIN_M=2, BARQ_GEMV_MULTI_MAX=0), dict(BARQ_GEMM_MIN_M=16, BARQ_GEMV_MULTI_MAX=0)]
+    for n, k in shapes:
+        w = synth.gen_weights(t, n, k, 820)
+        wd = dev(w)
+        for m in (2, 3, 4, 7, 15):
+            x = synth.gen_f32(m * k, 821 + m).reshape(m, k)
+            xq = orc.quantize_act(at, x)
+            ref = orc.matmul(t, w, n, k, at, xq, m)
+            for env_v in variants:
+                print(f"small m {name} n={n} k={k} m={m} {env_v}", flush=True)
+                with env(**env_v):
+                    assert_close_1e3(be.matmul(t, wd, n, k, at, dev(xq), m).cpu().numpy(), ref)
+                    y = np.empty((m, n), np.float32)
+                    be.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
+                    assert_close_1e3(y, ref)
 
 
 GEMV_VARIANTS = [dict(BARQ_GEMV_DMA=c) for c in (-1, 422, 444, 482, 822, 842, 222, 242, 411, 811)] + [
