@@ -359,7 +359,7 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
     } else if (!aligned(x, aq == BARQ_TYPE_Q8_K ? 4 : 2)) {
         return fail(BARQ_E_INVALID, "activation blocks misaligned");
     }
-    if (barq::gemv_multi_supported(w_type, m))
+    if (barq::gemv_multi_supported(w_type, w, n_rows, k, xq, m))
         return launched(barq::gemv_q8_multi_launch(w_type, w, n_rows, k, xq, m, y, s), "gemv_q8_multi");
     if (b32) return launched(barq::b32_gemm_launch(w_type, w, n_rows, k, xq, m, at<uint8_t>(h, qbytes), y, s), "gemm_b32");
     if (gemm && w4 && barq::gemm_mfma_supported(w_type, n_rows, k, m))

@@ -263,16 +263,28 @@ static hipError_t launch_q8_multi(const uint8_t* W, size_t row_bytes, const uint
     return hipGetLastError();
 }
 
-// Tokens up to which a Q4_K matmul runs the multi-row GEMV (BARQ_GEMV_MULTI_MAX
-// overrides, 0 turns it off; at most 4).
-bool gemv_multi_supported(int w_type, size_t m) {
+static int dma_bit(int w_type);
+
+// A matmul of 2-4 tokens as one GEMV over all of them: the register GEMV for
+// Q4_K, the LDS-streamed one for the formats that take it at batch 1 (its
+// layout conditions, and the tokens' staged rows within LDS).
+// BARQ_GEMV_MULTI_MAX caps the tokens (0 turns it off).
+static bool multi_dma(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m) {
+    return (tuning_env("BARQ_GEMV_DMA_TYPES", 2 | 4 | 8 | 16) & dma_bit(w_type)) &&
+           gemv_dma_supported(w_type, W, n_rows, k, xq) && gemv_dma_multi_fits(w_type, k, m);
+}
+
+bool gemv_multi_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m) {
     const int mx = tuning_env("BARQ_GEMV_MULTI_MAX", 4);
-    return w_type == TYPE_Q4_K && m >= 2 && (int)m <= (mx < 4 ? mx : 4);
+    if (m < 2 || (int)m > (mx < 4 ? mx : 4) || n_rows > (size_t)INT32_MAX) return false;
+    if (multi_dma(w_type, W, n_rows, k, xq, m)) return true;
+    return w_type == TYPE_Q4_K && k % 256 == 0;
 }
 
 hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,
                                 float* y, hipStream_t s) {
-    if (!gemv_multi_supported(w_type, m) || k % 256 != 0 || n_rows > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    if (!gemv_multi_supported(w_type, W, n_rows, k, xq, m)) return hipErrorInvalidValue;
+    if (multi_dma(w_type, W, n_rows, k, xq, m)) return gemv_dma_launch(w_type, W, n_rows, k, xq, y, s, m);
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     const size_t rb = k / 256 * 144, xrb = k / 256 * 292;

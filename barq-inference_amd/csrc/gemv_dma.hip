@@ -218,8 +218,11 @@ struct DQ40B {
     }
 };
 
-// W waves per workgroup, R rows per wave, D slices in flight per wave.
-template <class P, int W, int R, int D>
+// W waves per workgroup, R rows per wave, D slices in flight per wave; NX
+// activation rows (tokens), each staged in its own x_region of LDS and dotted
+// with every weight slice, so the weights are streamed once for all of them
+// (y is [NX x n_rows]).
+template <class P, int W, int R, int D, int NX = 1>
 __global__ __launch_bounds__(W * 64)
 void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t* __restrict__ xq, uint32_t x_bytes,
                      float* __restrict__ y, int n_rows, int nblk, uint32_t x_region) {
@@ -232,13 +235,17 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
     const int row0 = (blockIdx.x * W + wave) * R;
     const int n_it = (nblk + P::SLICE_BLOCKS - 1) / P::SLICE_BLOCKS;
     uint8_t* xs = smem;
-    uint8_t* bufs = smem + x_region + wave * (D * SL);
+    uint8_t* bufs = smem + NX * x_region + wave * (D * SL);
 
-    // activation: every wave copies part of it
+    // activation: every wave copies part of it (each token's row with its own
+    // descriptor, so reads past a row return zeros as for one token)
     {
-        const i32x4v xr = make_rsrc4(xq, x_bytes);
         const int n_instr = (P::XS::chunks(nblk) + 63) / 64;
-        for (int q = wave; q < n_instr; q += W) lds_load16(xr, xs + 1024 * q, P::XS::src(64 * q + l, nblk), 0);
+        for (int q = wave; q < NX * n_instr; q += W) {
+            const int j = q / n_instr, qq = q - j * n_instr;
+            const i32x4v xr = make_rsrc4(xq + (size_t)j * x_bytes, x_bytes);
+            lds_load16(xr, xs + (size_t)j * x_region + 1024 * qq, P::XS::src(64 * qq + l, nblk), 0);
+        }
     }
     const bool live = row0 < n_rows;
     const int rows_here = live ? min(R, n_rows - row0) : 1;
@@ -269,14 +276,16 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
     if (!live) return;   // after the barrier: the other waves needed this wave's activation part
 
     const typename F::Lane c = F::lane(l);
-    float acc[R];
+    constexpr int NA = NX * R;   // token j, row r at j * R + r
+    float acc[NA];
     #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int i = 0; i < NA; i++) acc[i] = 0.0f;
 
     for (int it = 0; it < n_it; it++) {
         const bool act = F::active(it, c, nblk);
-        typename F::X x;
-        P::load_x(x, xs, it, c, nblk);
+        typename F::X x[NX];
+        #pragma unroll
+        for (int j = 0; j < NX; j++) P::load_x(x[j], xs + (size_t)j * x_region, it, c, nblk);
         #pragma unroll
         for (int r = 0; r < R; r++) {
             const int u = it * R + r;
@@ -287,8 +296,11 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
             }
             typename F::Wt w;
             P::load_w(w, bufs + (r % D) * SL, c);
-            const float v = F::dot(w, x, c);
-            if (act) acc[r] += v;
+            #pragma unroll
+            for (int j = 0; j < NX; j++) {
+                const float v = F::dot(w, x[j], c);
+                if (act) acc[j * R + r] += v;
+            }
             // the slice buffer is reused for unit u + D once its values are in registers
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (u + D < U) issue(u + D);
@@ -296,12 +308,13 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
     }
 
     #pragma unroll
-    for (int g = 0; g < R; g += 4) {
-        const float v = reduce4(acc[g], g + 1 < R ? acc[g + 1] : 0.0f, g + 2 < R ? acc[g + 2] : 0.0f,
-                                g + 3 < R ? acc[g + 3] : 0.0f);
+    for (int g = 0; g < NA; g += 4) {
+        const float v = reduce4(acc[g], g + 1 < NA ? acc[g + 1] : 0.0f, g + 2 < NA ? acc[g + 2] : 0.0f,
+                                g + 3 < NA ? acc[g + 3] : 0.0f);
         if ((l & 15) == 0) {
-            const int rr = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
-            if (rr < R && row0 + rr < n_rows) y[row0 + rr] = v;
+            const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+            const int j = f / R, rr = f - j * R;
+            if (f < NA && row0 + rr < n_rows) y[(size_t)j * n_rows + row0 + rr] = v;
         }
     }
 }
@@ -309,25 +322,37 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
 // ---- launch ------------------------------------------------------------------
 // tuning: BARQ_GEMV_DMA = W*100+R*10+D selects another launch shape (e.g. 842); -1 turns the path off
 
-template <class P, int W, int R, int D>
+template <class P, int W, int R, int D, int NX = 1>
 static hipError_t launch_dma(const uint8_t* Wq, uint32_t rb, size_t n_rows, int nblk, const uint8_t* xq,
                              uint32_t x_bytes, uint32_t x_region, float* y, hipStream_t s) {
-    const size_t lds = x_region + (size_t)W * D * 1024 * P::SLICE_INSTR;
+    const size_t lds = (size_t)NX * x_region + (size_t)W * D * 1024 * P::SLICE_INSTR;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     // the whole 160 KiB enabled once per instance (thread-safe static init),
     // so concurrent callers never lower it below their own launch
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_dma_kernel<P, W, R, D>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_dma_kernel<P, W, R, D, NX>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)((n_rows + (size_t)W * R - 1) / ((size_t)W * R));
-    hipLaunchKernelGGL((gemv_dma_kernel<P, W, R, D>), dim3(grid), dim3(W * 64), lds, s, Wq, rb, xq, x_bytes, y,
+    hipLaunchKernelGGL((gemv_dma_kernel<P, W, R, D, NX>), dim3(grid), dim3(W * 64), lds, s, Wq, rb, xq, x_bytes, y,
                        (int)n_rows, nblk, x_region);
     return hipGetLastError();
 }
 
+// The default launch shapes for NX tokens (several tokens: no tuning cases).
+template <class P, int NX>
+static hipError_t launch_dma_default(const uint8_t* w, uint32_t rb, size_t n_rows, int nblk, const uint8_t* x,
+                                     uint32_t x_bytes, uint32_t x_region, float* y, hipStream_t s) {
+    // measured on MI355X: four rows per wave for the 128256-row Q6_K head
+    // (C3); for the 32-element formats one row per wave (more workgroups) up
+    // to 8192 rows (C1: 3.82 against 3.94 us), two above
+    if constexpr (P::SLICE_BLOCKS == 16) return launch_dma<P, 4, 4, 2, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    else if (n_rows <= 8192) return launch_dma<P, 4, 1, 1, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    else return launch_dma<P, 4, 2, 2, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+}
+
 template <class P>
 static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const void* xq, float* y, hipStream_t s,
-                               int blk_bytes, int x_blk_bytes) {
+                               int blk_bytes, int x_blk_bytes, size_t m) {
     const int nblk = (int)(k / (P::SLICE_BLOCKS == 16 ? 256 : 32));
     const uint32_t rb = (uint32_t)(nblk * blk_bytes);
     const int xnb = P::XS::BLK_ELEMS == 256 ? (int)(k / 256) : nblk;
@@ -336,19 +361,20 @@ static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const voi
     const uint32_t x_region = (uint32_t)((xch + 63) / 64 * 1024);
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const uint8_t* x = static_cast<const uint8_t*>(xq);
+    switch (m) {
+    case 1: break;
+    case 2: return launch_dma_default<P, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    case 3: return launch_dma_default<P, 3>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    case 4: return launch_dma_default<P, 4>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    default: return hipErrorInvalidValue;
+    }
 #define BARQ_DMA_CASE(WW, RR, DD) \
     case WW * 100 + RR * 10 + DD: return launch_dma<P, WW, RR, DD>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
     switch (tuning_env("BARQ_GEMV_DMA")) {
     BARQ_DMA_CASE(4, 2, 2) BARQ_DMA_CASE(4, 4, 4) BARQ_DMA_CASE(4, 8, 2) BARQ_DMA_CASE(8, 2, 2)
     BARQ_DMA_CASE(8, 4, 2) BARQ_DMA_CASE(2, 2, 2) BARQ_DMA_CASE(2, 4, 2) BARQ_DMA_CASE(4, 1, 1)
     BARQ_DMA_CASE(8, 1, 1)
-    default:
-        // measured on MI355X: four rows per wave for the 128256-row Q6_K head
-        // (C3); for the 32-element formats one row per wave (more
-        // workgroups) up to 8192 rows (C1: 3.82 against 3.94 us), two above
-        if constexpr (P::SLICE_BLOCKS == 16) return launch_dma<P, 4, 4, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
-        else if (n_rows <= 8192) return launch_dma<P, 4, 1, 1>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
-        else return launch_dma<P, 4, 2, 2>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    default: return launch_dma_default<P, 1>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
     }
 #undef BARQ_DMA_CASE
 }
@@ -373,17 +399,25 @@ bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, cons
     return rb * 8 < (1ull << 31) && (xch + 63) / 64 * 1024 <= 96 * 1024;
 }
 
+// m tokens (1-4); y is [m x n_rows]
 hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, float* y,
-                           hipStream_t s) {
+                           hipStream_t s, size_t m) {
     if (n_rows == 0) return hipSuccess;
     switch (w_type) {
-    case TYPE_Q6_K: return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES);
-    case TYPE_Q4_K: return dispatch_dma<DQ4K>(W, n_rows, k, xq, y, s, Q4_K_BYTES, Q8_K_BYTES);
-    case TYPE_Q4_0: return dispatch_dma<DQ40>(W, n_rows, k, xq, y, s, Q4_0_BYTES, Q8_0_BYTES);
-    case TYPE_Q8_0: return dispatch_dma<DQ80>(W, n_rows, k, xq, y, s, Q8_0_BYTES, Q8_0_BYTES);
-    case TYPE_Q4_0_BARQ: return dispatch_dma<DQ40B>(W, n_rows, k, xq, y, s, Q4_0_BARQ_BYTES, Q8_0_BYTES);
+    case TYPE_Q6_K: return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES, m);
+    case TYPE_Q4_K: return dispatch_dma<DQ4K>(W, n_rows, k, xq, y, s, Q4_K_BYTES, Q8_K_BYTES, m);
+    case TYPE_Q4_0: return dispatch_dma<DQ40>(W, n_rows, k, xq, y, s, Q4_0_BYTES, Q8_0_BYTES, m);
+    case TYPE_Q8_0: return dispatch_dma<DQ80>(W, n_rows, k, xq, y, s, Q8_0_BYTES, Q8_0_BYTES, m);
+    case TYPE_Q4_0_BARQ: return dispatch_dma<DQ40B>(W, n_rows, k, xq, y, s, Q4_0_BARQ_BYTES, Q8_0_BYTES, m);
     default: return hipErrorInvalidValue;
     }
+}
+
+// The staged rows of m tokens fit LDS beside the default slice buffers
+// (gemv_dma_supported bounds one token's at 96 KiB).
+bool gemv_dma_multi_fits(int w_type, size_t k, size_t m) {
+    const size_t xch = w_type == TYPE_Q6_K || w_type == TYPE_Q4_K ? k / 256 * 19 : (k / 32 * Q8_0_BYTES + 15) / 16;
+    return m * ((xch + 63) / 64 * 1024) <= 96 * 1024;
 }
 
 }  // namespace barq

@@ -38,15 +38,16 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
                           float* y, hipStream_t s);
 hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
                            float* y, hipStream_t s);
-// Q4_K against 2-4 Q8_K rows at once (y[m x n_rows]): the weights read once
-bool gemv_multi_supported(int w_type, size_t m);
+// 2-4 Q8 activation rows at once (y[m x n_rows]): the weights read once
+bool gemv_multi_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m);
 hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,
                                 float* y, hipStream_t s);
 
 // gemv_dma.hip: the same GEMV streaming row slices through LDS
 bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq);
 hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, float* y,
-                           hipStream_t s);
+                           hipStream_t s, size_t m = 1);
+bool gemv_dma_multi_fits(int w_type, size_t k, size_t m);
 
 // gemm_mfma.hip: Y[m x n] = X W^T with int8 MFMA (X as Q8_K rows); ws holds
 // gemm_mfma_workspace(...) bytes (K slices' partial products, often none)

@@ -153,9 +153,10 @@ int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* 
  *   matvec: y[n_rows] = W x.
  *   matmul: Y[m x n_rows] (row-major) = X W^T, X is m rows of k (f32 or Q8
  *           blocks per row) — gemm_f32(X, W^T, m, k, n_rows).
- * Q4_K with m = 2..4 runs one GEMV over all rows (weights read once).  From
- * m = 3 (m = 4 for Q4_0 / Q4_0_BARQ; m = 5 for Q4_K) matmul runs the
- * LDS-staged int8-MFMA kernel instead of one GEMV per row; it may use the
+ * m = 2..4 runs one GEMV over all rows (weights read once); from m = 5
+ * (or where that GEMV's layout conditions fail, from m = 3, or 4 for
+ * Q4_0 / Q4_0_BARQ) matmul runs the LDS-staged int8-MFMA kernel instead of
+ * one GEMV per row; it may use the
  * handle's workspace (repacked Q8_0 rows, K-slice partial products), which
  * grows on the first call that needs more. */
 int barq_rocm_matvec(barq_rocm_handle* h, int w_type, const void* w,

@@ -123,14 +123,15 @@ def test_gemm_k_slices(be, orc, w_type):
 
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_matmul_small_m(be, orc, name):
-    """A few activation rows: Q4_K runs 2-4 rows on the multi-row GEMV
-    (k = 5120 also: a second, partial 4096-element chunk); otherwise the MFMA
-    GEMMs from 3 rows (4 for Q4_0) and one GEMV per row below; each M also
-    with the GEMM and the per-row GEMVs forced (BARQ_GEMM_MIN_M=2 or 16, the
-    multi-row GEMV off), device and host buffers."""
+    """A few activation rows: 2-4 rows run one GEMV over all of them (the
+    register GEMV for Q4_K, the LDS-streamed one for the other formats; k =
+    5120 adds a second, partial 4096-element chunk), 5 and more the MFMA
+    GEMMs; each M also with the GEMM and the per-row GEMVs forced
+    (BARQ_GEMM_MIN_M=2 or 16 with the multi-row GEMV off), device and host
+    buffers."""
     t = getattr(B, name)
     at = B.Q8_PARTNER[t]
-    shapes = [(300, 1024)] + ([(77, 5120)] if t == B.Q4_K else [])   # Q4_K: 2-4 rows take the multi-row GEMV
+    shapes = [(300, 1024), (77, 5120)]
     variants = [{}, dict(BARQ_GEMM_MIN_M=2, BARQ_GEMV_MULTI_MAX=0), dict(BARQ_GEMM_MIN_M=16, BARQ_GEMV_MULTI_MAX=0)]
     for n, k in shapes:
         w = synth.gen_weights(t, n, k, 820)
