@@ -600,6 +600,8 @@ struct MoeArena {
 constexpr size_t MOE_DOWN_KS = 2;
 // assignments (rows * k) up to which grouping and gather-quantize share a launch
 constexpr size_t MOE_FUSED_GROUP_MAX = 2048;
+// assignments up to which the expert projections run as grouped GEMVs
+constexpr size_t MOE_GEMV_MAX_ASSIGN = 4;
 
 MoeArena moe_arena(size_t base, size_t ne, size_t hidden, size_t n_ff, size_t na, bool q8) {
     Arena a;
@@ -661,6 +663,39 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
             BARQ_CHECK(launched(barq::quantize_q8_k_gather_launch(x, tokens, na, hidden, qb, s), "quantize_act"));
         const size_t chunk = gt == ut ? 32 : 64;   // expert weight pointers per grouped launch
         std::vector<const void*> wp;
+        // Single-token steps (decode): expert-grouped GEMVs, which stream each
+        // used expert's weights once at GEMV speed instead of through 32-row
+        // MFMA tiles (measured faster for one token only; BARQ_MOE_GEMV=2 also
+        // takes them for any step of at most 4 assignments, 0 never).
+        const int moe_gemv = barq::moe_gemv_enabled();
+        const bool gemv_step = na <= MOE_GEMV_MAX_ASSIGN && (moe_gemv == 2 || (moe_gemv == 1 && rows == 1)) &&
+                               barq::moe_gemv_supported(gt, chunk, gt == ut ? 2 : 1, n_ff, hidden) &&
+                               barq::moe_gemv_supported(ut, chunk, gt == ut ? 2 : 1, n_ff, hidden) &&
+                               barq::moe_gemv_supported(dt, 64, 1, hidden, n_ff);
+        if (gemv_step) {
+            for (size_t e0 = 0; e0 < ne; e0 += chunk) {
+                const size_t c = ne - e0 < chunk ? ne - e0 : chunk;
+                if (gt == ut) {
+                    wp.assign(gate + e0, gate + e0 + c);
+                    wp.insert(wp.end(), up + e0, up + e0 + c);
+                    BARQ_CHECK(launched(barq::moe_gemv_launch(gt, wp.data(), c, 2, offsets + e0, na, rows, qb, n_ff, hidden, gb,
+                                                              na * n_ff, s), "moe gate/up gemv"));
+                } else {
+                    BARQ_CHECK(launched(barq::moe_gemv_launch(gt, gate + e0, c, 1, offsets + e0, na, rows, qb, n_ff, hidden, gb, 0, s),
+                                        "moe gate gemv"));
+                    BARQ_CHECK(launched(barq::moe_gemv_launch(ut, up + e0, c, 1, offsets + e0, na, rows, qb, n_ff, hidden, ub, 0, s),
+                                        "moe up gemv"));
+                }
+            }
+            BARQ_CHECK(launched(barq::swiglu_q8_k_launch(gb, ub, na, n_ff, qb, s), "swiglu"));
+            for (size_t e0 = 0; e0 < ne; e0 += 64) {
+                const size_t c = ne - e0 < 64 ? ne - e0 : 64;
+                BARQ_CHECK(launched(barq::moe_gemv_launch(dt, down + e0, c, 1, offsets + e0, na, rows, qb, hidden, n_ff, yg, 0, s),
+                                    "moe down gemv"));
+            }
+            return launched(barq::moe_scatter_launch(yg, ids, weights, rowpos, rows, k, hidden, out, s, 1, 0),
+                            "moe_scatter");
+        }
         for (size_t e0 = 0; e0 < ne; e0 += chunk) {
             const size_t c = ne - e0 < chunk ? ne - e0 : chunk;
             if (gt == ut) {

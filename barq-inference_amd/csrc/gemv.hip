@@ -89,10 +89,12 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
 // weight slices are loaded once per chunk and dotted with every row's
 // activation slice, so the weights are read once instead of once per token.
 // y is [NX x n_rows] (row-major, token-major).
+// nvalid <= NX tokens are real: the others re-read token nvalid - 1 and are
+// not stored (one instantiation serves every count up to NX).
 template <class F, int R, int WAVES, int NX>
-__global__ __launch_bounds__(WAVES * 64)
-void gemv_q8_multi_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
-                          size_t x_row_bytes, float* __restrict__ y, int n_rows, int k) {
+__device__ __forceinline__ void gemv_multi_body(const uint8_t* __restrict__ W, size_t row_bytes,
+                                                const uint8_t* __restrict__ xq, size_t x_row_bytes,
+                                                float* __restrict__ y, int n_rows, int k, int nvalid = NX) {
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
@@ -112,7 +114,7 @@ void gemv_q8_multi_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const
         if (F::active(it, c, nblk)) {
             typename F::X xs[NX];
             #pragma unroll
-            for (int j = 0; j < NX; j++) F::load_x(xs[j], xq + (size_t)j * x_row_bytes, it, c, nblk);
+            for (int j = 0; j < NX; j++) F::load_x(xs[j], xq + (size_t)min(j, nvalid - 1) * x_row_bytes, it, c, nblk);
             typename F::Wt w[R];
             #pragma unroll
             for (int r = 0; r < R; r++) F::load_w(w[r], wrow + (size_t)min(r, last) * row_bytes, it, c, nblk);
@@ -131,8 +133,58 @@ void gemv_q8_multi_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const
         if ((l & 15) == 0) {
             const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
             const int j = f / R, rr = f - j * R;
-            if (f < NA && rr <= last) y[(size_t)j * n_rows + row0 + rr] = v;
+            if (f < NA && j < nvalid && rr <= last) y[(size_t)j * n_rows + row0 + rr] = v;
         }
+    }
+}
+
+template <class F, int R, int WAVES, int NX>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q8_multi_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
+                          size_t x_row_bytes, float* __restrict__ y, int n_rows, int k) {
+    gemv_multi_body<F, R, WAVES, NX>(W, row_bytes, xq, x_row_bytes, y, n_rows, k);
+}
+
+// Expert-grouped GEMV for decode-size MoE steps.  A step of na assignments
+// has rows in at most na experts, so the grid has `slots` = min(na, ne) rows
+// of workgroups per weight set: blockIdx.y = mat * slots + slot takes the
+// slot-th expert e that has rows (found from the device offsets with one
+// ballot: no host synchronisation), i.e. rows [offsets[e], offsets[e + 1])
+// of the grouped activation rows X against the weights w[mat * ne + e]
+// (n_rows x k) into rows of Y + mat * ymat, NXP tokens per pass (the host
+// sets NXP to the step's token count, which bounds an expert's rows unless a
+// token repeats an expert; the VGPRs, and so the waves per SIMD, follow NXP).
+// Slots past the experts that have rows exit at once.
+struct MoeGemvWeights { const uint8_t* w[MOE_GEMV_MAXE]; };
+
+template <class F, int R, int WAVES, int NXP>
+__global__ __launch_bounds__(WAVES * 64)
+void moe_gemv_kernel(MoeGemvWeights wt, const int32_t* __restrict__ offsets, int ne, int slots,
+                     const uint8_t* __restrict__ X, size_t xrb, float* __restrict__ Y, size_t ymat, size_t row_bytes,
+                     int n_rows, int k) {
+    const int mat = blockIdx.y / slots;
+    int slot = blockIdx.y - mat * slots;
+    const int lane = threadIdx.x & 63;
+    int e = -1;
+    for (int e0 = 0; e0 < ne; e0 += 64) {   // wave-uniform
+        const int ee = e0 + lane;
+        const uint64_t has = __ballot(ee < ne && offsets[ee + 1] > offsets[ee]);
+        const int cnt = __popcll(has);
+        if (slot < cnt) {
+            uint64_t m = has;
+            for (int i = 0; i < slot; i++) m &= m - 1;
+            e = e0 + __ffsll((unsigned long long)m) - 1;
+            break;
+        }
+        slot -= cnt;
+    }
+    if (e < 0) return;
+    const int r0 = offsets[e], c = offsets[e + 1] - r0;
+    const uint8_t* W = wt.w[mat * ne + e];
+    for (int j0 = 0; j0 < c; j0 += NXP) {
+        const uint8_t* xq = X + (size_t)(r0 + j0) * xrb;
+        float* y = Y + (size_t)mat * ymat + (size_t)(r0 + j0) * n_rows;
+        gemv_multi_body<F, R, WAVES, NXP>(W, row_bytes, xq, xrb, y, n_rows, k, c - j0 < NXP ? c - j0 : NXP);
     }
 }
 
@@ -294,6 +346,57 @@ hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t
     case 3: return launch_q8_multi<FmtQ4K, 2, 4, 3>(w, rb, x, xrb, y, n, kk, s);
     default: return launch_q8_multi<FmtQ4K, 2, 4, 4>(w, rb, x, xrb, y, n, kk, s);
     }
+}
+
+template <class F, int R, int WAVES, int NXP>
+static hipError_t launch_moe_gemv_t(const MoeGemvWeights& wt, const int32_t* offsets, int ne, int nm, int slots,
+                                    const uint8_t* x, size_t xrb, float* y, size_t ymat, size_t rb, int n, int k,
+                                    hipStream_t s) {
+    const unsigned gx = (unsigned)((n + R * WAVES - 1) / (R * WAVES));
+    hipLaunchKernelGGL((moe_gemv_kernel<F, R, WAVES, NXP>), dim3(gx, (unsigned)(slots * nm)), dim3(WAVES * 64), 0, s,
+                       wt, offsets, ne, slots, x, xrb, y, ymat, rb, n, k);
+    return hipGetLastError();
+}
+
+template <class F, int R, int WAVES>
+static hipError_t launch_moe_gemv(const MoeGemvWeights& wt, const int32_t* offsets, int ne, int nm, int slots, int nxp,
+                                  const uint8_t* x, size_t xrb, float* y, size_t ymat, size_t rb, int n, int k,
+                                  hipStream_t s) {
+    switch (nxp) {
+    case 1: return launch_moe_gemv_t<F, R, WAVES, 1>(wt, offsets, ne, nm, slots, x, xrb, y, ymat, rb, n, k, s);
+    case 2: return launch_moe_gemv_t<F, R, WAVES, 2>(wt, offsets, ne, nm, slots, x, xrb, y, ymat, rb, n, k, s);
+    case 3: return launch_moe_gemv_t<F, R, WAVES, 3>(wt, offsets, ne, nm, slots, x, xrb, y, ymat, rb, n, k, s);
+    default: return launch_moe_gemv_t<F, R, WAVES, 4>(wt, offsets, ne, nm, slots, x, xrb, y, ymat, rb, n, k, s);
+    }
+}
+
+// BARQ_MOE_GEMV: 1 (default) single-token MoE steps take the grouped GEMVs,
+// 2 any step of at most 4 assignments, 0 none
+int moe_gemv_enabled() { return tuning_env("BARQ_MOE_GEMV", 1); }
+
+bool moe_gemv_supported(int w_type, size_t n_experts, size_t n_mats, size_t n_rows, size_t k) {
+    return (w_type == TYPE_Q4_K || w_type == TYPE_Q6_K) && k % 256 == 0 && k > 0 && n_experts > 0 && n_mats > 0 &&
+           n_experts * n_mats <= (size_t)MOE_GEMV_MAXE && n_rows > 0 && n_rows <= (size_t)INT32_MAX &&
+           k <= (size_t)INT32_MAX;
+}
+
+hipError_t moe_gemv_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
+                           size_t n_assign, size_t tokens, const void* xq, size_t n_rows, size_t k, float* y,
+                           size_t y_mat_stride, hipStream_t s) {
+    if (!moe_gemv_supported(w_type, n_experts, n_mats, n_rows, k) || n_assign == 0 || tokens == 0)
+        return hipErrorInvalidValue;
+    const int slots = (int)(n_assign < n_experts ? n_assign : n_experts);
+    const int nxp = (int)(tokens < 4 ? tokens : 4);
+    MoeGemvWeights wt = {};
+    for (size_t i = 0; i < n_experts * n_mats; i++) wt.w[i] = static_cast<const uint8_t*>(W[i]);
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+    const size_t xrb = k / 256 * 292;
+    const int ne = (int)n_experts, nm = (int)n_mats, n = (int)n_rows, kk = (int)k;
+    if (w_type == TYPE_Q4_K)
+        return launch_moe_gemv<FmtQ4K, 2, 4>(wt, offsets, ne, nm, slots, nxp, x, xrb, y, y_mat_stride, k / 256 * 144, n,
+                                             kk, s);
+    return launch_moe_gemv<FmtQ6K, 1, 8>(wt, offsets, ne, nm, slots, nxp, x, xrb, y, y_mat_stride, k / 256 * 210, n,
+                                         kk, s);
 }
 
 // Formats that take the LDS-streaming GEMV (gemv_dma.hip) when its layout

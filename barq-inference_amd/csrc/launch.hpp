@@ -38,6 +38,15 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
                           float* y, hipStream_t s);
 hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
                            float* y, hipStream_t s);
+// Expert-grouped GEMV for decode-size MoE steps (Q4_K or Q6_K weights
+// W[mat * n_experts + e], grouped Q8_K rows, row ranges from the device
+// offsets; y rows of y + mat * y_mat_stride in grouped order)
+constexpr int MOE_GEMV_MAXE = 64;
+bool moe_gemv_supported(int w_type, size_t n_experts, size_t n_mats, size_t n_rows, size_t k);
+int moe_gemv_enabled();   // BARQ_MOE_GEMV (0: off, 1: one-token steps, 2: up to 4 assignments)
+hipError_t moe_gemv_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
+                           size_t n_assign, size_t tokens, const void* xq, size_t n_rows, size_t k, float* y,
+                           size_t y_mat_stride, hipStream_t s);
 // 2-4 Q8 activation rows at once (y[m x n_rows]): the weights read once
 bool gemv_multi_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m);
 hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,

@@ -317,6 +317,12 @@ MOE_CASES = {
     # grouping fused with the gather-quantize over several 256-assignment
     # chunks (with skipped ids)
     "many_chunks": dict(ne=6, hid=256, nff=256, rows=700, k=2),
+    # decode-size steps (at most 4 assignments): expert-grouped GEMVs
+    "decode_1": dict(ne=8, hid=512, nff=1024, rows=1, k=2),
+    "decode_1_repeat": dict(ne=4, hid=256, nff=512, rows=1, k=2),
+    "decode_2_repeat": dict(ne=4, hid=256, nff=512, rows=2, k=2),
+    "decode_top1": dict(ne=3, hid=512, nff=512, rows=4, k=1),
+    "decode_mixed": dict(ne=3, hid=512, nff=512, rows=2, k=2, gt=B.Q6_K, ut=B.Q4_K),
 }
 
 
@@ -336,10 +342,27 @@ def test_moe_ffn_grouped_cases(be, orc, name):
     if name == "many_chunks":
         ids[::37, 1] = -1       # skipped ids spread over the chunks
         ids[300, :] = [5, 5]
+    if name == "decode_1_repeat":
+        ids[:] = [[2, 2]]           # one token, the same expert twice: two passes
+    if name == "decode_2_repeat":
+        ids[:] = [[3, 3], [3, 1]]   # three rows on one expert
+    if name == "decode_top1":
+        ids[:, 0] = 1               # four rows on one expert
     out = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs], hid, nff,
                      dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
     ref = orc.moe_ffn(gt, gates, ut, ups, dt, downs, hid, nff, x, ids, w, orc.Q8_K)
     assert_close_1e3(host(out), ref)
+    if name.startswith("decode"):
+        # the same step on the grouped MFMA GEMM (0) and on the grouped GEMVs
+        # (2: also for more than one token, several rows per expert)
+        for mode in ("0", "2"):
+            os.environ["BARQ_MOE_GEMV"] = mode
+            try:
+                out2 = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs],
+                                  hid, nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
+            finally:
+                os.environ.pop("BARQ_MOE_GEMV", None)
+            assert_close_1e3(host(out2), ref)
     if name == "many_chunks":
         # grouping in its own launch (the path above 2048 assignments, or with
         # BARQ_MOE_FUSED_GROUP=0) gives the same rows in the same order
