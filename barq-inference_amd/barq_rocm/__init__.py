@@ -7,13 +7,15 @@ torch-allocated device buffers (backend) and the deterministic synthetic
 inputs of the benchmark configurations (synth).
 """
 from . import _lib
-from ._lib import (ACT_F32, ACT_F32_Q8, BLOCK_BYTES, BLOCK_ELEMS, F16, F32, MEM_DEVICE, MEM_HOST, Q4_0,
-                   Q4_0_BARQ, Q4_K, Q4_K_BARQ, Q6_K, Q8_0, Q8_K, Q8_PARTNER, BarqError)
+from ._lib import (ACT_F32, ACT_F32_Q8, BLOCK_BYTES, BLOCK_ELEMS, E_BACKEND, E_DIM, E_INVALID, E_QUANT,
+                   E_UNSUPPORTED, F16, F32, MEM_DEVICE, MEM_HOST, Q4_0, Q4_0_BARQ, Q4_K,
+                   Q4_K_BARQ, Q6_K, Q8_0, Q8_K, Q8_PARTNER, BarqError)
 from .backend import Backend
 
 __all__ = [
     "_lib", "Backend", "BarqError", "ACT_F32", "ACT_F32_Q8", "BLOCK_BYTES", "BLOCK_ELEMS", "F16", "F32",
     "MEM_DEVICE", "MEM_HOST", "Q4_0", "Q4_0_BARQ", "Q4_K", "Q4_K_BARQ", "Q6_K", "Q8_0", "Q8_K", "Q8_PARTNER",
+    "E_BACKEND", "E_DIM", "E_INVALID", "E_QUANT", "E_UNSUPPORTED",
 ]
 
 

@@ -56,7 +56,7 @@ EXPORTS = (
     "barq_rocm_matvec", "barq_rocm_matmul",
     "barq_rocm_gemm_f32", "barq_rocm_gemv_f32", "barq_rocm_dequantize_split",
     "barq_rocm_quantized_matmul_split", "barq_rocm_quantize_q4_0_barq", "barq_rocm_quantize_q4_k_barq",
-    "barq_rocm_q4_k_barq_bytes", "barq_rocm_moe_route",
+    "barq_rocm_q4_k_barq_bytes", "barq_rocm_moe_route", "barq_rocm_moe_reduce", "barq_rocm_moe_route_reduce",
     "barq_rocm_moe_ffn", "barq_rocm_gguf_open", "barq_rocm_gguf_close", "barq_rocm_gguf_info",
     "barq_rocm_gguf_tensor", "barq_rocm_gguf_find_tensor", "barq_rocm_gguf_kv_type", "barq_rocm_gguf_kv_int",
     "barq_rocm_gguf_kv_number", "barq_rocm_gguf_kv_string", "barq_rocm_cache_create", "barq_rocm_cache_get",
@@ -111,6 +111,8 @@ def _declare(lib):
         "barq_rocm_quantize_q4_k_barq": (_i, [_vp, _vp, _sz, _vp, _i]),
         "barq_rocm_q4_k_barq_bytes": (_sz, [_sz]),
         "barq_rocm_moe_route": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _i]),
+        "barq_rocm_moe_reduce": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, ctypes.c_float, _vp, _vp, _i]),
+        "barq_rocm_moe_route_reduce": (_i, [_vp, _vp, _sz, _sz, _sz, _sz, ctypes.c_float, _vp, _vp, _i]),
         "barq_rocm_moe_ffn": (_i, [_vp, _sz, _i, _vp, _i, _vp, _i, _vp, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp, _i]),
         "barq_rocm_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
         "barq_rocm_gguf_close": (_i, [_vp]),

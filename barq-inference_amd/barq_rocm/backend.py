@@ -223,6 +223,40 @@ class Backend:
             self.sync()
         return ids, w
 
+    def moe_route_reduce(self, logits, rows, n_experts, top_k, max_active, min_weight, mem=L.MEM_DEVICE):
+        """Top-k routing followed by reduce_expert_assignments in one launch."""
+        k = max(1, min(top_k, n_experts))
+        if mem == L.MEM_HOST:
+            ids = np.empty((rows, k), dtype=np.int32)
+            w = np.empty((rows, k), dtype=np.float32)
+        else:
+            import torch
+            ids = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+            w = torch.empty((rows, k), dtype=torch.float32, device=logits.device)
+        L.check(self._lib.barq_rocm_moe_route_reduce(self.h, _ptr(logits), rows, n_experts, top_k, max_active,
+                                                     min_weight, _ptr(ids), _ptr(w), mem))
+        if mem == L.MEM_DEVICE:
+            self.sync()
+        return ids, w
+
+    def moe_reduce(self, ids, weights, max_active, min_weight, mem=L.MEM_DEVICE, out=None):
+        """reduce_expert_assignments on rows x k slots; out=(ids, weights) may be the inputs."""
+        rows, k = tuple(ids.shape)
+        if out is not None:
+            oi, ow = out
+        elif mem == L.MEM_HOST:
+            oi = np.empty((rows, k), dtype=np.int32)
+            ow = np.empty((rows, k), dtype=np.float32)
+        else:
+            import torch
+            oi = torch.empty((rows, k), dtype=torch.int32, device=ids.device)
+            ow = torch.empty((rows, k), dtype=torch.float32, device=ids.device)
+        L.check(self._lib.barq_rocm_moe_reduce(self.h, _ptr(ids), _ptr(weights), rows, k, max_active, min_weight,
+                                               _ptr(oi), _ptr(ow), mem))
+        if mem == L.MEM_DEVICE:
+            self.sync()
+        return oi, ow
+
     def moe_ffn(self, gate_type, gates, up_type, ups, down_type, downs, hidden, n_ff, x, rows, ids, weights,
                 top_k, act, mem=L.MEM_DEVICE, sync=True, out=None):
         ne = len(gates)

@@ -85,18 +85,21 @@ size_t weight_align(int t) {
 
 int barq_api::ensure_ws(barq_rocm_handle* h, size_t bytes) {
     if (bytes <= h->ws_size) return ok();
-    if (h->ws) {
-        BARQ_HIP(hipStreamSynchronize(h->stream));
-        BARQ_HIP(hipFree(h->ws));
-        h->ws = nullptr;
-        h->ws_size = 0;
-    }
+    // At least double, so the retired buffers together stay smaller than the
+    // live one.  The old buffer is not freed here: kernels still running on
+    // any stream, and HIP graphs captured earlier, may reference it.
     size_t want = bytes < 16 * 1024 * 1024 ? 16 * 1024 * 1024 : bytes;
-    hipError_t e = hipMalloc(&h->ws, want);
-    if (e != hipSuccess) {
-        h->ws = nullptr;
-        return fail(BARQ_E_ALLOC, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
+    if (want < 2 * h->ws_size) want = 2 * h->ws_size;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess && want > bytes) {
+        (void)hipGetLastError();
+        want = bytes;
+        e = hipMalloc(&p, want);
     }
+    if (e != hipSuccess) return fail(BARQ_E_ALLOC, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
+    if (h->ws) h->retired.push_back(h->ws);
+    h->ws = p;
     h->ws_size = want;
     return ok();
 }
@@ -135,10 +138,15 @@ int barq_rocm_create(int device, barq_rocm_handle** out) {
     if (hipSetDevice(device) != hipSuccess) return fail(BARQ_E_BACKEND, "hipSetDevice(%d) failed", device);
     auto* h = new barq_rocm_handle();
     h->device = device;
+    h->tuning = barq::Tuning::from_env();
     e = hipStreamCreateWithFlags(&h->own, hipStreamNonBlocking);
+    if (e == hipSuccess) {
+        e = hipEventCreateWithFlags(&h->switch_ev, hipEventDisableTiming);
+        if (e != hipSuccess) (void)hipStreamDestroy(h->own);
+    }
     if (e != hipSuccess) {
         delete h;
-        return fail(BARQ_E_BACKEND, "hipStreamCreate: %s", hipGetErrorString(e));
+        return fail(BARQ_E_BACKEND, "stream/event creation: %s", hipGetErrorString(e));
     }
     h->stream = h->own;
     *out = h;
@@ -147,9 +155,12 @@ int barq_rocm_create(int device, barq_rocm_handle** out) {
 
 int barq_rocm_destroy(barq_rocm_handle* h) {
     if (!h) return ok();
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->own && h->own != h->stream) (void)hipStreamSynchronize(h->own);
     if (h->ws) (void)hipFree(h->ws);
+    for (void* p : h->retired) (void)hipFree(p);
+    if (h->switch_ev) (void)hipEventDestroy(h->switch_ev);
     if (h->own) (void)hipStreamDestroy(h->own);
     delete h;
     return ok();
@@ -157,7 +168,14 @@ int barq_rocm_destroy(barq_rocm_handle* h) {
 
 int barq_rocm_set_stream(barq_rocm_handle* h, void* stream) {
     BARQ_CHECK(check_handle(h));
-    h->stream = stream ? static_cast<hipStream_t>(stream) : h->own;
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : h->own;
+    if (next == h->stream) return ok();
+    // Work already enqueued on the old stream (which may still use the
+    // workspace) completes before anything enqueued on the new one starts.
+    DeviceGuard g(h);
+    BARQ_HIP(hipEventRecord(h->switch_ev, h->stream));
+    BARQ_HIP(hipStreamWaitEvent(next, h->switch_ev, 0));
+    h->stream = next;
     return ok();
 }
 
@@ -165,7 +183,7 @@ void* barq_rocm_get_stream(barq_rocm_handle* h) { return h ? static_cast<void*>(
 
 int barq_rocm_synchronize(barq_rocm_handle* h) {
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     BARQ_HIP(hipStreamSynchronize(h->stream));
     return ok();
 }
@@ -179,7 +197,7 @@ int barq_rocm_dequantize(barq_rocm_handle* h, int type, const void* blocks, size
     if (n_elems == 0) return ok();
     if (!blocks || !out) return fail(BARQ_E_INVALID, "dequantize: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t in_bytes = n_elems / be * blk_bytes(type);
     if (mem == BARQ_MEM_DEVICE) {
         if (!aligned(blocks, type == BARQ_TYPE_F16 ? 8 : weight_align(type)) || !aligned(out, 16))
@@ -210,7 +228,7 @@ int barq_rocm_quantize_act(barq_rocm_handle* h, int act_type, const float* x, si
     if (n_rows == 0 || k == 0) return ok();
     if (!x || !out) return fail(BARQ_E_INVALID, "quantize_act: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t out_bytes = n_rows * row_bytes_of(act_type, k);
     if (mem == BARQ_MEM_DEVICE) {
         if (!aligned(x, 16) || !aligned(out, act_type == BARQ_TYPE_Q8_K ? 4 : 2))
@@ -237,7 +255,7 @@ int barq_rocm_rms_norm(barq_rocm_handle* h, const float* x, const float* weight,
     if (!barq::rms_norm_supported(n)) return fail(BARQ_E_DIM, "rms_norm: n=%zu must be a multiple of 4 and at most 16384", n);
     if (!x || !weight || !y) return fail(BARQ_E_INVALID, "rms_norm: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     if (mem == BARQ_MEM_DEVICE) {
         if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(y, 16))
             return fail(BARQ_E_INVALID, "rms_norm: buffers must be 16-byte aligned");
@@ -265,7 +283,7 @@ int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* 
         return fail(BARQ_E_DIM, "rms_norm_quantize: n=%zu must be a multiple of 256 and at most 16384", n);
     if (!x || !weight || !out) return fail(BARQ_E_INVALID, "rms_norm_quantize: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t out_bytes = rows * row_bytes_of(act_type, n);
     if (mem == BARQ_MEM_DEVICE) {
         if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, act_type == BARQ_TYPE_Q8_K ? 4 : 2))
@@ -319,14 +337,17 @@ size_t matmul_scratch(int w_type, size_t n_rows, size_t k, int act_type, size_t 
     return q;
 }
 
-// Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).  With
-// use_ws false the call leaves the workspace alone (its caller keeps data
-// there): Q8 activations only, no 32-element-block GEMM, no K slices.
+// Device-pointer matmul core.  x holds m rows (f32 or Q8 blocks).  ws is
+// scratch of at least matmul_scratch(...) bytes, or null: then the call
+// takes quantized activations only and uses no scratch (no
+// 32-element-block GEMM, no K slices; the MoE path keeps its data in the
+// workspace meanwhile).
 int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
-               const void* x, size_t m, float* y, bool use_ws = true) {
+               const void* x, size_t m, float* y, uint8_t* ws) {
     hipStream_t s = h->stream;
-    if (!use_ws && (act_type == BARQ_ACT_F32 || act_type == BARQ_ACT_F32_Q8))
-        return fail(BARQ_E_INVALID, "matmul without workspace takes quantized activations");
+    const bool use_ws = ws != nullptr;
+    if (!use_ws && (act_type == BARQ_ACT_F32_Q8 || (act_type == BARQ_ACT_F32 && m > 1)))
+        return fail(BARQ_E_INVALID, "matmul without workspace takes quantized activations (or one f32 row)");
     if (!aligned(w, weight_align(w_type))) return fail(BARQ_E_INVALID, "weights must be %zu-byte aligned", weight_align(w_type));
     if (!aligned(y, 4)) return fail(BARQ_E_INVALID, "output must be 4-byte aligned");
     if (act_type == BARQ_ACT_F32) {
@@ -336,62 +357,91 @@ int matmul_dev(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, si
             return launched(barq::gemv_f32_launch(w_type, w, n_rows, k, static_cast<const float*>(x), y, s), "gemv_f32");
         }
         // literal matmul: dequantize W (bit-exact) then the sequential f32 GEMM
-        BARQ_CHECK(ensure_ws(h, n_rows * k * 4));
-        float* wf = at<float>(h, 0);
+        float* wf = reinterpret_cast<float*>(ws);
         BARQ_CHECK(launched(barq::dequant_launch(w_type, w, n_rows * k, wf, s), "dequantize"));
         return launched(barq::gemm_f32_nt_launch(static_cast<const float*>(x), wf, m, k, n_rows, y, s), "gemm_f32_nt");
     }
     const int aq = q8_partner(w_type);
     const uint8_t* xq = static_cast<const uint8_t*>(x);
-    // workspace: the quantized rows (when quantized here), then the repacked
-    // rows of the 32-element-block GEMM
+    // scratch: the quantized rows (when quantized here), then the repacked
+    // rows of the 32-element-block GEMM or the K slices' partial products
     // the MFMA GEMMs copy weight rows with 4-byte buffer->LDS loads
     const bool w4 = aligned(w, 4);
     const bool gemm = m >= (size_t)barq::gemm_min_rows(w_type);
     const bool b32 = use_ws && gemm && w4 && barq::b32_supported(w_type, n_rows, k, m);
     const size_t qbytes = act_type == BARQ_ACT_F32_Q8 ? round_up(m * row_bytes_of(aq, k), 256) : 0;
-    if (use_ws)
-        if (const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m)) BARQ_CHECK(ensure_ws(h, need));
     if (act_type == BARQ_ACT_F32_Q8) {
         if (!aligned(x, 16)) return fail(BARQ_E_INVALID, "f32 activations must be 16-byte aligned");
-        BARQ_CHECK(launched(quantize_act_dev(aq, static_cast<const float*>(x), m, k, h->ws, s), "quantize_act"));
-        xq = static_cast<const uint8_t*>(h->ws);
+        BARQ_CHECK(launched(quantize_act_dev(aq, static_cast<const float*>(x), m, k, ws, s), "quantize_act"));
+        xq = ws;
     } else if (!aligned(x, aq == BARQ_TYPE_Q8_K ? 4 : 2)) {
         return fail(BARQ_E_INVALID, "activation blocks misaligned");
     }
     if (barq::gemv_multi_supported(w_type, w, n_rows, k, xq, m))
         return launched(barq::gemv_q8_multi_launch(w_type, w, n_rows, k, xq, m, y, s), "gemv_q8_multi");
-    if (b32) return launched(barq::b32_gemm_launch(w_type, w, n_rows, k, xq, m, at<uint8_t>(h, qbytes), y, s), "gemm_b32");
+    if (b32) return launched(barq::b32_gemm_launch(w_type, w, n_rows, k, xq, m, ws + qbytes, y, s), "gemm_b32");
     if (gemm && w4 && barq::gemm_mfma_supported(w_type, n_rows, k, m))
-        return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, use_ws ? at<uint8_t>(h, qbytes) : nullptr,
-                                                   y, s), "gemm_mfma");
+        return launched(barq::gemm_q8k_mfma_launch(w_type, w, n_rows, k, xq, m, use_ws ? ws + qbytes : nullptr, y, s),
+                        "gemm_mfma");
     const size_t xrb = row_bytes_of(aq, k);
     for (size_t r = 0; r < m; r++)
         BARQ_CHECK(launched(barq::gemv_q8_launch(w_type, w, n_rows, k, xq + r * xrb, y + r * n_rows, s), "gemv_q8"));
     return ok();
 }
 
-int matmul_any(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
-               const void* x, size_t m, float* y, int mem, const char* what) {
-    BARQ_CHECK(check_mem(mem));
+int check_matmul_args(int w_type, size_t n_rows, size_t k, int act_type, const void* w, const void* x, size_t m,
+                      const float* y, const char* what) {
     BARQ_CHECK(check_linear(w_type, k, act_type, what));
     if (n_rows == 0 || m == 0) return ok();
     if (!w || !x || !y) return fail(BARQ_E_INVALID, "%s: null buffer", what);
     if (n_rows > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "%s: dimensions exceed 2^31", what);
+    return ok();
+}
+
+}  // namespace
+}  // extern "C"
+
+int barq_api::matmul_fixed_scratch(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k,
+                                   int act_type, const void* x, size_t m, float* y, void* ws, size_t ws_bytes,
+                                   const char* what) {
+    BARQ_CHECK(check_matmul_args(w_type, n_rows, k, act_type, w, x, m, y, what));
+    if (n_rows == 0 || m == 0) return ok();
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
-    if (mem == BARQ_MEM_DEVICE) return matmul_dev(h, w_type, w, n_rows, k, act_type, x, m, y);
+    DeviceGuard g(h);
+    const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m);
+    if (need > ws_bytes)
+        return fail(BARQ_E_UNSUPPORTED, "%s: this call needs %zu bytes of scratch, more than the %zu available", what,
+                    need, ws_bytes);
+    return matmul_dev(h, w_type, w, n_rows, k, act_type, x, m, y, need ? static_cast<uint8_t*>(ws) : nullptr);
+}
+
+extern "C" {
+namespace {
+
+int matmul_any(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
+               const void* x, size_t m, float* y, int mem, const char* what) {
+    BARQ_CHECK(check_mem(mem));
+    BARQ_CHECK(check_matmul_args(w_type, n_rows, k, act_type, w, x, m, y, what));
+    if (n_rows == 0 || m == 0) return ok();
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    const size_t need = matmul_scratch(w_type, n_rows, k, act_type, m);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (need) BARQ_CHECK(ensure_ws(h, need));
+        return matmul_dev(h, w_type, w, n_rows, k, act_type, x, m, y, need ? at<uint8_t>(h, 0) : nullptr);
+    }
     // host buffers: stage W, x, y after the region matmul_dev itself may use
     const size_t wbytes = n_rows * row_bytes_of(w_type, k);
     const size_t xbytes = m * act_row_bytes(act_type, w_type, k);
     const size_t ybytes = m * n_rows * 4;
     Arena a;
-    a.add(matmul_scratch(w_type, n_rows, k, act_type, m));
+    a.add(need);
     size_t ow = a.add(wbytes), ox = a.add(xbytes), oy = a.add(ybytes);
     BARQ_CHECK(ensure_ws(h, a.used));
     BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ow), w, wbytes, hipMemcpyHostToDevice, h->stream));
     BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ox), x, xbytes, hipMemcpyHostToDevice, h->stream));
-    BARQ_CHECK(matmul_dev(h, w_type, at<uint8_t>(h, ow), n_rows, k, act_type, at<uint8_t>(h, ox), m, at<float>(h, oy)));
+    BARQ_CHECK(matmul_dev(h, w_type, at<uint8_t>(h, ow), n_rows, k, act_type, at<uint8_t>(h, ox), m, at<float>(h, oy),
+                          need ? at<uint8_t>(h, 0) : nullptr));
     BARQ_HIP(hipMemcpyAsync(y, at<float>(h, oy), ybytes, hipMemcpyDeviceToHost, h->stream));
     BARQ_HIP(hipStreamSynchronize(h->stream));
     return ok();
@@ -418,7 +468,7 @@ int barq_rocm_gemm_f32(barq_rocm_handle* h, const float* a, const float* b, size
     if (!a || !b || !c) return fail(BARQ_E_INVALID, "gemm_f32: null buffer");
     if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "gemm_f32: dimensions exceed 2^31");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     if (mem == BARQ_MEM_DEVICE) return launched(barq::gemm_f32_launch(a, b, m, k, n, c, h->stream), "gemm_f32");
     Arena ar;
     size_t oa = ar.add(m * k * 4), ob = ar.add(k * n * 4), oc = ar.add(m * n * 4);
@@ -437,7 +487,7 @@ int barq_rocm_gemv_f32(barq_rocm_handle* h, const float* a, const float* x, size
     if (!a || !x || !y) return fail(BARQ_E_INVALID, "gemv_f32: null buffer");
     if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "gemv_f32: dimensions exceed 2^31");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     if (mem == BARQ_MEM_DEVICE) return launched(barq::gemv_f32_plain_launch(a, x, m, n, y, h->stream), "gemv_f32");
     Arena ar;
     size_t oa = ar.add(m * n * 4), ox = ar.add(n * 4), oy = ar.add(m * 4);
@@ -461,7 +511,7 @@ int barq_rocm_dequantize_split(barq_rocm_handle* h, int kind, const uint8_t* qua
     if (n_out == 0) return ok();
     if (!out || (n_quants && !quants) || (n_scales && !scales)) return fail(BARQ_E_INVALID, "dequantize_split: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const int q8 = kind == BARQ_TYPE_Q8_0;
     if (mem == BARQ_MEM_DEVICE)
         return launched(barq::dequant_split_launch(q8, quants, n_quants, scales, n_scales, block_size, out, n_out, h->stream), "dequantize_split");
@@ -486,7 +536,7 @@ int barq_rocm_quantized_matmul_split(barq_rocm_handle* h, const float* a, const 
     if (!a || !c || (n_bq && !bq) || (n_bs && !bs)) return fail(BARQ_E_INVALID, "quantized_matmul: null buffer");
     if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX || k > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "quantized_matmul: dimensions exceed 2^31");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const int q8 = kind == BARQ_TYPE_Q8_0;
     Arena ar;
     size_t ob = ar.add(k * n * 4);
@@ -521,7 +571,7 @@ int barq_rocm_quantize_q4_0_barq(barq_rocm_handle* h, const float* x, size_t n, 
     if (n == 0) return ok();
     if (!x || !out) return fail(BARQ_E_INVALID, "quantize_q4_0_barq: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t ob_bytes = n / 32 * 20;
     if (mem == BARQ_MEM_DEVICE) {
         if (!aligned(out, 4)) return fail(BARQ_E_INVALID, "quantize_q4_0_barq: out must be 4-byte aligned");
@@ -542,7 +592,7 @@ int barq_rocm_quantize_q4_k_barq(barq_rocm_handle* h, const float* x, size_t n, 
     if (n == 0) return ok();
     if (!x || !out) return fail(BARQ_E_INVALID, "quantize_q4_k_barq: null buffer");
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t ob_bytes = barq_rocm_q4_k_barq_bytes(n);
     if (mem == BARQ_MEM_DEVICE) {
         if (!aligned(out, 4)) return fail(BARQ_E_INVALID, "quantize_q4_k_barq: out must be 4-byte aligned");
@@ -564,26 +614,73 @@ size_t barq_rocm_q4_k_barq_bytes(size_t n) { return n / 256 * 136 + (n % 256 ? 8
 // ---------------------------------------------------------------------------
 // MoE
 
-int barq_rocm_moe_route(barq_rocm_handle* h, const float* logits, size_t rows, size_t n_experts, size_t top_k,
-                        int32_t* ids, float* weights, int mem) {
+namespace {
+
+int moe_route_any(barq_rocm_handle* h, const float* logits, size_t rows, size_t n_experts, size_t top_k,
+                  size_t max_active, float min_weight, int32_t* ids, float* weights, int mem, const char* what) {
     BARQ_CHECK(check_mem(mem));
     if (n_experts == 0) return fail(BARQ_E_INVALID, "Routing logits must contain at least one expert");
-    if (n_experts > 256) return fail(BARQ_E_UNSUPPORTED, "moe_route: at most 256 experts");
+    if (n_experts > 256) return fail(BARQ_E_UNSUPPORTED, "%s: at most 256 experts", what);
     size_t k = top_k < 1 ? 1 : (top_k > n_experts ? n_experts : top_k);
-    if (k > 64) return fail(BARQ_E_UNSUPPORTED, "moe_route: top_k at most 64");
+    if (k > 64) return fail(BARQ_E_UNSUPPORTED, "%s: top_k at most 64", what);
     if (rows == 0) return ok();
-    if (!logits || !ids || !weights) return fail(BARQ_E_INVALID, "moe_route: null buffer");
+    if (rows > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "%s: rows exceed 2^31", what);
+    if (!logits || !ids || !weights) return fail(BARQ_E_INVALID, "%s: null buffer", what);
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     if (mem == BARQ_MEM_DEVICE)
-        return launched(barq::moe_route_launch(logits, rows, n_experts, k, ids, weights, h->stream), "moe_route");
+        return launched(barq::moe_route_launch(logits, rows, n_experts, k, ids, weights, h->stream, max_active,
+                                               min_weight), what);
     Arena a;
     size_t ol = a.add(rows * n_experts * 4), oi = a.add(rows * k * 4), ow = a.add(rows * k * 4);
     BARQ_CHECK(ensure_ws(h, a.used));
     BARQ_HIP(hipMemcpyAsync(at<float>(h, ol), logits, rows * n_experts * 4, hipMemcpyHostToDevice, h->stream));
-    BARQ_CHECK(launched(barq::moe_route_launch(at<float>(h, ol), rows, n_experts, k, at<int32_t>(h, oi), at<float>(h, ow), h->stream), "moe_route"));
+    BARQ_CHECK(launched(barq::moe_route_launch(at<float>(h, ol), rows, n_experts, k, at<int32_t>(h, oi),
+                                               at<float>(h, ow), h->stream, max_active, min_weight), what));
     BARQ_HIP(hipMemcpyAsync(ids, at<int32_t>(h, oi), rows * k * 4, hipMemcpyDeviceToHost, h->stream));
     BARQ_HIP(hipMemcpyAsync(weights, at<float>(h, ow), rows * k * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+}  // namespace
+
+int barq_rocm_moe_route(barq_rocm_handle* h, const float* logits, size_t rows, size_t n_experts, size_t top_k,
+                        int32_t* ids, float* weights, int mem) {
+    return moe_route_any(h, logits, rows, n_experts, top_k, 0, 0.0f, ids, weights, mem, "moe_route");
+}
+
+int barq_rocm_moe_route_reduce(barq_rocm_handle* h, const float* logits, size_t rows, size_t n_experts,
+                               size_t top_k, size_t max_active, float min_weight, int32_t* ids, float* weights,
+                               int mem) {
+    return moe_route_any(h, logits, rows, n_experts, top_k, max_active > 0 ? max_active : 1, min_weight, ids, weights,
+                         mem, "moe_route_reduce");
+}
+
+int barq_rocm_moe_reduce(barq_rocm_handle* h, const int32_t* ids, const float* weights, size_t rows, size_t top_k,
+                         size_t max_active, float min_weight, int32_t* out_ids, float* out_weights, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (top_k == 0) return fail(BARQ_E_INVALID, "moe_reduce: top_k must be > 0");
+    if (top_k > 64) return fail(BARQ_E_UNSUPPORTED, "moe_reduce: top_k at most 64");
+    if (rows == 0) return ok();
+    if (rows > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "moe_reduce: rows exceed 2^31");
+    if (!ids || !weights || !out_ids || !out_weights) return fail(BARQ_E_INVALID, "moe_reduce: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    if (mem == BARQ_MEM_DEVICE)
+        return launched(barq::moe_reduce_launch(ids, weights, rows, top_k, max_active, min_weight, out_ids, out_weights,
+                                                h->stream), "moe_reduce");
+    const size_t nb = rows * top_k * 4;
+    Arena a;
+    size_t oi = a.add(nb), ow = a.add(nb);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<int32_t>(h, oi), ids, nb, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ow), weights, nb, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::moe_reduce_launch(at<int32_t>(h, oi), at<float>(h, ow), rows, top_k, max_active,
+                                                min_weight, at<int32_t>(h, oi), at<float>(h, ow), h->stream),
+                        "moe_reduce"));
+    BARQ_HIP(hipMemcpyAsync(out_ids, at<int32_t>(h, oi), nb, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipMemcpyAsync(out_weights, at<float>(h, ow), nb, hipMemcpyDeviceToHost, h->stream));
     BARQ_HIP(hipStreamSynchronize(h->stream));
     return ok();
 }
@@ -743,8 +840,8 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
         if (!c) continue;
         if (q8) {
             // the arena holds this call's data from offset `base`: no workspace
-            BARQ_CHECK(matmul_dev(h, gt, gate[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, gb + r0 * n_ff, false));
-            BARQ_CHECK(matmul_dev(h, ut, up[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, ub + r0 * n_ff, false));
+            BARQ_CHECK(matmul_dev(h, gt, gate[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, gb + r0 * n_ff, nullptr));
+            BARQ_CHECK(matmul_dev(h, ut, up[e], n_ff, hidden, in_act, xin + r0 * xq_row, c, ub + r0 * n_ff, nullptr));
         } else {
             float* wf = at<float>(h, o_wf);
             BARQ_CHECK(launched(barq::dequant_launch(gt, gate[e], n_ff * hidden, wf, s), "dequantize"));
@@ -761,7 +858,7 @@ int moe_ffn_dev(barq_rocm_handle* h, size_t ne, int gt, const void* const* gate,
         const size_t r0 = (size_t)off[e], c = (size_t)off[e + 1] - r0;
         if (!c) continue;
         if (q8) {
-            BARQ_CHECK(matmul_dev(h, dt, down[e], hidden, n_ff, in_act, hin + r0 * hq_row, c, yg + r0 * hidden, false));
+            BARQ_CHECK(matmul_dev(h, dt, down[e], hidden, n_ff, in_act, hin + r0 * hq_row, c, yg + r0 * hidden, nullptr));
         } else {
             float* wf = at<float>(h, o_wf);
             BARQ_CHECK(launched(barq::dequant_launch(dt, down[e], hidden * n_ff, wf, s), "dequantize"));
@@ -790,7 +887,7 @@ int barq_rocm_moe_ffn(barq_rocm_handle* h, size_t ne, int gt, const void* const*
     for (size_t e = 0; e < ne; e++)
         if (!gate[e] || !up[e] || !down[e]) return fail(BARQ_E_INVALID, "moe_ffn: null expert weight %zu", e);
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     if (mem == BARQ_MEM_DEVICE) return moe_ffn_dev(h, ne, gt, gate, ut, up, dt, down, hidden, n_ff, x, rows, ids, weights, k, act, out, 0);
     // host buffers: stage everything into the front of the workspace
     const size_t gb = n_ff * row_bytes_of(gt, hidden), ub = n_ff * row_bytes_of(ut, hidden), db = hidden * row_bytes_of(dt, n_ff);

@@ -7,13 +7,21 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
+
+#include "common.hpp"
 
 struct barq_rocm_handle {
     int device = 0;
     hipStream_t own = nullptr;
     hipStream_t stream = nullptr;
-    void* ws = nullptr;        // device workspace, grown on demand
+    hipEvent_t switch_ev = nullptr;   // orders the old stream before the new one in set_stream
+    void* ws = nullptr;               // device workspace, grown on demand
     size_t ws_size = 0;
+    // Workspaces replaced by a larger one: kept until barq_rocm_destroy, since
+    // kernels still in flight or HIP graphs captured earlier may use them.
+    std::vector<void*> retired;
+    barq::Tuning tuning;              // tuning overrides, read at creation
 };
 
 namespace barq_api {
@@ -37,9 +45,15 @@ inline int ok() { return BARQ_OK; }
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Grows the handle's device workspace to at least `bytes` (waiting for the
-// stream before a reallocation).
+// Grows the handle's device workspace to at least `bytes` (at least doubling
+// it; the old buffer is retired, not freed, until the handle is destroyed).
 int ensure_ws(barq_rocm_handle* h, size_t bytes);
+
+// matmul on device buffers with caller-provided scratch of ws_bytes bytes:
+// no workspace growth and no allocation.  Fails with BARQ_E_UNSUPPORTED,
+// before anything is enqueued, when the call needs more scratch than that.
+int matmul_fixed_scratch(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
+                         const void* x, size_t m, float* y, void* ws, size_t ws_bytes, const char* what);
 
 // Carves 256-byte aligned slices out of the workspace.
 struct Arena {
@@ -71,16 +85,20 @@ inline int launched(hipError_t e, const char* what) {
     return ok();
 }
 
-// Make the handle's device current for the duration of a call.
+// Make the handle's device current for the duration of a call (and, given
+// the handle, its tuning snapshot).
 struct DeviceGuard {
     int prev = -1;
     bool changed = false;
-    explicit DeviceGuard(int dev) {
+    barq::TuningScope tune;
+    explicit DeviceGuard(int dev, const barq::Tuning* t = nullptr) : tune(t) {
         if (hipGetDevice(&prev) == hipSuccess && prev != dev) changed = hipSetDevice(dev) == hipSuccess;
     }
+    explicit DeviceGuard(const barq_rocm_handle* h) : DeviceGuard(h->device, &h->tuning) {}
     ~DeviceGuard() {
         if (changed) (void)hipSetDevice(prev);
     }
 };
 
 }  // namespace barq_api
+

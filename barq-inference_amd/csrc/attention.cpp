@@ -56,7 +56,7 @@ int barq_rocm_rope(barq_rocm_handle* h, const float* x, size_t seq_len, size_t n
     if (!x || !inv_freq || !out) return fail(BARQ_E_INVALID, "rope: null buffer");
     BARQ_CHECK(check_int_range(seq_len * n_heads * head_dim, "rope: seq_len*n_heads*head_dim"));
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t n = seq_len * n_heads * head_dim;
     if (mem == BARQ_MEM_DEVICE)
         return launched(barq::rope_launch(layout, x, out, seq_len, n_heads, head_dim, start_pos, freq_scale, inv_freq,
@@ -81,7 +81,7 @@ int barq_rocm_transpose_heads(barq_rocm_handle* h, const float* x, size_t seq_le
     if (!x || !out) return fail(BARQ_E_INVALID, "transpose_heads: null buffer");
     BARQ_CHECK(check_int_range(seq_len * n_heads * head_dim, "transpose_heads: seq_len*n_heads*head_dim"));
     BARQ_CHECK(check_handle(h));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t n = seq_len * n_heads * head_dim;
     if (mem == BARQ_MEM_DEVICE)
         return launched(barq::transpose_heads_launch(x, out, seq_len, n_heads, head_dim, seq_len * head_dim, h->stream),
@@ -110,7 +110,7 @@ int barq_rocm_kv_cache_create(barq_rocm_handle* h, size_t max_size, size_t n_lay
     BARQ_CHECK(check_int_range(max_size, "kv_cache_create: max_size"));
     const size_t elems = n_layers * n_head_kv * max_size * head_dim;
     if (elems / n_layers / n_head_kv / max_size != head_dim) return fail(BARQ_E_DIM, "kv_cache_create: size overflow");
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     auto* c = new barq_rocm_kv_cache();
     c->device = h->device;
     c->max_size = max_size;
@@ -177,7 +177,7 @@ int barq_rocm_kv_cache_append(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t
         return fail(BARQ_E_INVALID, "kv_cache_append: layer %zu holds %zu of %zu positions, %zu more do not fit", layer,
                     c->len[layer], c->max_size, n_tokens);
     if (h->device != c->device) return fail(BARQ_E_INVALID, "kv_cache_append: cache is on another device");
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t row = n_tokens * head_dim * sizeof(float);
     const size_t dst_off = layer * c->layer_stride() + c->len[layer] * head_dim;
     const hipMemcpyKind kind = mem == BARQ_MEM_DEVICE ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
@@ -207,7 +207,7 @@ int barq_rocm_kv_cache_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, s
                     layer, c->len[layer], c->max_size, n_tokens);
     if (h->device != c->device) return fail(BARQ_E_INVALID, "kv_cache_append_rope: cache is on another device");
     BARQ_CHECK(check_int_range(n_tokens * c->n_head_kv * c->head_dim, "kv_cache_append_rope: elements"));
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t hd = c->head_dim, n = n_tokens * c->n_head_kv * hd;
     const size_t dst_off = layer * c->layer_stride() + c->len[layer] * hd;
     const float *kp = k_proj, *vp = v_proj, *fp = inv_freq;
@@ -255,7 +255,7 @@ int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_
     BARQ_CHECK(check_int_range(q_len, "attention: q_len"));
     BARQ_CHECK(check_int_range(start_pos + q_len, "attention: start_pos + q_len"));
     if (q_len > 65535) return fail(BARQ_E_DIM, "attention: q_len %zu above 65535", q_len);
-    DeviceGuard g(h->device);
+    DeviceGuard g(h);
     const size_t nq = n_head * q_len * head_dim;
     const size_t wsp = barq::attention_workspace(n_head, head_dim, q_len, kv_len, n_head_kv);
     Arena a;

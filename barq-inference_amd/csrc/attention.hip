@@ -366,7 +366,7 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
     const size_t g = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
     const size_t groups = (g == 1 || g > 8 || (g & (g - 1))) ? n_head : n_head_kv;
     const size_t wg = groups * (q_len ? q_len : 1);
-    const int wg_override = tuning_env("BARQ_ATTN_WG");   // workgroup-count target (tuning)
+    const int wg_override = tuning_env(TUNE_ATTN_WG);   // workgroup-count target (tuning)
     const size_t target = wg_override > 0 ? (size_t)wg_override : 512;
     size_t ns = (target + wg - 1) / wg;
     size_t max_ns = (kv_len + 63) / 64;

@@ -6,17 +6,68 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <stdlib.h>
 
 namespace barq {
 
 // Launch-shape overrides for tuning sweeps (BARQ_GEMM_*, BARQ_GEMV_*,
-// BARQ_ATTN_*): read at every launch, so one process can compare variants;
-// unset (or 0) keeps the measured default.
-inline int tuning_env(const char* name, int def = 0) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : def;
+// BARQ_MOE_*, BARQ_ATTN_*).  The environment is read once, when a handle is
+// created (Tuning::from_env); every call made through that handle sees the
+// same snapshot, so a launcher and the workspace sizing that precedes it
+// cannot disagree, and no call reads the environment while another thread
+// may be changing it.  Unset keeps the measured default.
+enum Tune : int {
+    TUNE_GEMM_BM, TUNE_GEMM_KG, TUNE_GEMM_NS, TUNE_GEMM_KS, TUNE_GEMM_XCD, TUNE_GEMM_IMPL, TUNE_GEMM_MIN_M,
+    TUNE_GEMV_DMA, TUNE_GEMV_DMA_TYPES, TUNE_GEMV_MULTI_MAX, TUNE_GEMV_CFG_R, TUNE_GEMV_CFG_W,
+    TUNE_MOE_GEMV, TUNE_MOE_FUSED_GROUP, TUNE_ATTN_WG, TUNE_COUNT
+};
+
+struct Tuning {
+    bool set[TUNE_COUNT] = {};
+    int val[TUNE_COUNT] = {};
+
+    static Tuning from_env() {
+        static const char* const names[TUNE_COUNT] = {
+            "BARQ_GEMM_BM", "BARQ_GEMM_KG", "BARQ_GEMM_NS", "BARQ_GEMM_KS", "BARQ_GEMM_XCD", "BARQ_GEMM_IMPL",
+            "BARQ_GEMM_MIN_M", "BARQ_GEMV_DMA", "BARQ_GEMV_DMA_TYPES", "BARQ_GEMV_MULTI_MAX", nullptr, nullptr,
+            "BARQ_MOE_GEMV", "BARQ_MOE_FUSED_GROUP", "BARQ_ATTN_WG"};
+        Tuning t;
+        for (int i = 0; i < TUNE_COUNT; i++) {
+            if (!names[i]) continue;
+            if (const char* e = getenv(names[i])) {
+                t.set[i] = true;
+                t.val[i] = atoi(e);
+            }
+        }
+        // BARQ_GEMV_CFG = "R,W": rows per wave and waves per workgroup
+        int r = 0, w = 0;
+        if (const char* e = getenv("BARQ_GEMV_CFG"))
+            if (sscanf(e, "%d,%d", &r, &w) == 2) {
+                t.set[TUNE_GEMV_CFG_R] = t.set[TUNE_GEMV_CFG_W] = true;
+                t.val[TUNE_GEMV_CFG_R] = r;
+                t.val[TUNE_GEMV_CFG_W] = w;
+            }
+        return t;
+    }
+};
+
+// The snapshot of the handle whose call is running on this thread (set by
+// the C ABI entry points for the duration of a call; null: defaults).
+inline thread_local const Tuning* t_tuning = nullptr;
+
+inline int tuning_env(Tune key, int def = 0) {
+    const Tuning* t = t_tuning;
+    return t && t->set[key] ? t->val[key] : def;
 }
+
+struct TuningScope {
+    const Tuning* prev;
+    explicit TuningScope(const Tuning* t) : prev(t_tuning) { t_tuning = t; }
+    ~TuningScope() { t_tuning = prev; }
+    TuningScope(const TuningScope&) = delete;
+    TuningScope& operator=(const TuningScope&) = delete;
+};
 
 // GGUF block geometry (barq_core/src/gguf.rs:168-186 block sizes; bytes
 // from gguf.rs:529-530,645,747,854 and llama.cpp block_q4_0/block_q8_K).

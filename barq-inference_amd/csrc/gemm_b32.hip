@@ -352,12 +352,12 @@ static hipError_t b32_launch_t(const void* W, size_t n_rows, size_t k, const int
     if ((k / (32 * B32_SB)) % (KG * ks) != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL((b32_gemm_kernel<F, BM, NS, KG>), dim3((unsigned)(tiles_m * tiles_n * ks)), dim3(256 * KG), 0, s,
                        static_cast<const uint8_t*>(W), wrb, xr, dx, y, (int)m, (int)n_rows, (int)k, tiles_m, ks,
-                       tuning_env("BARQ_GEMM_XCD", 1));
+                       tuning_env(TUNE_GEMM_XCD, 1));
     return hipGetLastError();
 }
 
 static int b32_bm(size_t m) {
-    const int bm = tuning_env("BARQ_GEMM_BM", m > 32 ? 64 : 32);
+    const int bm = tuning_env(TUNE_GEMM_BM, m > 32 ? 64 : 32);
     return bm == 32 ? 32 : 64;
 }
 
@@ -369,7 +369,7 @@ static int b32_k_slices(size_t m, size_t n_rows, size_t k) {
     const size_t tiles = (m + bm - 1) / bm * ((n_rows + B32_BN - 1) / B32_BN), steps = k / (32 * B32_SB);
     int ks = 1;
     while (ks < 16 && tiles * ks * 2 <= 256 && steps % (size_t)(ks * 4) == 0) ks *= 2;
-    const int ovr = tuning_env("BARQ_GEMM_KS");
+    const int ovr = tuning_env(TUNE_GEMM_KS);
     if (ovr > 0 && (ovr & (ovr - 1)) == 0 && ovr <= 16 && steps % (size_t)(2 * ovr) == 0) ks = ovr;
     return ks;
 }
@@ -383,7 +383,7 @@ static hipError_t b32_dispatch(const void* W, size_t n_rows, size_t k, const int
     const int bm = b32_bm(m);
     const size_t tiles = (m + bm - 1) / bm * ((n_rows + B32_BN - 1) / B32_BN);
     const size_t steps = k / (32 * B32_SB) / ks;   // per slice
-    int kg = tuning_env("BARQ_GEMM_KG", ks == 1 && tiles < 256 && steps % 4 == 0 ? 4 : 2);
+    int kg = tuning_env(TUNE_GEMM_KG, ks == 1 && tiles < 256 && steps % 4 == 0 ? 4 : 2);
     if (kg != 1 && kg != 2 && kg != 4) kg = 2;
     if (kg > F::KG_MAX) kg = F::KG_MAX;   // LDS: Q8_0 weight rows are twice as long
     if (steps % kg != 0) kg = steps % 2 == 0 ? 2 : 1;

@@ -827,7 +827,7 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     if ((GROUPED ? a.nsb : a.nsb / a.ks) % KG != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, KG, GROUPED>), dim3(grid), dim3(64 * NW * KG), 0, s, a.wt, a.wrb, a.X, a.xrb,
                        a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, a.ks, a.ykstride,
-                       tuning_env("BARQ_GEMM_XCD", 1));   // XCD-aware tile order (ungrouped)
+                       tuning_env(TUNE_GEMM_XCD, 1));   // XCD-aware tile order (ungrouped)
     return hipGetLastError();
 }
 
@@ -846,7 +846,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // tile covers both 32-row halves of its 32 columns (bm 64: the weight
     // fragment is decoded once for two MFMA row tiles; 26.5-27.1 against
     // 27.6-29.0 us at C4 for eight waves of 32 x 32, bm 65)
-    const int g_kq_ns = tuning_env("BARQ_GEMM_NS"), g_kq_bm = tuning_env("BARQ_GEMM_BM");
+    const int g_kq_ns = tuning_env(TUNE_GEMM_NS), g_kq_bm = tuning_env(TUNE_GEMM_BM);
     const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 64 : 32);
     if (bm == 16) {
         if (g_kq_ns == 2) return kq_launch_t<F, 16, 2, 4, GROUPED>(a, s);
@@ -859,7 +859,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     if constexpr (!GROUPED) {
         // two K-groups of waves share a tile's pipeline (twice the waves per
         // SIMD for the same LDS) when the super-block count is even
-        const int kg = tuning_env("BARQ_GEMM_KG", 2);
+        const int kg = tuning_env(TUNE_GEMM_KG, 2);
         if (kg == 2 && (a.nsb / a.ks) % 2 == 0) {
             if constexpr (F::TYPE == TYPE_Q4_K) {
                 if (bm == 65) return kq_launch_t<F, 64, 2, 8, GROUPED, 2>(a, s);
@@ -887,7 +887,7 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
 // Raw buffer loads use 32-bit offsets: each weight matrix and the activation
 // rows must stay below 2 GiB.  Q6_K needs row bytes that are a multiple of 4
 // (an even number of super-blocks).
-int kq_k_slices_override() { return tuning_env("BARQ_GEMM_KS"); }
+int kq_k_slices_override() { return tuning_env(TUNE_GEMM_KS); }
 
 // Activation rows from which matmul runs the MFMA GEMMs instead of one GEMV
 // per row (BARQ_GEMM_MIN_M overrides; at least 2).  Measured on MI355X at
@@ -897,7 +897,7 @@ int kq_k_slices_override() { return tuning_env("BARQ_GEMM_KS"); }
 // 12.8 against 10.2 / 13.4).
 int gemm_min_rows(int w_type) {
     const int def = w_type == TYPE_Q4_0 || w_type == TYPE_Q4_0_BARQ ? 4 : 3;
-    const int v = tuning_env("BARQ_GEMM_MIN_M", def);
+    const int v = tuning_env(TUNE_GEMM_MIN_M, def);
     return v < 2 ? 2 : v;
 }
 
@@ -928,10 +928,10 @@ static KQArgs kq_args(int w_type, size_t n_rows, size_t k, const void* xq, float
 // their parity).  BARQ_GEMM_KS overrides (a power of two up to 16).
 // The tile height kq_dispatch picks (for an even super-block count per slice).
 static size_t kq_tile_rows(int w_type, size_t m) {
-    const int bm_env = tuning_env("BARQ_GEMM_BM");
+    const int bm_env = tuning_env(TUNE_GEMM_BM);
     const int bm = bm_env ? bm_env : (m > 32 ? 64 : 32);
     if (bm == 16) return 16;
-    if (tuning_env("BARQ_GEMM_KG", 2) == 2) return w_type == TYPE_Q4_K && (bm == 64 || bm == 65) ? 64 : 32;
+    if (tuning_env(TUNE_GEMM_KG, 2) == 2) return w_type == TYPE_Q4_K && (bm == 64 || bm == 65) ? 64 : 32;
     return bm >= 64 ? 64 : 32;
 }
 
@@ -940,7 +940,7 @@ int kq_k_slices(int w_type, size_t m, size_t n_rows, size_t k) {
     const size_t tiles = (m + bm - 1) / bm * ((n_rows + KQ_BN - 1) / KQ_BN), nsb = k / 256;
     int ks = 1;
     while (ks < 16 && tiles * ks * 2 <= 256 && nsb % (size_t)(ks * 4) == 0) ks *= 2;
-    const int ovr = tuning_env("BARQ_GEMM_KS");
+    const int ovr = tuning_env(TUNE_GEMM_KS);
     if (ovr > 0 && (ovr & (ovr - 1)) == 0 && ovr <= 16 && nsb % (size_t)(2 * ovr) == 0) ks = ovr;
     return ks;
 }

@@ -414,7 +414,7 @@ static hipError_t launch_kq(const uint8_t* W, size_t wrb, const uint8_t* X, size
 // Activation-tile height: the largest of 128/64/32/16 that still gives
 // every CU two workgroups, never taller than M needs.
 static int pick_bm(int M, int N) {
-    if (const int o = tuning_env("BARQ_GEMM_BM")) return o;
+    if (const int o = tuning_env(TUNE_GEMM_BM)) return o;
     const int tiles_n = (N + GM_BN - 1) / GM_BN;
     int bm = 128;
     while (bm > 16 && (bm >= 2 * ((M + 15) / 16 * 16) || (long)tiles_n * ((M + bm - 1) / bm) < 512)) bm >>= 1;
@@ -450,7 +450,7 @@ bool gemm_mfma_supported(int w_type, size_t n_rows, size_t k, size_t m) {
 }
 
 static bool use_kq(int w_type, size_t n_rows, size_t k, size_t m) {
-    return tuning_env("BARQ_GEMM_IMPL", 2) != 0 && kq_supported(w_type, n_rows, k, m);
+    return tuning_env(TUNE_GEMM_IMPL, 2) != 0 && kq_supported(w_type, n_rows, k, m);
 }
 
 size_t gemm_mfma_workspace(int w_type, size_t n_rows, size_t k, size_t m) {

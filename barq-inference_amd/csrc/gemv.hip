@@ -258,11 +258,7 @@ struct GemvCfg { int r, waves; };
 
 // BARQ_GEMV_CFG="R,W" overrides the launch shape (used for tuning sweeps).
 static GemvCfg env_cfg() {
-    GemvCfg c = {0, 0};
-    if (const char* e = getenv("BARQ_GEMV_CFG")) {
-        if (sscanf(e, "%d,%d", &c.r, &c.waves) != 2) c = {0, 0};
-    }
-    return c;
+    return GemvCfg{tuning_env(TUNE_GEMV_CFG_R), tuning_env(TUNE_GEMV_CFG_W)};
 }
 
 
@@ -322,12 +318,12 @@ static int dma_bit(int w_type);
 // layout conditions, and the tokens' staged rows within LDS).
 // BARQ_GEMV_MULTI_MAX caps the tokens (0 turns it off).
 static bool multi_dma(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m) {
-    return (tuning_env("BARQ_GEMV_DMA_TYPES", 2 | 4 | 8 | 16) & dma_bit(w_type)) &&
+    return (tuning_env(TUNE_GEMV_DMA_TYPES, 2 | 4 | 8 | 16) & dma_bit(w_type)) &&
            gemv_dma_supported(w_type, W, n_rows, k, xq) && gemv_dma_multi_fits(w_type, k, m);
 }
 
 bool gemv_multi_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m) {
-    const int mx = tuning_env("BARQ_GEMV_MULTI_MAX", 4);
+    const int mx = tuning_env(TUNE_GEMV_MULTI_MAX, 4);
     if (m < 2 || (int)m > (mx < 4 ? mx : 4) || n_rows > (size_t)INT32_MAX) return false;
     if (multi_dma(w_type, W, n_rows, k, xq, m)) return true;
     return w_type == TYPE_Q4_K && k % 256 == 0;
@@ -372,7 +368,7 @@ static hipError_t launch_moe_gemv(const MoeGemvWeights& wt, const int32_t* offse
 
 // BARQ_MOE_GEMV: 1 (default) single-token MoE steps take the grouped GEMVs,
 // 2 any step of at most 4 assignments, 0 none
-int moe_gemv_enabled() { return tuning_env("BARQ_MOE_GEMV", 1); }
+int moe_gemv_enabled() { return tuning_env(TUNE_MOE_GEMV, 1); }
 
 bool moe_gemv_supported(int w_type, size_t n_experts, size_t n_mats, size_t n_rows, size_t k) {
     return (w_type == TYPE_Q4_K || w_type == TYPE_Q6_K) && k % 256 == 0 && k > 0 && n_experts > 0 && n_mats > 0 &&
@@ -417,7 +413,7 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
     const uint8_t* w = static_cast<const uint8_t*>(W);
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     const int n = (int)n_rows, kk = (int)k;
-    if (tuning_env("BARQ_GEMV_DMA_TYPES", 2 | 4 | 8 | 16) & dma_bit(w_type) &&
+    if (tuning_env(TUNE_GEMV_DMA_TYPES, 2 | 4 | 8 | 16) & dma_bit(w_type) &&
         gemv_dma_supported(w_type, W, n_rows, k, xq))
         return gemv_dma_launch(w_type, W, n_rows, k, xq, y, s);
     switch (w_type) {

@@ -370,7 +370,7 @@ static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const voi
     }
 #define BARQ_DMA_CASE(WW, RR, DD) \
     case WW * 100 + RR * 10 + DD: return launch_dma<P, WW, RR, DD>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
-    switch (tuning_env("BARQ_GEMV_DMA")) {
+    switch (tuning_env(TUNE_GEMV_DMA)) {
     BARQ_DMA_CASE(4, 2, 2) BARQ_DMA_CASE(4, 4, 4) BARQ_DMA_CASE(4, 8, 2) BARQ_DMA_CASE(8, 2, 2)
     BARQ_DMA_CASE(8, 4, 2) BARQ_DMA_CASE(2, 2, 2) BARQ_DMA_CASE(2, 4, 2) BARQ_DMA_CASE(4, 1, 1)
     BARQ_DMA_CASE(8, 1, 1)
@@ -385,7 +385,7 @@ static hipError_t dispatch_dma(const void* W, size_t n_rows, size_t k, const voi
 // block pairs per lane, offsets within one wave's rows stay below 2 GiB and
 // the staged activation fits in LDS beside the slice buffers.
 bool gemv_dma_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq) {
-    if (tuning_env("BARQ_GEMV_DMA") < 0 || k == 0 || n_rows > (size_t)INT32_MAX) return false;
+    if (tuning_env(TUNE_GEMV_DMA) < 0 || k == 0 || n_rows > (size_t)INT32_MAX) return false;
     if (((uintptr_t)W & 3) || ((uintptr_t)xq & 3)) return false;
     size_t rb = 0, xch = 0;
     switch (w_type) {

@@ -408,7 +408,7 @@ extern "C" {
 int barq_rocm_cache_create(barq_rocm_handle* h, const barq_rocm_gguf* g, barq_rocm_cache** out) {
     if (!h || !g || !out) return fail(BARQ_E_INVALID, "cache_create: null argument");
     *out = nullptr;
-    DeviceGuard dg(h->device);
+    DeviceGuard dg(h);
     auto* c = new barq_rocm_cache();
     c->device = h->device;
     uint64_t total = 0;

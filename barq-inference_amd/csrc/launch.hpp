@@ -107,8 +107,14 @@ hipError_t gemm_f32_nt_launch(const float* a, const float* b_nk, size_t m, size_
                               hipStream_t s);
 
 // moe.hip
+// top-k routing; max_active > 0 adds reduce_expert_assignments (dropped
+// slots: id -1, weight 0)
 hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, size_t top_k,
-                            int32_t* ids, float* weights, hipStream_t s);
+                            int32_t* ids, float* weights, hipStream_t s, size_t max_active = 0,
+                            float min_weight = 0.0f);
+// reduce_expert_assignments on rows x k slots (out may alias in)
+hipError_t moe_reduce_launch(const int32_t* ids, const float* weights, size_t rows, size_t k, size_t max_active,
+                             float min_weight, int32_t* out_ids, float* out_weights, hipStream_t s);
 // CSR grouping of routing assignments (batch_by_expert): offsets[n_experts+1],
 // tokens/wts[rows*top_k] in expert-major, ascending-token order.
 hipError_t moe_group_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,

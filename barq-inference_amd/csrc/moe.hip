@@ -13,19 +13,56 @@ constexpr int MOE_MAX_TOPK = 64;
 constexpr int MOE_FUSED_MAX = 2048;   // assignments the fused grouping + gather handles
 constexpr float F32_EPSILON = 1.1920929e-7f;
 
+// reduce_expert_assignments (moe_fused.rs:147-194) on one row of k slots
+// held by the calling thread (ci: expert ids, id < 0 an absent slot; cw:
+// weights).  Keeps the slots with weight >= min_w (none: the largest, the
+// later slot winning ties, as Iterator::max_by with partial_cmp does), sorts
+// them by weight descending (stable), keeps at most keep_max and divides by
+// their sequential sum floored at f32::EPSILON.  The kept slots end up first;
+// returns their number.
+__device__ int ser_reduce_row(int* ci, float* cw, int k, int keep_max, float min_w) {
+    int n = 0, best = -1;
+    float bw = 0.0f;
+    for (int i = 0; i < k; i++) {
+        const int e = ci[i];
+        const float w = cw[i];
+        if (e < 0) continue;
+        if (best < 0 || !(bw > w)) { best = e; bw = w; }
+        if (w >= min_w) { ci[n] = e; cw[n] = w; n++; }   // n <= i: reads stay ahead of writes
+    }
+    if (n == 0 && best >= 0) { ci[0] = best; cw[0] = bw; n = 1; }
+    for (int i = 1; i < n; i++) {
+        const int ti = ci[i];
+        const float tw = cw[i];
+        int j = i;
+        while (j > 0 && cw[j - 1] < tw) { ci[j] = ci[j - 1]; cw[j] = cw[j - 1]; j--; }
+        ci[j] = ti;
+        cw[j] = tw;
+    }
+    if (n > keep_max) n = keep_max;
+    float sum = -0.0f;
+    for (int i = 0; i < n; i++) sum += cw[i];
+    sum = fmaxf(sum, F32_EPSILON);
+    for (int i = 0; i < n; i++) cw[i] = cw[i] / sum;
+    return n;
+}
+
 // select_top_k_experts (moe_fused.rs:95-144), one thread per row: a stable
 // descending sort keeps equal logits in index order, so the first k picks
 // are the largest values with the lowest index winning ties; softmax over
 // the kept k with the max subtracted and the denominator floored at
-// f32::EPSILON.  k = clamp(top_k, 1, n_experts) (:121).
+// f32::EPSILON.  k = clamp(top_k, 1, n_experts) (:121).  With keep_max > 0
+// the row then goes through reduce_expert_assignments (the MoE forward of
+// advanced/src/moe.rs:157-162); dropped slots get id -1, weight 0.
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int rows, int ne,
-                                                       int k, int32_t* __restrict__ ids,
-                                                       float* __restrict__ weights) {
+                                                       int k, int keep_max, float min_w,
+                                                       int32_t* __restrict__ ids, float* __restrict__ weights) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
     const float* row = logits + (size_t)r * ne;
     uint64_t taken[MOE_MAX_EXPERTS / 64] = {0, 0, 0, 0};
     int sel[MOE_MAX_TOPK];
+    float sw[MOE_MAX_TOPK];
     for (int i = 0; i < k; i++) {
         int best = -1;
         float bv = 0.0f;
@@ -42,17 +79,46 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
     float denom = 0.0f;
     for (int i = 0; i < k; i++) denom += expf(row[sel[i]] - mx);
     denom = fmaxf(denom, F32_EPSILON);
+    for (int i = 0; i < k; i++) sw[i] = expf(row[sel[i]] - mx) / denom;
+    const int n = keep_max > 0 ? ser_reduce_row(sel, sw, k, keep_max, min_w) : k;
     for (int i = 0; i < k; i++) {
-        ids[(size_t)r * k + i] = sel[i];
-        weights[(size_t)r * k + i] = expf(row[sel[i]] - mx) / denom;
+        ids[(size_t)r * k + i] = i < n ? sel[i] : -1;
+        weights[(size_t)r * k + i] = i < n ? sw[i] : 0.0f;
     }
 }
 
 hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, size_t top_k,
-                            int32_t* ids, float* weights, hipStream_t s) {
+                            int32_t* ids, float* weights, hipStream_t s, size_t max_active, float min_weight) {
     if (rows == 0) return hipSuccess;
     hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, logits,
-                       (int)rows, (int)n_experts, (int)top_k, ids, weights);
+                       (int)rows, (int)n_experts, (int)top_k, (int)max_active, min_weight, ids, weights);
+    return hipGetLastError();
+}
+
+// reduce_expert_assignments on given rows x k slots (in place allowed)
+__global__ __launch_bounds__(64) void moe_reduce_kernel(const int32_t* ids, const float* weights, int rows, int k,
+                                                        int keep_max, float min_w, int32_t* out_ids,
+                                                        float* out_weights) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    int ci[MOE_MAX_TOPK];
+    float cw[MOE_MAX_TOPK];
+    for (int i = 0; i < k; i++) {
+        ci[i] = ids[(size_t)r * k + i];
+        cw[i] = weights[(size_t)r * k + i];
+    }
+    const int n = ser_reduce_row(ci, cw, k, keep_max, min_w);
+    for (int i = 0; i < k; i++) {
+        out_ids[(size_t)r * k + i] = i < n ? ci[i] : -1;
+        out_weights[(size_t)r * k + i] = i < n ? cw[i] : 0.0f;
+    }
+}
+
+hipError_t moe_reduce_launch(const int32_t* ids, const float* weights, size_t rows, size_t k, size_t max_active,
+                             float min_weight, int32_t* out_ids, float* out_weights, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_reduce_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, ids, weights,
+                       (int)rows, (int)k, (int)(max_active > 0 ? max_active : 1), min_weight, out_ids, out_weights);
     return hipGetLastError();
 }
 
@@ -285,7 +351,7 @@ __global__ __launch_bounds__(256) void moe_group_gather_q8k_kernel(
 }
 
 // BARQ_MOE_FUSED_GROUP=0 keeps grouping and gather-quantize in two launches
-int moe_fused_group_enabled() { return tuning_env("BARQ_MOE_FUSED_GROUP", 1); }
+int moe_fused_group_enabled() { return tuning_env(TUNE_MOE_FUSED_GROUP, 1); }
 
 hipError_t moe_group_gather_q8k_launch(const int32_t* ids, const float* weights, size_t rows, size_t top_k,
                                        size_t n_experts, const float* x, size_t hidden, void* out, int32_t* offsets,

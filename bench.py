@@ -171,6 +171,32 @@ def measure_traffic(config, w_type_name=None):
                          write_scale=round(wsc, 4))
 
 
+def host_cpu():
+    """CPU model as /proc/cpuinfo names it, with family/model/stepping (a
+    virtualised host may report only the vendor's brand)."""
+    info = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" not in line:
+                    if info:
+                        break
+                    continue
+                key, val = (p.strip() for p in line.split(":", 1))
+                info.setdefault(key, val)
+    except OSError:
+        pass
+    name = info.get("model name") or platform.processor() or "unknown CPU"
+    fam = [f"{k_} {info[k_]}" for k_ in ("cpu family", "model", "stepping") if k_ in info]
+    sockets = "?"
+    try:
+        with open("/proc/cpuinfo") as f:
+            sockets = str(len({ln.split(":", 1)[1].strip() for ln in f if ln.startswith("physical id")}) or "?")
+    except OSError:
+        pass
+    return f"{name} ({', '.join(fam)}; {sockets} socket(s))"
+
+
 def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
     """The reference's per-call CPU path on a bounded sample (oracle restatement)."""
     import numpy as np
@@ -178,7 +204,10 @@ def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
 
     wf = orc.dequantize(w_type, w, n * k)                  # load-time dequant (not timed)
     out = {}
-    threads = max(1, min(16, os.cpu_count() or 1))
+    nproc = os.cpu_count() or 1
+    # variant (iii) runs on every host core this process may be scheduled on
+    # (nproc unless an affinity mask narrows it)
+    threads = max(1, len(os.sched_getaffinity(0)))
     # (i) literal: gemm_f32(x[1 x k], W^T[k x n]) column by column (blas.rs:199-210)
     w_t = np.ascontiguousarray(wf.reshape(n, k).T)          # weight_cache.rs:196-201
     y = np.zeros(n, np.float32)
@@ -217,15 +246,7 @@ def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
     thr_s = t_used / reps
     out["simd_threads"] = dict(us_per_call=thr_s * 1e6, threads=used, calls=reps, sample_s=round(t_used, 3))
     simd = {2: "avx512", 1: "avx2", 0: "scalar"}[orc.cpub_simd_level()]
-    cpu_model = platform.processor() or ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cpu_model = host_cpu()
     for v in out.values():
         v["gbs_alg"] = alg_bytes / (v["us_per_call"] * 1e-6) / 1e9
     return {
@@ -236,7 +257,10 @@ def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
         "sample": (f"reference per-call path (blas.rs:199-210 gemm_f32 at M=1 over f32 W^T dequantized at load, "
                    f"not timed), {out['literal_1core']['cols_sampled']} output columns timed "
                    f"({out['literal_1core']['cols_sampled'] / n:.1f} calls' worth) in "
-                   f"{out['literal_1core']['sample_s']} s; {cpu_model}, {simd}"),
+                   f"{out['literal_1core']['sample_s']} s; {cpu_model}, {simd}; nproc {nproc}, "
+                   f"variant (iii) on {out['simd_threads']['threads']} threads"),
+        "host_cpu": cpu_model,
+        "nproc": nproc,
         "us_per_call": round(out["literal_1core"]["us_per_call"], 1),
         "variants": {k_: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                      for k_, v in out.items()},

@@ -228,6 +228,24 @@ int barq_rocm_quantize_q4_k_barq(barq_rocm_handle* h, const float* x, size_t n, 
 int barq_rocm_moe_route(barq_rocm_handle* h, const float* logits, size_t rows,
                         size_t n_experts, size_t top_k, int32_t* ids,
                         float* weights, int mem);
+/* reduce: reduce_expert_assignments (moe_fused.rs:147-194), the smart expert
+ *   reduction MoEInference::forward_with_routing runs between routing and
+ *   dispatch (advanced/src/moe.rs:157-162, ser_threshold 0.05 and
+ *   max_active = n_expert_per_token by default, :24-31).  Per row of top_k
+ *   slots (id < 0: an absent slot): keep the assignments with weight >=
+ *   min_weight (if none, the largest; the later slot wins ties), sort them by
+ *   weight descending (stable), keep at most max(max_active, 1), divide by
+ *   their sequential f32 sum floored at f32::EPSILON.  Kept assignments come
+ *   first; the rest of the row gets id -1 and weight 0, which moe_ffn skips.
+ *   out_ids / out_weights may be ids / weights.
+ * route_reduce: route then reduce in one launch; ids/weights rows x
+ *   clamp(top_k, 1, n_experts). */
+int barq_rocm_moe_reduce(barq_rocm_handle* h, const int32_t* ids, const float* weights,
+                         size_t rows, size_t top_k, size_t max_active, float min_weight,
+                         int32_t* out_ids, float* out_weights, int mem);
+int barq_rocm_moe_route_reduce(barq_rocm_handle* h, const float* logits, size_t rows,
+                               size_t n_experts, size_t top_k, size_t max_active,
+                               float min_weight, int32_t* ids, float* weights, int mem);
 int barq_rocm_moe_ffn(barq_rocm_handle* h, size_t n_experts,
                       int gate_type, const void* const* gate,
                       int up_type, const void* const* up,

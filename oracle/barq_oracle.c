@@ -570,6 +570,51 @@ size_t orc_moe_select_top_k(const float* logits, size_t rows, size_t cols,
     return kk;
 }
 
+void orc_moe_reduce_experts(const int32_t* ids, const float* weights, size_t rows, size_t k,
+                            size_t max_active, float min_weight, int32_t* out_ids, float* out_weights) {
+    /* reduce_expert_assignments (moe_fused.rs:147-194).  A row's assignments
+       are its k slots; a slot with id < 0 is absent (an assignment dropped
+       earlier).  Output: the kept assignments first, then id -1 / weight 0. */
+    const size_t keep_max = max_active > 0 ? max_active : 1;    /* .max(1), :180 */
+    int32_t* ci = (int32_t*)malloc((k ? k : 1) * sizeof(int32_t));
+    float* cw = (float*)malloc((k ? k : 1) * sizeof(float));
+    if (!ci || !cw) { free(ci); free(cw); return; }
+    for (size_t r = 0; r < rows; r++) {
+        const int32_t* ri = ids + r * k;
+        const float* rw = weights + r * k;
+        size_t n = 0;
+        for (size_t i = 0; i < k; i++)                          /* filter(weight >= min_weight), :161 */
+            if (ri[i] >= 0 && rw[i] >= min_weight) { ci[n] = ri[i]; cw[n] = rw[i]; n++; }
+        if (n == 0) {
+            /* max_by with partial_cmp().unwrap_or(Equal) (:165-171): the running
+               maximum is replaced unless it compares Greater, so among equal
+               weights (and NaN) the later slot wins */
+            long best = -1;
+            for (size_t i = 0; i < k; i++) {
+                if (ri[i] < 0) continue;
+                if (best < 0 || !(rw[best] > rw[i])) best = (long)i;
+            }
+            if (best >= 0) { ci[0] = ri[best]; cw[0] = rw[best]; n = 1; }
+        }
+        /* stable sort by weight, descending (:177) */
+        for (size_t i = 1; i < n; i++) {
+            int32_t ti = ci[i]; float tw = cw[i];
+            size_t j = i;
+            while (j > 0 && cw[j - 1] < tw) { ci[j] = ci[j - 1]; cw[j] = cw[j - 1]; j--; }
+            ci[j] = ti; cw[j] = tw;
+        }
+        if (n > keep_max) n = keep_max;                         /* truncate, :178 */
+        float sum = -0.0f;                                      /* Sum<f32>: sequential fold, :180-184 */
+        for (size_t i = 0; i < n; i++) sum += cw[i];
+        sum = fmaxf(sum, 1.1920929e-7f);                        /* .max(f32::EPSILON) */
+        for (size_t i = 0; i < k; i++) {
+            out_ids[r * k + i] = i < n ? ci[i] : -1;
+            out_weights[r * k + i] = i < n ? cw[i] / sum : 0.0f;
+        }
+    }
+    free(ci); free(cw);
+}
+
 void orc_moe_batch_by_expert(const int32_t* ids, const float* weights,
                              size_t rows, size_t k, size_t n_experts,
                              int32_t* offsets, int32_t* tokens, float* wts) {

@@ -123,6 +123,15 @@ void orc_quantized_matmul_split(const float* a, const uint8_t* bq, size_t n_bq,
    rows x k_eff, k_eff = clamp(k, 1, cols) is returned (0 on bad input). */
 size_t orc_moe_select_top_k(const float* logits, size_t rows, size_t cols,
                             size_t k, int32_t* ids, float* weights);
+/* reduce_expert_assignments (moe_fused.rs:147-194), smart expert reduction:
+   per row, keep the assignments with weight >= min_weight (if none, the
+   largest, the later slot winning ties), sorted by weight descending
+   (stable), at most max(max_active, 1), weights renormalised by their
+   sequential sum floored at f32::EPSILON.  ids/weights are rows x k; ids < 0
+   are absent slots.  Output rows x k: kept assignments first, then id -1,
+   weight 0 (out may alias in). */
+void orc_moe_reduce_experts(const int32_t* ids, const float* weights, size_t rows, size_t k,
+                            size_t max_active, float min_weight, int32_t* out_ids, float* out_weights);
 /* batch_by_expert (moe_fused.rs:196-223): CSR grouping.  offsets has
    n_experts+1 entries; tokens/wts have rows*k entries (ascending token order
    inside an expert).  Empty experts have offsets[e]==offsets[e+1]. */

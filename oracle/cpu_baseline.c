@@ -87,22 +87,28 @@ static void* run_job(void* p) {
     return NULL;
 }
 
-/* (iii) rows [r0, r1) split over `threads` pthreads; returns threads used */
+/* (iii) rows [r0, r1) split over `threads` pthreads (at most 512); returns
+   the number of row ranges run (a range whose thread cannot be created runs
+   on the calling thread) */
+#define CPUB_MAX_THREADS 512
 int cpub_gemv_simd_threaded(const float* a, const float* x, size_t n, size_t r0, size_t r1,
                             float* y, int threads) {
     if (threads < 1) threads = 1;
-    if (threads > 256) threads = 256;
-    pthread_t tid[256];
-    struct job jobs[256];
+    if (threads > CPUB_MAX_THREADS) threads = CPUB_MAX_THREADS;
+    pthread_t tid[CPUB_MAX_THREADS];
+    char created[CPUB_MAX_THREADS];
+    struct job jobs[CPUB_MAX_THREADS];
     size_t rows = r1 - r0, per = (rows + (size_t)threads - 1) / (size_t)threads;
     int used = 0;
     for (int t = 0; t < threads; t++) {
         size_t s = r0 + (size_t)t * per, e = s + per < r1 ? s + per : r1;
         if (s >= e) break;
         jobs[t] = (struct job){a, x, n, s, e, y};
-        if (pthread_create(&tid[t], NULL, run_job, &jobs[t]) != 0) { run_job(&jobs[t]); continue; }
+        created[t] = pthread_create(&tid[t], NULL, run_job, &jobs[t]) == 0;
+        if (!created[t]) run_job(&jobs[t]);
         used = t + 1;
     }
-    for (int t = 0; t < used; t++) pthread_join(tid[t], NULL);
+    for (int t = 0; t < used; t++)
+        if (created[t]) pthread_join(tid[t], NULL);
     return used;
 }

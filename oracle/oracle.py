@@ -48,6 +48,7 @@ def lib():
             "orc_dequantize_signed_8bit_split": (None, [_vp, _sz, _vp, _sz, _sz, _vp, _sz]),
             "orc_quantized_matmul_split": (None, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz, _i, _sz, _vp]),
             "orc_moe_select_top_k": (_sz, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "orc_moe_reduce_experts": (None, [_vp, _vp, _sz, _sz, _sz, ctypes.c_float, _vp, _vp]),
             "orc_moe_batch_by_expert": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
             "orc_moe_dispatch": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
             "orc_moe_ffn": (_i, [_i, _vp, _i, _vp, _i, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp]),
@@ -269,6 +270,18 @@ def moe_select_top_k(logits: np.ndarray, k: int):
     got = lib().orc_moe_select_top_k(_p(logits), rows, cols, k, _p(ids), _p(w))
     assert got == kk
     return ids, w
+
+
+def moe_reduce_experts(ids: np.ndarray, weights: np.ndarray, max_active: int, min_weight: float):
+    """reduce_expert_assignments (moe_fused.rs:147-194) on rows x k slots
+    (id < 0: absent); kept assignments first, then -1 / 0."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    rows, k = ids.shape
+    oi = np.empty_like(ids)
+    ow = np.empty_like(weights)
+    lib().orc_moe_reduce_experts(_p(ids), _p(weights), rows, k, max_active, ctypes.c_float(min_weight), _p(oi), _p(ow))
+    return oi, ow
 
 
 def moe_batch_by_expert(ids: np.ndarray, weights: np.ndarray, n_experts: int):

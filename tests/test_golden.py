@@ -77,6 +77,11 @@ def test_kat_moe(orc):
     ids, w = orc.moe_select_top_k(np.float32(c["logits"]).reshape(c["rows"], c["n_experts"]), c["top_k"])
     assert ids.tolist() == c["ids"], c["src"]
     assert np.all(np.abs(w.sum(1) - c["weight_row_sum"]) < c["tol"])
+    c = k["moe_reduce_experts"][0]
+    ids, w = orc.moe_reduce_experts(np.int32(c["ids"]), np.float32(c["weights"]), c["max_active"], c["min_weight"])
+    kept = [[int(e) for e in row if e >= 0] for row in ids]
+    assert kept == c["reduced_ids"], c["src"]
+    assert np.all(np.abs(w.sum(1) - c["weight_row_sum"]) < c["tol"]), c["src"]
     c = k["moe_dispatch"][0]
     fns = [lambda a, s=s: a * s for s in c["expert_scale"]]
     out = orc.moe_dispatch(np.float32(c["input"]).reshape(c["rows"], c["hidden"]), len(fns), np.int32(c["ids"]),

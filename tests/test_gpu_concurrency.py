@@ -70,3 +70,36 @@ def test_distinct_handles_from_threads():
     for key, got in results.items():
         for a, b in zip(got, ref):
             assert torch.equal(a, b), key
+
+
+def test_stream_switch_orders_workspace_users():
+    """barq_rocm_set_stream between two calls that use the handle's one
+    workspace (f32 activations quantized into it, then a GEMM reading them):
+    the second call, on the new stream, must not overwrite the first call's
+    quantized rows while the first GEMM, on the old stream, still reads them.
+    The first call is made long (a large matmul) so an unordered second call
+    would land inside it."""
+    import torch
+    n, k, m = 14336, 4096, 256
+    w = torch.from_numpy(synth.gen_q4_k(n, k, 21)).cuda()
+    xa = torch.from_numpy(synth.gen_f32(m * k, 22).reshape(m, k)).cuda()
+    xb = torch.from_numpy(synth.gen_f32(m * k, 23).reshape(m, k) * 3.0).cuda()
+    be = B.Backend(0)
+    try:
+        ref_a = be.matmul(B.Q4_K, w, n, k, B.ACT_F32_Q8, xa, m)
+        ref_b = be.matmul(B.Q4_K, w, n, k, B.ACT_F32_Q8, xb, m)
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        for it in range(3):
+            ya = torch.full((m, n), float("nan"), device="cuda")
+            yb = torch.full((m, n), float("nan"), device="cuda")
+            torch.cuda.synchronize()
+            be.set_stream(s1.cuda_stream)
+            be.matmul_raw(B.Q4_K, w, n, k, B.ACT_F32_Q8, xa, m, ya, B.MEM_DEVICE)
+            be.set_stream(s2.cuda_stream)
+            be.matmul_raw(B.Q4_K, w, n, k, B.ACT_F32_Q8, xb, m, yb, B.MEM_DEVICE)
+            torch.cuda.synchronize()
+            assert torch.equal(ya, ref_a), f"iteration {it}: first call's result changed"
+            assert torch.equal(yb, ref_b), f"iteration {it}: second call's result changed"
+        be.set_stream(None)
+    finally:
+        be.close()

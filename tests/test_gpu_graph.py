@@ -122,3 +122,32 @@ def test_attention_graph_replays(be):
                                                  o.data_ptr(), B.MEM_DEVICE))
     replays_match(be, lambda: call(1, out), out, lambda: call(0, out2))
     c.close()
+
+
+def test_graph_replay_after_workspace_growth(be):
+    """A graph captured around a call that uses the workspace keeps working
+    after a later, larger call grows the workspace: the old buffer is
+    retired, not freed, so the captured kernels still address valid memory."""
+    import torch
+    be2 = B.Backend(0)   # a fresh handle: its workspace starts at the 16 MiB minimum
+    try:
+        n, k, m = 1152, 4096, 16
+        w = dev(synth.gen_q4_k(n, k, 31))
+        x = dev(synth.gen_f32(m * k, 32).reshape(m, k))
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        y2 = torch.empty((2, n), dtype=torch.float32, device="cuda")
+        # the literal f32 matmul dequantizes W into the workspace: n * k * 4 B
+        # = 18.9 MB, more than the first allocation
+        assert n * k * 4 > 16 * 1024 * 1024
+        grown = []
+
+        def grow_once():
+            if not grown:
+                be2.matmul_raw(B.Q4_K, w, n, k, B.ACT_F32, x, 2, y2, B.MEM_DEVICE)
+                grown.append(1)
+            else:
+                be2.matmul_raw(B.Q4_K, w, n, k, B.ACT_F32_Q8, x, 1, y2, B.MEM_DEVICE)
+        replays_match(be2, lambda: be2.matmul_raw(B.Q4_K, w, n, k, B.ACT_F32_Q8, x, m, y, B.MEM_DEVICE), y, grow_once)
+        assert grown
+    finally:
+        be2.close()

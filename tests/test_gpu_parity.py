@@ -5,6 +5,7 @@ matmul outputs within 1e-3 (relative L2 and max-abs relative to max |y|),
 the tolerance the north star states.  The oracle for the Q8 paths runs on
 the same quantized activations the GPU produced (after checking those are
 bit-exact with the oracle's own quantization)."""
+import contextlib
 import os
 
 import numpy as np
@@ -17,6 +18,25 @@ from conftest import assert_bits_equal, assert_close_1e3
 pytestmark = pytest.mark.gpu
 
 TYPES = {"Q4_0": B.Q4_0, "Q4_0_BARQ": B.Q4_0_BARQ, "Q8_0": B.Q8_0, "Q4_K": B.Q4_K, "Q6_K": B.Q6_K}
+
+
+@contextlib.contextmanager
+def tuned(**kv):
+    """A handle created with tuning variables kv set (read at creation)."""
+    old = {k: os.environ.get(k) for k in kv}
+    os.environ.update({k: str(v) for k, v in kv.items()})
+    try:
+        b = B.Backend(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    try:
+        yield b
+    finally:
+        b.close()
 
 
 def dev(a):
@@ -271,6 +291,55 @@ def test_moe_route(be, orc):
     assert ids.tolist() == [[1, 2], [0, 2]]
 
 
+def test_moe_route_reduce_and_reduce(be, orc):
+    """Smart expert reduction (reduce_expert_assignments, moe_fused.rs:147-194)
+    after top-k routing, fused into the routing launch and on its own:
+    tokens with a wide logit gap lose their second expert at the default
+    threshold 0.05 (advanced/src/moe.rs:24-31)."""
+    rows, ne, k = 96, 8, 3
+    logits = synth.gen_f32(rows * ne, 77).reshape(rows, ne)
+    logits[::3, 5] += 4.0                      # a dominant expert: the others fall below 0.05
+    logits[1::7, :] = 0.0                      # all equal: ties, nothing dropped at k = 3
+    rid, rw = orc.moe_select_top_k(logits, k)
+    ref_i, ref_w = orc.moe_reduce_experts(rid, rw, 2, 0.05)
+    assert (ref_i[:, 1] < 0).sum() > 10 and (ref_i[:, 1] >= 0).sum() > 10
+    # standalone reduce on the oracle's routing: bit-exact
+    gi, gw = be.moe_reduce(dev(rid), dev(rw), 2, 0.05)
+    assert np.array_equal(host(gi), ref_i)
+    assert_bits_equal(host(gw), ref_w)
+    gi, gw = be.moe_reduce(rid, rw, 2, 0.05, mem=B.MEM_HOST)
+    assert np.array_equal(gi, ref_i)
+    # in place
+    ti, tw = dev(rid), dev(rw)
+    be.moe_reduce(ti, tw, 2, 0.05, out=(ti, tw))
+    assert np.array_equal(host(ti), ref_i)
+    # fused with the routing (device expf: weights within float rounding)
+    fi, fw = be.moe_route_reduce(dev(logits), rows, ne, k, 2, 0.05)
+    assert np.array_equal(host(fi), ref_i)
+    assert np.allclose(host(fw), ref_w, rtol=1e-6, atol=1e-7)
+    # the reference's own test (moe_fused.rs:338-350)
+    gi, gw = be.moe_reduce(np.int32([[0, 1, 2], [2, 1, 0]]), np.float32([[0.7, 0.2, 0.1], [0.4, 0.35, 0.25]]), 2, 0.15,
+                           mem=B.MEM_HOST)
+    assert gi.tolist() == [[0, 1, -1], [2, 1, -1]]
+    assert np.all(np.abs(gw.sum(1) - 1.0) < 1e-6)
+
+
+def test_moe_ffn_after_reduction(be, orc):
+    """The MoE step on reduced assignments (dropped slots are id -1): the
+    experts each token keeps, weighted by the renormalised weights."""
+    ne, hid, nff, rows, k = 6, 512, 1024, 40, 2
+    gates, ups, downs, x, _, _ = _moe_case(orc, ne, hid, nff, rows, k, 880)
+    logits = synth.gen_f32(rows * ne, 881).reshape(rows, ne)
+    logits[::2, 3] += 5.0
+    ids, w = orc.moe_select_top_k(logits, k)
+    ids, w = orc.moe_reduce_experts(ids, w, k, 0.05)
+    assert (ids[:, 1] < 0).sum() >= 10
+    out = be.moe_ffn(B.Q4_K, [dev(g) for g in gates], B.Q4_K, [dev(u) for u in ups], B.Q6_K, [dev(d) for d in downs],
+                     hid, nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
+    ref = orc.moe_ffn(B.Q4_K, gates, B.Q4_K, ups, B.Q6_K, downs, hid, nff, x, ids, w, orc.Q8_K)
+    assert_close_1e3(host(out), ref)
+
+
 @pytest.mark.parametrize("act", ["q8", "f32"])
 def test_moe_ffn_small(be, orc, act):
     ne, hid, nff, rows, k = 4, 512, 1024, 24, 2
@@ -323,6 +392,10 @@ MOE_CASES = {
     "decode_2_repeat": dict(ne=4, hid=256, nff=512, rows=2, k=2),
     "decode_top1": dict(ne=3, hid=512, nff=512, rows=4, k=1),
     "decode_mixed": dict(ne=3, hid=512, nff=512, rows=2, k=2, gt=B.Q6_K, ut=B.Q4_K),
+    # decode with a down projection over several 4096-element chunks, the
+    # last one partial (k = 5120 and 14336, Mixtral's n_ff)
+    "decode_long_k": dict(ne=4, hid=256, nff=5120, rows=1, k=2),
+    "decode_mixtral_nff": dict(ne=2, hid=512, nff=14336, rows=1, k=2),
 }
 
 
@@ -356,22 +429,16 @@ def test_moe_ffn_grouped_cases(be, orc, name):
         # the same step on the grouped MFMA GEMM (0) and on the grouped GEMVs
         # (2: also for more than one token, several rows per expert)
         for mode in ("0", "2"):
-            os.environ["BARQ_MOE_GEMV"] = mode
-            try:
-                out2 = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs],
-                                  hid, nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
-            finally:
-                os.environ.pop("BARQ_MOE_GEMV", None)
+            with tuned(BARQ_MOE_GEMV=mode) as b:
+                out2 = b.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs],
+                                 hid, nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
             assert_close_1e3(host(out2), ref)
     if name == "many_chunks":
         # grouping in its own launch (the path above 2048 assignments, or with
         # BARQ_MOE_FUSED_GROUP=0) gives the same rows in the same order
-        os.environ["BARQ_MOE_FUSED_GROUP"] = "0"
-        try:
-            out2 = be.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs], hid,
-                              nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
-        finally:
-            os.environ.pop("BARQ_MOE_FUSED_GROUP", None)
+        with tuned(BARQ_MOE_FUSED_GROUP=0) as b:
+            out2 = b.moe_ffn(gt, [dev(g) for g in gates], ut, [dev(u) for u in ups], dt, [dev(d) for d in downs], hid,
+                             nff, dev(x), rows, dev(ids), dev(w), k, B.ACT_F32_Q8)
         assert np.array_equal(host(out2), host(out))
 
 

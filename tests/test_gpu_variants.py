@@ -1,7 +1,8 @@
 """Every launch-shape override the kernels accept (the BARQ_GEMM_*,
-BARQ_GEMV_* and BARQ_ATTN_* tuning variables, read at each launch) against
-the oracle, in one process: the variants that measured slower stay off by
-default but must still compute the same product.  Bars as in
+BARQ_GEMV_*, BARQ_MOE_* and BARQ_ATTN_* tuning variables, read when a handle
+is created) against the oracle, in one process: each variant runs on a
+fresh handle created under its settings.  The variants that measured slower
+stay off by default but must still compute the same product.  Bars as in
 test_gpu_parity.py / test_gpu_attention.py."""
 import contextlib
 import os
@@ -24,16 +25,22 @@ def dev(a):
 
 @contextlib.contextmanager
 def env(**kv):
+    """A handle created with the tuning variables kv set (the library reads
+    them at handle creation); the environment is restored before the body."""
     old = {k: os.environ.get(k) for k in kv}
     os.environ.update({k: str(v) for k, v in kv.items()})
     try:
-        yield
+        b = B.Backend(0)
     finally:
         for k, v in old.items():
             if v is None:
                 os.environ.pop(k, None)
             else:
                 os.environ[k] = v
+    try:
+        yield b
+    finally:
+        b.close()
 
 
 GEN = {B.Q4_K: synth.gen_q4_k, B.Q6_K: synth.gen_q6_k, B.Q4_0: synth.gen_q4_0, B.Q8_0: synth.gen_q8_0}
@@ -78,14 +85,14 @@ def test_gemm_32_element_blocks(be, orc, name):
         xq = orc.quantize_act(at, x)
         ref = orc.matmul(t, w, n, k, at, xq, m)
         print(f"gemm {name} n={n} k={k} m={m} {env_v}", flush=True)
-        with env(**env_v):
-            got = be.matmul(t, dev(w), n, k, at, dev(xq), m).cpu().numpy()
+        with env(**env_v) as b:
+            got = b.matmul(t, dev(w), n, k, at, dev(xq), m).cpu().numpy()
             assert_close_1e3(got, ref)
             y = np.empty((m, n), np.float32)
-            be.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
+            b.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
             assert_close_1e3(y, ref)
             # f32 activations quantized inside the call
-            got_f = be.matmul(t, dev(w), n, k, B.ACT_F32_Q8, dev(x), m).cpu().numpy()
+            got_f = b.matmul(t, dev(w), n, k, B.ACT_F32_Q8, dev(x), m).cpu().numpy()
             assert_close_1e3(got_f, ref)
 
 
@@ -96,8 +103,8 @@ def test_gemm_variants(be, orc, w_type):
     wd, xd = dev(w), dev(xq)
     for v in GEMM_VARIANTS:
         print("gemm variant", w_type, v, flush=True)
-        with env(**v):
-            got = be.matmul(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd, m).cpu().numpy()
+        with env(**v) as b:
+            got = b.matmul(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd, m).cpu().numpy()
         assert_close_1e3(got, ref)
 
 
@@ -131,7 +138,8 @@ def test_matmul_small_m(be, orc, name):
     buffers."""
     t = getattr(B, name)
     at = B.Q8_PARTNER[t]
-    shapes = [(300, 1024), (77, 5120)]
+    # above 8192 rows the 32-element formats take another multi-token launch shape
+    shapes = [(300, 1024), (77, 5120), (8200, 512)]
     variants = [{}, dict(BARQ_GEMM_MIN_M=2, BARQ_GEMV_MULTI_MAX=0), dict(BARQ_GEMM_MIN_M=16, BARQ_GEMV_MULTI_MAX=0)]
     for n, k in shapes:
         w = synth.gen_weights(t, n, k, 820)
@@ -142,10 +150,10 @@ def test_matmul_small_m(be, orc, name):
             ref = orc.matmul(t, w, n, k, at, xq, m)
             for env_v in variants:
                 print(f"small m {name} n={n} k={k} m={m} {env_v}", flush=True)
-                with env(**env_v):
-                    assert_close_1e3(be.matmul(t, wd, n, k, at, dev(xq), m).cpu().numpy(), ref)
+                with env(**env_v) as b:
+                    assert_close_1e3(b.matmul(t, wd, n, k, at, dev(xq), m).cpu().numpy(), ref)
                     y = np.empty((m, n), np.float32)
-                    be.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
+                    b.matmul_raw(t, w, n, k, at, xq, m, y, B.MEM_HOST)
                     assert_close_1e3(y, ref)
 
 
@@ -162,8 +170,8 @@ def test_gemv_variants(be, orc, w_type):
     wd, xd = dev(w), dev(xq)
     for v in GEMV_VARIANTS:
         print("gemv variant", w_type, v, flush=True)
-        with env(**v):
-            got = be.matvec(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd).cpu().numpy()
+        with env(**v) as b:
+            got = b.matvec(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd).cpu().numpy()
         assert_close_1e3(got, ref.ravel())
 
 
@@ -183,9 +191,9 @@ def test_moe_variants(be, orc):
     gd, ud, dd = [dev(a) for a in gates], [dev(a) for a in ups], [dev(a) for a in downs]
     for v in MOE_VARIANTS:
         print("moe variant", v, flush=True)
-        with env(**v):
-            got = be.moe_ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, hid, nff, dev(x), rows, dev(ids), dev(w), k,
-                             B.ACT_F32_Q8).cpu().numpy()
+        with env(**v) as b:
+            got = b.moe_ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, hid, nff, dev(x), rows, dev(ids), dev(w), k,
+                            B.ACT_F32_Q8).cpu().numpy()
         assert_close_1e3(got, ref)
 
 
@@ -200,7 +208,7 @@ def test_attention_split_variants(be, orc):
     ref = orc.attention(q, k, v, n_head, 2, kv, kv - 2)
     for wg in (1, 8, 64, 256, 4096):
         print("attention workgroup target", wg, flush=True)
-        with env(BARQ_ATTN_WG=wg):
-            got = A.compute_attention(be, q, c, 0, n_head, n_kv, hd, 2, kv, kv - 2, mem=B.MEM_HOST)
+        with env(BARQ_ATTN_WG=wg) as b:
+            got = A.compute_attention(b, q, c, 0, n_head, n_kv, hd, 2, kv, kv - 2, mem=B.MEM_HOST)
         assert np.max(np.abs(got - ref)) <= 2e-5 * np.max(np.abs(v))
     c.close()

@@ -168,6 +168,29 @@ def test_split_quantized_matmul_reference_test(orc):
     assert c.size == 4 and c.reshape(-1).tolist() == [3.0, 3.0, 7.0, 7.0]
 
 
+@pytest.mark.parametrize("bs", [5, 7, 3])
+def test_split_packed_4bit_odd_block_size_placement(orc, bs):
+    # cuda_quant.rs:44-75: block b's quants start div_ceil(bs, 2) bytes after
+    # block b-1's; an odd block leaves the high nibble of its last byte unused.
+    # One nibble at a time is set to 3: it must land on exactly the element the
+    # byte-to-element map gives (or on none for the padding nibble), scaled by
+    # its block's scale.  A stride of bs // 2 bytes fails this.
+    n_blocks = 4
+    stride = (bs + 1) // 2
+    n_out = n_blocks * bs
+    scales = np.float32([1.0, 2.0, -0.5, 4.0])
+    for j in range(n_blocks * stride):
+        for shift in (0, 4):
+            q = np.zeros(n_blocks * stride, np.uint8)
+            q[j] = 3 << shift
+            out = orc.dequantize_split(False, q, scales, bs, n_out)
+            b, rel = j // stride, 2 * (j % stride) + shift // 4
+            expect = np.zeros(n_out, np.float32)
+            if rel < bs:
+                expect[b * bs + rel] = 3.0 * scales[b]
+            assert np.array_equal(out, expect), (bs, j, shift)
+
+
 def test_split_uncovered_outputs_are_zero(orc):
     out = orc.dequantize_split(True, np.int8([1, -2, 3]).view(np.uint8), np.float32([2.0]), 4, 10)
     assert out.tolist() == [2.0, -4.0, 6.0] + [0.0] * 7
@@ -202,6 +225,65 @@ def test_select_top_k_ties_keep_index_order_and_clamp(orc):
     assert ids.tolist() == [[1]]
 
 
+def test_reduce_experts_threshold_cap_and_renormalisation(orc):
+    # moe_fused.rs:147-194, checked against closed forms rather than a retyped loop
+    w = np.float32([[0.5, 0.3, 0.15, 0.05]])
+    ids = np.int32([[3, 1, 0, 2]])
+    # nothing below the threshold, cap above k: order kept, weights unchanged up to the
+    # division by their float sum (exactly 1.0 here)
+    oi, ow = orc.moe_reduce_experts(ids, w, 8, 0.0)
+    assert oi.tolist() == [[3, 1, 0, 2]]
+    assert np.float32(np.float32(np.float32(0.5 + np.float32(0.3)) + np.float32(0.15)) + np.float32(0.05)) == 1.0
+    assert np.array_equal(ow, w)
+    # the threshold drops the last two, the rest renormalise to 0.5/0.8, 0.3/0.8
+    oi, ow = orc.moe_reduce_experts(ids, w, 8, 0.1)
+    assert oi.tolist() == [[3, 1, 0, -1]]
+    assert ow[0, 3] == 0.0
+    oi, ow = orc.moe_reduce_experts(ids, w, 2, 0.1)          # the cap keeps the two largest
+    assert oi.tolist() == [[3, 1, -1, -1]]
+    assert np.allclose(ow[0, :2], [0.625, 0.375], rtol=1e-6, atol=0)
+    oi, ow = orc.moe_reduce_experts(ids, w, 0, 0.0)          # max_active 0 keeps one (.max(1))
+    assert oi.tolist() == [[3, -1, -1, -1]] and ow[0, 0] == 1.0
+
+
+def test_reduce_experts_sorts_descending_and_stable(orc):
+    # unsorted input is sorted by weight, equal weights keep slot order
+    ids = np.int32([[4, 7, 2, 9, 5]])
+    w = np.float32([[0.1, 0.3, 0.2, 0.3, 0.1]])
+    oi, ow = orc.moe_reduce_experts(ids, w, 5, 0.0)
+    assert oi.tolist() == [[7, 9, 2, 4, 5]]
+    assert np.all(np.diff(ow[0]) <= 0)
+
+
+def test_reduce_experts_all_below_threshold_keeps_the_last_maximum(orc):
+    # Iterator::max_by returns the last of equal maxima (moe_fused.rs:165-171)
+    ids = np.int32([[1, 2, 3], [6, 5, 4]])
+    w = np.float32([[0.02, 0.04, 0.04], [0.03, 0.01, 0.02]])
+    oi, ow = orc.moe_reduce_experts(ids, w, 2, 0.05)
+    assert oi.tolist() == [[3, -1, -1], [6, -1, -1]]
+    assert ow[:, 0].tolist() == [1.0, 1.0]
+
+
+def test_reduce_experts_absent_slots_and_alias(orc):
+    ids = np.int32([[-1, 2, -1, 0]])
+    w = np.float32([[0.9, 0.3, 0.9, 0.7]])    # weights of absent slots are ignored
+    oi, ow = orc.moe_reduce_experts(ids, w, 4, 0.0)
+    assert oi.tolist() == [[0, 2, -1, -1]]
+    assert np.allclose(ow, [[0.7, 0.3, 0.0, 0.0]], rtol=1e-6)
+    oi2, ow2 = orc.moe_reduce_experts(oi, ow, 4, 0.0)        # reducing again changes nothing
+    assert np.array_equal(oi2, oi) and np.allclose(ow2, ow, rtol=1e-6)
+
+
+def test_reduce_experts_sum_is_floored_at_epsilon(orc):
+    ids = np.int32([[0, 1]])
+    w = np.float32([[0.0, 0.0]])
+    oi, ow = orc.moe_reduce_experts(ids, w, 2, 0.0)
+    assert oi.tolist() == [[0, 1]] and ow.tolist() == [[0.0, 0.0]]
+    w = np.float32([[1e-8, 0.0]])              # 1e-8 / EPSILON, not 1e-8 / 1e-8
+    oi, ow = orc.moe_reduce_experts(ids, w, 2, 0.0)
+    assert ow[0, 0] == np.float32(np.float32(1e-8) / np.float32(1.1920929e-7))
+
+
 def test_batch_by_expert(orc):
     ids = np.int32([[1, 0], [1, 2], [0, 1]])
     w = np.float32([[0.6, 0.4], [0.7, 0.3], [0.5, 0.5]])
@@ -232,6 +314,41 @@ def test_dispatch_matches_naive_per_token(orc):
     assert np.allclose(out, naive, atol=1e-6)
 
 
+def test_moe_ffn_q8k_equals_dispatch_with_quantized_ffn(orc):
+    # orc_moe_ffn (act Q8_K, the GPU's integer path) == dispatch_experts with an
+    # expert built from independent pieces: Q8_K rows by quantize_q8_k, the
+    # Q8_K matmul, SiLU as ops.rs:191-211 computes it (x / (1 + exp(-x)), with
+    # the same libm expf the oracle links), the up product, Q8_K again, down.
+    # Bit-equal.
+    import ctypes
+    from barq_rocm import synth
+    import barq_rocm as B
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    ne, hid, nff, rows = 3, 256, 512, 5
+    gates = [synth.gen_q4_k(nff, hid, 110 + e) for e in range(ne)]
+    ups = [synth.gen_q4_k(nff, hid, 120 + e) for e in range(ne)]
+    downs = [synth.gen_q6_k(hid, nff, 130 + e) for e in range(ne)]
+    x = synth.gen_f32(rows * hid, 140).reshape(rows, hid)
+    ids, w = orc.moe_select_top_k(synth.gen_f32(rows * ne, 141).reshape(rows, ne), 2)
+    out = orc.moe_ffn(B.Q4_K, gates, B.Q4_K, ups, B.Q6_K, downs, hid, nff, x, ids, w, orc.Q8_K)
+
+    def ffn(e):
+        def f(a):
+            r = a.shape[0]
+            xq = np.concatenate([orc.quantize_q8_k(a[i]) for i in range(r)])
+            g = orc.matmul(B.Q4_K, gates[e], nff, hid, orc.Q8_K, xq, r).reshape(-1)
+            u = orc.matmul(B.Q4_K, ups[e], nff, hid, orc.Q8_K, xq, r).reshape(-1)
+            ex = np.float32([libm.expf(float(-v)) for v in g])
+            h = (g / (np.float32(1.0) + ex)) * u
+            hq = np.concatenate([orc.quantize_q8_k(h[i * nff:(i + 1) * nff]) for i in range(r)])
+            return orc.matmul(B.Q6_K, downs[e], hid, nff, orc.Q8_K, hq, r)
+        return f
+    ref = orc.moe_dispatch(x, ne, ids, w, [ffn(e) for e in range(ne)])
+    assert np.array_equal(out.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
 def test_moe_ffn_literal_equals_dispatch_with_fused_ffn(orc):
     # orc_moe_ffn (act f32) == dispatch_experts with fused_ffn built from the
     # oracle's matmul and the elementwise SiLU*up, computed independently
@@ -255,3 +372,38 @@ def test_moe_ffn_literal_equals_dispatch_with_fused_ffn(orc):
         return f
     ref = orc.moe_dispatch(x, ne, ids, w, [ffn(e) for e in range(ne)])
     assert_close_1e3(out, ref, tol=1e-5)
+
+
+# ---- the timed CPU baseline (oracle/cpu_baseline.c) is the reference arithmetic ----
+
+def test_cpu_baseline_literal_equals_gemm_f32(orc):
+    # variant (i), blas.rs:199-210 at M = 1: bit-exact with the oracle's gemm_f32
+    rng = np.random.default_rng(3)
+    k, n = 640, 300
+    x = rng.standard_normal(k).astype(np.float32)
+    w_t = rng.standard_normal((k, n)).astype(np.float32)
+    y = np.zeros(n, np.float32)
+    orc.cpub_gemm_literal_m1(x, w_t, k, n, 0, 170, y)
+    orc.cpub_gemm_literal_m1(x, w_t, k, n, 170, n, y)
+    ref = orc.gemm_f32(x, w_t.reshape(-1), 1, k, n).reshape(-1)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_cpu_baseline_simd_dot_matches_gemv_f32(orc, threads):
+    # variants (ii)/(iii), simd.rs:115-168: an FMA-blocked dot, so equal to the
+    # sequential gemv_f32 only to float rounding; the threaded form computes
+    # the same rows bit for bit
+    rng = np.random.default_rng(4)
+    m, n = 257, 1000            # n not a multiple of the vector width: the scalar tail runs
+    a = rng.standard_normal((m, n)).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    ref = orc.gemv_f32(a.reshape(-1), x, m, n)
+    y1 = np.zeros(m, np.float32)
+    orc.cpub_gemv_simd(a, x, n, 0, m, y1)
+    bound = 4 * n * np.finfo(np.float32).eps * (np.abs(a) @ np.abs(x))
+    assert np.all(np.abs(y1.astype(np.float64) - ref) <= bound)
+    y2 = np.zeros(m, np.float32)
+    used = orc.cpub_gemv_simd_threaded(a, x, n, 0, m, y2, threads)
+    assert used == threads
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
