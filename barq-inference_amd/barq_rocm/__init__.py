@@ -8,14 +8,14 @@ inputs of the benchmark configurations (synth).
 """
 from . import _lib
 from ._lib import (ACT_F32, ACT_F32_Q8, BLOCK_BYTES, BLOCK_ELEMS, E_BACKEND, E_DIM, E_INVALID, E_QUANT,
-                   E_UNSUPPORTED, F16, F32, MEM_DEVICE, MEM_HOST, Q4_0, Q4_0_BARQ, Q4_K,
+                   E_UNSUPPORTED, F16, F32, MEM_DEVICE, MEM_HOST, NOALLOC_SCRATCH_BYTES, Q4_0, Q4_0_BARQ, Q4_K,
                    Q4_K_BARQ, Q6_K, Q8_0, Q8_K, Q8_PARTNER, BarqError)
 from .backend import Backend
 
 __all__ = [
     "_lib", "Backend", "BarqError", "ACT_F32", "ACT_F32_Q8", "BLOCK_BYTES", "BLOCK_ELEMS", "F16", "F32",
     "MEM_DEVICE", "MEM_HOST", "Q4_0", "Q4_0_BARQ", "Q4_K", "Q4_K_BARQ", "Q6_K", "Q8_0", "Q8_K", "Q8_PARTNER",
-    "E_BACKEND", "E_DIM", "E_INVALID", "E_QUANT", "E_UNSUPPORTED",
+    "E_BACKEND", "E_DIM", "E_INVALID", "E_QUANT", "E_UNSUPPORTED", "NOALLOC_SCRATCH_BYTES",
 ]
 
 

@@ -64,7 +64,11 @@ EXPORTS = (
     "barq_rocm_rope", "barq_rocm_transpose_heads", "barq_rocm_kv_cache_create", "barq_rocm_kv_cache_append",
     "barq_rocm_kv_cache_append_rope", "barq_rocm_kv_cache_size", "barq_rocm_kv_cache_layer_len",
     "barq_rocm_kv_cache_head", "barq_rocm_kv_cache_clear", "barq_rocm_kv_cache_destroy", "barq_rocm_attention",
+    "barq_rocm_matmul_noalloc",
 )
+
+# bytes of the fixed per-GPU scratch behind barq_rocm_matmul_noalloc
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 ROPE_INTERLEAVED = 0
 ROPE_SPLIT_HALF = 1
@@ -143,6 +147,7 @@ def _declare(lib):
         "barq_rocm_kv_cache_clear": (_i, [_vp]),
         "barq_rocm_kv_cache_destroy": (_i, [_vp]),
         "barq_rocm_attention": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _i]),
+        "barq_rocm_matmul_noalloc": (_i, [_vp, _i, _vp, _sz, _sz, _i, _vp, _sz, _vp]),
     }
     for name, (res, args) in P.items():
         fn = getattr(lib, name)

@@ -72,6 +72,10 @@ class Backend:
     def matmul_raw(self, w_type, w, n_rows, k, act_type, x, m, y, mem):
         L.check(self._lib.barq_rocm_matmul(self.h, w_type, _ptr(w), n_rows, k, act_type, _ptr(x), m, _ptr(y), mem))
 
+    def matmul_noalloc_raw(self, w_type, w, n_rows, k, act_type, x, m, y):
+        """barq_rocm_matmul_noalloc: device buffers, the fixed per-GPU scratch."""
+        L.check(self._lib.barq_rocm_matmul_noalloc(self.h, w_type, _ptr(w), n_rows, k, act_type, _ptr(x), m, _ptr(y)))
+
     # ---- torch-tensor conveniences (device memory) ----------------------
     def dequantize(self, type_, blocks, n, sync=True):
         import torch

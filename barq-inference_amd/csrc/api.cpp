@@ -136,6 +136,7 @@ int barq_rocm_create(int device, barq_rocm_handle** out) {
         return fail(BARQ_E_UNSUPPORTED, "device %d is %s; libbarq_rocm is built for gfx950 only", device, prop.gcnArchName);
     DeviceGuard g(device);
     if (hipSetDevice(device) != hipSuccess) return fail(BARQ_E_BACKEND, "hipSetDevice(%d) failed", device);
+    if (const int rc = barq::noalloc_init(device)) return rc;
     auto* h = new barq_rocm_handle();
     h->device = device;
     h->tuning = barq::Tuning::from_env();

@@ -102,3 +102,8 @@ struct DeviceGuard {
 
 }  // namespace barq_api
 
+namespace barq {
+// Looks up, once per device, the device address of the fixed scratch array
+// behind barq_rocm_matmul_noalloc (the device must be current).
+int noalloc_init(int device);
+}  // namespace barq

@@ -369,6 +369,25 @@ int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_
                         size_t n_head, size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len,
                         size_t start_pos, float* out, int mem);
 
+/* ---- matmul without allocation -------------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc.  Same product, dispatch and results as barq_rocm_matmul with
+ * mem = BARQ_MEM_DEVICE (all buffers are device pointers), but its scratch
+ * (activation rows quantized in the call for BARQ_ACT_F32_Q8, the
+ * 32-element-block GEMM's repacked rows, K-slice partial products, the
+ * literal f32 path's dequantized weights) is a fixed array of
+ * BARQ_NOALLOC_SCRATCH_BYTES per GPU, set up by barq_rocm_create, instead of
+ * the handle's growable workspace.  A call that needs more scratch fails
+ * with BARQ_E_UNSUPPORTED before anything is enqueued.  Calls allocate
+ * nothing.  Every no-allocation call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (other streams, other handles, other
+ * threads) race on it and must be ordered by the caller. */
+#define BARQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+int barq_rocm_matmul_noalloc(barq_rocm_handle* h, int w_type, const void* w,
+                             size_t n_rows, size_t k, int act_type, const void* x,
+                             size_t m, float* y);
+
 #ifdef __cplusplus
 }
 #endif
