@@ -137,6 +137,37 @@ class Backend:
             self.sync()
         return y
 
+    def swiglu(self, out_type, gate, up, mem=L.MEM_DEVICE, sync=True):
+        """The dense FFN's SwiGLU (transformer.rs:394-399) of gate/up [rows, n]:
+        f32 h (out_type F32) or its Q8_K / Q8_0 blocks."""
+        rows, n = tuple(gate.shape)
+        nbytes = rows * (n * 4 if out_type == L.F32 else n // L.BLOCK_ELEMS[out_type] * L.BLOCK_BYTES[out_type])
+        if mem == L.MEM_HOST:
+            out = np.empty((rows, n), np.float32) if out_type == L.F32 else np.empty(nbytes, np.uint8)
+        else:
+            import torch
+            out = (torch.empty((rows, n), dtype=torch.float32, device=gate.device) if out_type == L.F32
+                   else torch.empty(nbytes, dtype=torch.uint8, device=gate.device))
+        L.check(self._lib.barq_rocm_swiglu(self.h, out_type, _ptr(gate), _ptr(up), rows, n, _ptr(out), mem))
+        if mem == L.MEM_DEVICE and sync:
+            self.sync()
+        return out
+
+    def ffn(self, gate_type, gate, up_type, up, down_type, down, n_embd, n_ff, act, x, m, mem=L.MEM_DEVICE,
+            sync=True, out=None):
+        """LlamaTransformer::feed_forward (transformer.rs:378-408) of m rows."""
+        if out is None:
+            if mem == L.MEM_HOST:
+                out = np.empty((m, n_embd), np.float32)
+            else:
+                import torch
+                out = torch.empty((m, n_embd), dtype=torch.float32, device=x.device)
+        L.check(self._lib.barq_rocm_ffn(self.h, gate_type, _ptr(gate), up_type, _ptr(up), down_type, _ptr(down),
+                                        n_embd, n_ff, act, _ptr(x), m, _ptr(out), mem))
+        if mem == L.MEM_DEVICE and sync:
+            self.sync()
+        return out
+
     def gemm_f32(self, a, b, m, k, n, mem=L.MEM_DEVICE):
         if mem == L.MEM_HOST:
             c = np.empty((m, n), dtype=np.float32)

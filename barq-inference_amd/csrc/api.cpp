@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -458,6 +459,145 @@ int barq_rocm_matvec(barq_rocm_handle* h, int w_type, const void* w, size_t n_ro
 int barq_rocm_matmul(barq_rocm_handle* h, int w_type, const void* w, size_t n_rows, size_t k, int act_type,
                      const void* x, size_t m, float* y, int mem) {
     return matmul_any(h, w_type, w, n_rows, k, act_type, x, m, y, mem, "matmul");
+}
+
+// ---------------------------------------------------------------------------
+// dense FFN (LlamaTransformer::feed_forward, transformer.rs:378-408)
+
+int barq_rocm_swiglu(barq_rocm_handle* h, int out_type, const float* gate, const float* up, size_t rows, size_t n,
+                     void* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (out_type != BARQ_TYPE_F32 && out_type != BARQ_TYPE_Q8_K && out_type != BARQ_TYPE_Q8_0)
+        return fail(BARQ_E_UNSUPPORTED, "swiglu: out_type must be F32, Q8_K or Q8_0, got %d", out_type);
+    if (rows == 0 || n == 0) return ok();
+    if (out_type != BARQ_TYPE_F32 && n % blk_elems(out_type))
+        return fail(BARQ_E_QUANT, "swiglu: n=%zu is not a multiple of %zu", n, blk_elems(out_type));
+    if (!gate || !up || !out) return fail(BARQ_E_INVALID, "swiglu: null buffer");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    const size_t out_bytes = rows * (out_type == BARQ_TYPE_F32 ? n * 4 : row_bytes_of(out_type, n));
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(out, out_type == BARQ_TYPE_Q8_0 ? 2 : 4))
+            return fail(BARQ_E_INVALID, "swiglu: gate/up must be 16-byte aligned, out %d-byte",
+                        out_type == BARQ_TYPE_Q8_0 ? 2 : 4);
+        return launched(barq::ffn_swiglu_launch(out_type, gate, up, rows, n, out, h->stream), "swiglu");
+    }
+    Arena a;
+    const size_t og = a.add(rows * n * 4), ou = a.add(rows * n * 4), oo = a.add(out_bytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, og), gate, rows * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ou), up, rows * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::ffn_swiglu_launch(out_type, at<float>(h, og), at<float>(h, ou), rows, n, at<uint8_t>(h, oo),
+                                                h->stream), "swiglu"));
+    BARQ_HIP(hipMemcpyAsync(out, at<uint8_t>(h, oo), out_bytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+namespace {
+
+// Workspace of a device FFN call, from offset `base`: the input rows
+// quantized here, g and u (m x n_ff f32 each; h in f32 reuses g), h's
+// quantized rows, then scratch for the three projections.
+struct FfnArena {
+    size_t xq, g, u, hq, mm, end;
+};
+
+FfnArena ffn_arena(size_t base, int gt, int ut, int dt, size_t n_embd, size_t n_ff, int act, size_t m) {
+    Arena a;
+    a.used = base;
+    FfnArena L;
+    const bool lit = act == BARQ_ACT_F32;
+    L.xq = a.add(act == BARQ_ACT_F32_Q8 ? m * row_bytes_of(q8_partner(gt), n_embd) : 0);
+    L.g = a.add(m * n_ff * 4);
+    L.u = a.add(m * n_ff * 4);
+    L.hq = a.add(lit ? 0 : m * row_bytes_of(q8_partner(dt), n_ff));
+    const int pa = lit ? BARQ_ACT_F32 : q8_partner(gt), pd = lit ? BARQ_ACT_F32 : q8_partner(dt);
+    size_t mm = matmul_scratch(gt, n_ff, n_embd, pa, m);
+    mm = std::max(mm, matmul_scratch(ut, n_ff, n_embd, pa, m));
+    mm = std::max(mm, matmul_scratch(dt, n_embd, n_ff, pd, m));
+    L.mm = a.add(mm);
+    L.end = a.used;
+    return L;
+}
+
+int ffn_dev(barq_rocm_handle* h, int gt, const void* gate, int ut, const void* up, int dt, const void* down,
+            size_t n_embd, size_t n_ff, int act, const void* x, size_t m, float* out, size_t base) {
+    hipStream_t s = h->stream;
+    const FfnArena L = ffn_arena(base, gt, ut, dt, n_embd, n_ff, act, m);
+    BARQ_CHECK(ensure_ws(h, L.end));
+    float* g = at<float>(h, L.g);
+    float* u = at<float>(h, L.u);
+    uint8_t* mm = at<uint8_t>(h, L.mm);
+    if (act == BARQ_ACT_F32) {
+        // the literal f32 arithmetic: f32 projections, f32 SwiGLU, f32 down
+        BARQ_CHECK(matmul_dev(h, gt, gate, n_ff, n_embd, BARQ_ACT_F32, x, m, g, mm));
+        BARQ_CHECK(matmul_dev(h, ut, up, n_ff, n_embd, BARQ_ACT_F32, x, m, u, mm));
+        BARQ_CHECK(launched(barq::ffn_swiglu_launch(BARQ_TYPE_F32, g, u, m, n_ff, g, s), "swiglu"));
+        return matmul_dev(h, dt, down, n_embd, n_ff, BARQ_ACT_F32, g, m, out, mm);
+    }
+    const int pa = q8_partner(gt), pd = q8_partner(dt);
+    const void* xq = x;
+    if (act == BARQ_ACT_F32_Q8) {
+        if (!aligned(x, 16)) return fail(BARQ_E_INVALID, "ffn: f32 activations must be 16-byte aligned");
+        BARQ_CHECK(launched(quantize_act_dev(pa, static_cast<const float*>(x), m, n_embd, at<uint8_t>(h, L.xq), s),
+                            "quantize_act"));
+        xq = at<uint8_t>(h, L.xq);
+    }
+    uint8_t* hq = at<uint8_t>(h, L.hq);
+    if (m == 1 && gt == ut && barq::gemv_glu_supported(gt, gate, up, n_ff, n_embd)) {
+        // gate and up in one launch, SwiGLU in its epilogue
+        BARQ_CHECK(launched(barq::gemv_glu_launch(gt, gate, up, n_ff, n_embd, xq, g, s), "gemv_glu"));
+        BARQ_CHECK(launched(quantize_act_dev(pd, g, 1, n_ff, hq, s), "quantize_act"));
+    } else {
+        BARQ_CHECK(matmul_dev(h, gt, gate, n_ff, n_embd, pa, xq, m, g, mm));
+        BARQ_CHECK(matmul_dev(h, ut, up, n_ff, n_embd, pa, xq, m, u, mm));
+        BARQ_CHECK(launched(barq::ffn_swiglu_launch(pd, g, u, m, n_ff, hq, s), "swiglu"));
+    }
+    return matmul_dev(h, dt, down, n_embd, n_ff, pd, hq, m, out, mm);
+}
+
+}  // namespace
+
+int barq_rocm_ffn(barq_rocm_handle* h, int gate_type, const void* gate, int up_type, const void* up, int down_type,
+                  const void* down, size_t n_embd, size_t n_ff, int act, const void* x, size_t m, float* out,
+                  int mem) {
+    BARQ_CHECK(check_mem(mem));
+    const bool quantized_in = act == BARQ_TYPE_Q8_0 || act == BARQ_TYPE_Q8_K;
+    if (act != BARQ_ACT_F32 && act != BARQ_ACT_F32_Q8 && !quantized_in)
+        return fail(BARQ_E_UNSUPPORTED, "ffn: act must be BARQ_ACT_F32, BARQ_ACT_F32_Q8, Q8_0 or Q8_K, got %d", act);
+    BARQ_CHECK(check_linear(gate_type, n_embd, quantized_in ? act : BARQ_ACT_F32, "ffn gate"));
+    BARQ_CHECK(check_linear(up_type, n_embd, quantized_in ? act : BARQ_ACT_F32, "ffn up"));
+    BARQ_CHECK(check_linear(down_type, n_ff, BARQ_ACT_F32, "ffn down"));
+    if (act != BARQ_ACT_F32 && q8_partner(gate_type) != q8_partner(up_type))
+        return fail(BARQ_E_UNSUPPORTED, "ffn: gate and up weights must share an activation type");
+    if (act != BARQ_ACT_F32 && row_bytes_of(q8_partner(down_type), n_ff) == 0)
+        return fail(BARQ_E_QUANT, "ffn: n_ff=%zu is not a multiple of the down input's block", n_ff);
+    if (m == 0 || n_embd == 0 || n_ff == 0) return ok();
+    if (!gate || !up || !down || !x || !out) return fail(BARQ_E_INVALID, "ffn: null buffer");
+    if (n_embd > (size_t)INT32_MAX || n_ff > (size_t)INT32_MAX) return fail(BARQ_E_DIM, "ffn: dimensions exceed 2^31");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(out, 4)) return fail(BARQ_E_INVALID, "ffn: output must be 4-byte aligned");
+        return ffn_dev(h, gate_type, gate, up_type, up, down_type, down, n_embd, n_ff, act, x, m, out, 0);
+    }
+    const size_t gb = n_ff * row_bytes_of(gate_type, n_embd), ub = n_ff * row_bytes_of(up_type, n_embd),
+                 db = n_embd * row_bytes_of(down_type, n_ff);
+    const size_t xb = m * (quantized_in ? row_bytes_of(act, n_embd) : n_embd * 4), ob = m * n_embd * 4;
+    Arena a;
+    const size_t og = a.add(gb), ou = a.add(ub), od = a.add(db), ox = a.add(xb), oo = a.add(ob);
+    const FfnArena L = ffn_arena(a.used, gate_type, up_type, down_type, n_embd, n_ff, act, m);
+    BARQ_CHECK(ensure_ws(h, L.end));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, og), gate, gb, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ou), up, ub, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, od), down, db, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, ox), x, xb, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(ffn_dev(h, gate_type, at<uint8_t>(h, og), up_type, at<uint8_t>(h, ou), down_type, at<uint8_t>(h, od),
+                       n_embd, n_ff, act, at<uint8_t>(h, ox), m, at<float>(h, oo), a.used));
+    BARQ_HIP(hipMemcpyAsync(out, at<float>(h, oo), ob, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
 }
 
 // ---------------------------------------------------------------------------

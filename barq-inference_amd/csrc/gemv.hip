@@ -85,6 +85,63 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
     }
 }
 
+// The SwiGLU of LlamaTransformer::feed_forward (transformer.rs:394-399):
+// (g * (1 / (1 + exp(-g)))) * u, each operation rounded as written.
+__device__ __forceinline__ float ffn_swiglu(float g, float u) {
+    return (g * (1.0f / (1.0f + expf(-g)))) * u;
+}
+
+// Gate and up projections of one activation row in one launch, with the
+// SwiGLU applied in the epilogue: h[i] = swiglu(G[i] . x, U[i] . x).  A wave
+// owns P consecutive outputs and loads the P gate rows and the P up rows
+// (2P rows in flight, as R = 2P rows of gemv_q8_kernel); the partial sums
+// fold as (g0, u0, g1, u1) through reduce4, so g_i and u_i meet in one lane
+// with one cross-half exchange.  Reading both matrices in one launch pays
+// the ramp-up and drain of a memory-bound kernel once for both.
+template <class F, int P, int WAVES, bool ONE>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q8_glu_kernel(const uint8_t* __restrict__ G, const uint8_t* __restrict__ U, size_t row_bytes,
+                        const uint8_t* __restrict__ xq, float* __restrict__ h, int n_rows, int k) {
+    static_assert(P == 1 || P == 2, "one or two outputs per wave");
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (wg_rows_remap<P * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * P;
+    if (row0 >= n_rows) return;
+    const typename F::Lane c = F::lane(l);
+    const int nblk = k / F::ROW_BLOCK_ELEMS;
+    const int n_it = ONE ? 1 : (k + 4095) / 4096;
+    const int last = n_rows - 1 - row0;
+    const uint8_t* grow = G + (size_t)row0 * row_bytes;
+    const uint8_t* urow = U + (size_t)row0 * row_bytes;
+
+    float acc[2 * P];   // g0, u0, g1, u1
+    #pragma unroll
+    for (int r = 0; r < 2 * P; r++) acc[r] = 0.0f;
+
+    for (int it = 0; it < n_it; it++) {
+        if (F::active(it, c, nblk)) {
+            typename F::X xs;
+            F::load_x(xs, xq, it, c, nblk);
+            typename F::Wt w[2 * P];
+            #pragma unroll
+            for (int p = 0; p < P; p++) {
+                const size_t off = (size_t)min(p, last) * row_bytes;
+                F::load_w(w[2 * p], grow + off, it, c, nblk);
+                F::load_w(w[2 * p + 1], urow + off, it, c, nblk);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            #pragma unroll
+            for (int r = 0; r < 2 * P; r++) acc[r] += F::dot(w[r], xs, c);
+        }
+    }
+
+    // lane 0: g0, lane 32: u0, lane 16: g1, lane 48: u1
+    const float v = reduce4(acc[0], acc[1], P > 1 ? acc[2] : 0.0f, P > 1 ? acc[3] : 0.0f);
+    const float other = __shfl_xor(v, 32);
+    if (l == 0) h[row0] = ffn_swiglu(v, other);
+    if (P > 1 && l == 16 && last >= 1) h[row0 + 1] = ffn_swiglu(v, other);
+}
+
 // A few activation rows (2-4 tokens of a small decode batch): each wave's
 // weight slices are loaded once per chunk and dotted with every row's
 // activation slice, so the weights are read once instead of once per token.
@@ -426,6 +483,42 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
     }
 }
 
+
+bool gemv_glu_supported(int w_type, const void* G, const void* U, size_t n_rows, size_t k) {
+    return w_type == TYPE_Q4_K && k % 256 == 0 && k > 0 && n_rows > 0 && n_rows <= (size_t)INT32_MAX &&
+           (reinterpret_cast<uintptr_t>(G) & 15) == 0 && (reinterpret_cast<uintptr_t>(U) & 15) == 0;
+}
+
+template <int P, int WAVES>
+static hipError_t launch_glu(const uint8_t* G, const uint8_t* U, size_t rb, const uint8_t* x, float* h, int n, int k,
+                             hipStream_t s) {
+    const unsigned grid = (unsigned)((n + P * WAVES - 1) / (P * WAVES));
+    if (k <= 4096)
+        hipLaunchKernelGGL((gemv_q8_glu_kernel<FmtQ4K, P, WAVES, true>), dim3(grid), dim3(WAVES * 64), 0, s, G, U, rb,
+                           x, h, n, k);
+    else
+        hipLaunchKernelGGL((gemv_q8_glu_kernel<FmtQ4K, P, WAVES, false>), dim3(grid), dim3(WAVES * 64), 0, s, G, U, rb,
+                           x, h, n, k);
+    return hipGetLastError();
+}
+
+hipError_t gemv_glu_launch(int w_type, const void* G, const void* U, size_t n_rows, size_t k, const void* xq, float* h,
+                           hipStream_t s) {
+    if (!gemv_glu_supported(w_type, G, U, n_rows, k)) return hipErrorInvalidValue;
+    const uint8_t* g = static_cast<const uint8_t*>(G);
+    const uint8_t* u = static_cast<const uint8_t*>(U);
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+    const size_t rb = k / 256 * 144;
+    const int n = (int)n_rows, kk = (int)k;
+    // BARQ_GEMV_GLU = 10 * P + W: P outputs per wave (1 or 2), W waves (2, 4, 8)
+    const int t = tuning_env(TUNE_GEMV_GLU, 14);
+    const int p = t / 10 == 2 ? 2 : 1;
+    const int w = t % 10 == 2 || t % 10 == 8 ? t % 10 : 4;
+    if (p == 2) return w == 2 ? launch_glu<2, 2>(g, u, rb, x, h, n, kk, s) : w == 8 ? launch_glu<2, 8>(g, u, rb, x, h, n, kk, s)
+                                                                                   : launch_glu<2, 4>(g, u, rb, x, h, n, kk, s);
+    return w == 2 ? launch_glu<1, 2>(g, u, rb, x, h, n, kk, s) : w == 8 ? launch_glu<1, 8>(g, u, rb, x, h, n, kk, s)
+                                                                       : launch_glu<1, 4>(g, u, rb, x, h, n, kk, s);
+}
 
 hipError_t gemv_f32_launch(int w_type, const void* W, size_t n_rows, size_t k, const float* x,
                            float* y, hipStream_t s) {

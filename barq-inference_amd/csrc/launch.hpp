@@ -22,8 +22,13 @@ hipError_t quantize_q4_k_barq_launch(const float* x, size_t n, uint8_t* out, hip
 // Q8_K rows of x[rows_idx[i] * k ..] for i < n_rows (gather fused in)
 hipError_t quantize_q8_k_gather_launch(const float* x, const int32_t* rows_idx, size_t n_rows, size_t k, void* out,
                                        hipStream_t s);
-// Q8_K rows of silu(g) * u (k-element rows; the product is not stored)
+// Q8_K rows of silu(g) * u with ops::Silu's rounding (the MoE expert FFN;
+// k-element rows; the product is not stored)
 hipError_t swiglu_q8_k_launch(const float* g, const float* u, size_t n_rows, size_t k, void* out, hipStream_t s);
+// The dense FFN's SwiGLU (transformer.rs:394-399) of n_rows rows of n:
+// out_type TYPE_F32 writes f32 h, TYPE_Q8_K / TYPE_Q8_0 its blocks
+hipError_t ffn_swiglu_launch(int out_type, const float* g, const float* u, size_t n_rows, size_t n, void* out,
+                             hipStream_t s);
 
 // norm.hip: RMSNorm rows (transformer.rs:148-172), alone or fused with the
 // Q8_K / Q8_0 quantizer (n % 256 == 0 for the fused form)
@@ -47,6 +52,11 @@ int moe_gemv_enabled();   // BARQ_MOE_GEMV (0: off, 1: one-token steps, 2: up to
 hipError_t moe_gemv_launch(int w_type, const void* const* W, size_t n_experts, size_t n_mats, const int32_t* offsets,
                            size_t n_assign, size_t tokens, const void* xq, size_t n_rows, size_t k, float* y,
                            size_t y_mat_stride, hipStream_t s);
+// Gate and up of one Q8_K row in one launch with the dense SwiGLU in the
+// epilogue: h[n_rows] (Q4_K weights, 16-byte aligned)
+bool gemv_glu_supported(int w_type, const void* G, const void* U, size_t n_rows, size_t k);
+hipError_t gemv_glu_launch(int w_type, const void* G, const void* U, size_t n_rows, size_t k, const void* xq, float* h,
+                           hipStream_t s);
 // 2-4 Q8 activation rows at once (y[m x n_rows]): the weights read once
 bool gemv_multi_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m);
 hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,

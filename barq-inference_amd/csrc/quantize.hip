@@ -54,9 +54,23 @@ __global__ __launch_bounds__(256) void quantize_q8_k_gather_kernel(const float* 
     q8_k_block(vv, lane, out + b * 292);
 }
 
-// Q8_K of h = silu(g) * u, silu(g) = g / (1 + exp(-g)) rounded first
-// (ops.rs:191-211, moe_fused.rs:61-66): the SwiGLU product is formed in
-// registers and never stored.
+// The two SwiGLU roundings of the reference:
+//   MoE expert FFN: silu(g) = g / (1 + exp(-g)) rounded first, then * u
+//     (ops::Silu, ops.rs:191-211; the product of moe_fused.rs:61-66);
+//   dense FFN: (g * (1 / (1 + exp(-g)))) * u (transformer.rs:394-399).
+template <bool DENSE>
+__device__ __forceinline__ float swiglu_form(float g, float u) {
+    if constexpr (DENSE) {
+        return (g * (1.0f / (1.0f + expf(-g)))) * u;
+    } else {
+        const float a = g / (1.0f + expf(-g));
+        return a * u;
+    }
+}
+
+// Q8_K of h = swiglu(g, u): the SwiGLU product is formed in registers and
+// never stored.
+template <bool DENSE>
 __global__ __launch_bounds__(256) void swiglu_q8_k_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                           uint8_t* __restrict__ out, size_t nb) {
     const size_t b = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -67,11 +81,34 @@ __global__ __launch_bounds__(256) void swiglu_q8_k_kernel(const float* __restric
     const float ga[4] = {gv.x, gv.y, gv.z, gv.w}, ua[4] = {uv.x, uv.y, uv.z, uv.w};
     float vv[4];
     #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float a = ga[j] / (1.0f + expf(-ga[j]));
-        vv[j] = a * ua[j];
-    }
+    for (int j = 0; j < 4; j++) vv[j] = swiglu_form<DENSE>(ga[j], ua[j]);
     q8_k_block(vv, lane, out + b * 292);
+}
+
+// Q8_0 of the dense FFN's h (one lane per element, as quantize_q8_0_kernel)
+__global__ __launch_bounds__(256) void swiglu_q8_0_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          uint8_t* __restrict__ out, size_t nb) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nb * 32) return;
+    const size_t b = e / 32;
+    const int l = (int)(e % 32);
+    const float v = swiglu_form<true>(g[e], u[e]);
+    float a = fabsf(v);
+    #pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float d = a / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q = (int)roundf(v * id);
+    uint8_t* blk = out + b * 34;
+    blk[2 + l] = (uint8_t)(int8_t)q;
+    if (l == 0) *reinterpret_cast<uint16_t*>(blk) = f32_to_f16_bits(d);
+}
+
+// f32 h of the dense FFN (n elements)
+__global__ __launch_bounds__(256) void swiglu_f32_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                         float* __restrict__ h, size_t n) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < n) h[e] = swiglu_form<true>(g[e], u[e]);
 }
 
 // quant::Q4_0::quantize (quant/src/q4_0.rs:23-67): scale = max_abs/8 (0 for an
@@ -131,8 +168,27 @@ hipError_t quantize_q8_k_gather_launch(const float* x, const int32_t* rows_idx, 
 hipError_t swiglu_q8_k_launch(const float* g, const float* u, size_t n_rows, size_t k, void* out, hipStream_t s) {
     const size_t nb = n_rows * (k / 256);
     if (nb == 0) return hipSuccess;
-    hipLaunchKernelGGL(swiglu_q8_k_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, g, u,
+    hipLaunchKernelGGL(swiglu_q8_k_kernel<false>, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, g, u,
                        static_cast<uint8_t*>(out), nb);
+    return hipGetLastError();
+}
+
+hipError_t ffn_swiglu_launch(int out_type, const float* g, const float* u, size_t n_rows, size_t n, void* out,
+                             hipStream_t s) {
+    const size_t total = n_rows * n;
+    if (total == 0) return hipSuccess;
+    if (out_type == TYPE_Q8_K) {
+        const size_t nb = total / 256;
+        hipLaunchKernelGGL(swiglu_q8_k_kernel<true>, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, s, g, u,
+                           static_cast<uint8_t*>(out), nb);
+    } else if (out_type == TYPE_Q8_0) {
+        const size_t nb = total / 32;
+        hipLaunchKernelGGL(swiglu_q8_0_kernel, dim3((unsigned)((nb * 32 + 255) / 256)), dim3(256), 0, s, g, u,
+                           static_cast<uint8_t*>(out), nb);
+    } else {
+        hipLaunchKernelGGL(swiglu_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, g, u,
+                           static_cast<float*>(out), total);
+    }
     return hipGetLastError();
 }
 

@@ -58,6 +58,9 @@ def parse():
                    help="time decode attention over the device KV cache (Llama-3-8B heads) instead of a config")
     p.add_argument("--kv-len", type=int, default=4096, help="--attn: cached positions per query")
     p.add_argument("--q-len", type=int, default=1, help="--attn: new tokens per call (1 = decode; > 1 = a prompt chunk)")
+    p.add_argument("--ffn", action="store_true",
+                   help="time the dense FFN (feed_forward: gate/up Q4_K, SwiGLU, down Q6_K) at Llama-3-8B shapes")
+    p.add_argument("--m", type=int, default=1, help="--ffn: tokens per call")
     p.add_argument("--probe-copy", action="store_true",
                    help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -404,6 +407,90 @@ def bench_norm(args):
     return 0
 
 
+def bench_ffn(args):
+    """The dense FFN of one Llama-3-8B layer (LlamaTransformer::feed_forward,
+    transformer.rs:378-408): Q4_K gate and up 14336 x 4096, SwiGLU, Q6_K down
+    4096 x 14336 (the Q4_K_M mix), on m rows already quantized to Q8_K (the
+    fused RMSNorm -> Q8_K of the layer writes them).  One token runs gate and
+    up in one launch with the SwiGLU in its epilogue; beside it the same work
+    as two separate GEMVs and the SwiGLU quantizer.  Layers rotate over
+    enough weight copies (> 320 MB) that the Infinity Cache cannot hold them."""
+    import numpy as np
+    import torch
+
+    import barq_rocm as B
+    from barq_rocm import synth
+
+    n_embd, n_ff, m = 4096, 14336, args.m
+    s0 = synth.config_seed(2)
+    gate = synth.gen_q4_k(n_ff, n_embd, synth.sub_seed(s0, 40))
+    up = synth.gen_q4_k(n_ff, n_embd, synth.sub_seed(s0, 41))
+    down = synth.gen_q6_k(n_embd, n_ff, synth.sub_seed(s0, 42))
+    x = synth.gen_f32(m * n_embd, synth.sub_seed(s0, 43)).reshape(m, n_embd)
+    wbytes = gate.nbytes + up.nbytes + down.nbytes
+    copies = args.copies or max(2, -(-320 * 2 ** 20 // wbytes))
+    be = B.Backend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    layers = [tuple(torch.from_numpy(a).cuda() for a in (gate, up, down)) for _ in range(copies)]
+    xq = be.quantize_act(B.Q8_K, torch.from_numpy(x).cuda(), sync=False)
+    out = torch.empty((m, n_embd), dtype=torch.float32, device="cuda")
+    g = torch.empty((m, n_ff), dtype=torch.float32, device="cuda")
+    u = torch.empty((m, n_ff), dtype=torch.float32, device="cuda")
+    hq = torch.empty(m * (n_ff // 256) * 292, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+
+    def fused(i):
+        gd, ud, dd = layers[i % copies]
+        be.ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, n_embd, n_ff, B.Q8_K, xq, m, sync=False, out=out)
+
+    def separate(i):
+        gd, ud, dd = layers[i % copies]
+        be.matmul_raw(B.Q4_K, gd, n_ff, n_embd, B.Q8_K, xq, m, g, B.MEM_DEVICE)
+        be.matmul_raw(B.Q4_K, ud, n_ff, n_embd, B.Q8_K, xq, m, u, B.MEM_DEVICE)
+        L = B._lib
+        L.check(be._lib.barq_rocm_swiglu(be.h, B.Q8_K, g.data_ptr(), u.data_ptr(), m, n_ff, hq.data_ptr(),
+                                         B.MEM_DEVICE))
+        be.matmul_raw(B.Q6_K, dd, n_embd, n_ff, B.Q8_K, hq, m, out, B.MEM_DEVICE)
+
+    for i in range(args.warmup):
+        fused(i)
+        separate(i)
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} FFN calls over {copies} layer copies ({copies * wbytes / 2**20:.0f} MiB)")
+    ms, method = time_launches(fused, args.steps, args.eager)
+    ms_sep, _ = time_launches(separate, args.steps, args.eager)
+    fused(0)
+    torch.cuda.synchronize()
+    alg = wbytes + m * (n_embd // 256) * 292 + m * (n_ff // 256) * 292 + m * n_ff * 4 * 2 + m * n_embd * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    rel = None
+    try:
+        from oracle import oracle as orc
+        ref = orc.ffn(B.Q4_K, gate, B.Q4_K, up, B.Q6_K, down, n_embd, n_ff, orc.Q8_K, xq.cpu().numpy(), m)
+        got = out.cpu().numpy()
+        rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    except Exception as e:
+        log(f"parity check skipped: {e}")
+    result = {
+        "metric": "dense FFN (Llama-3-8B, gate/up Q4_K + down Q6_K) achieved HBM GB/s + us/call, 1 GPU",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"feed_forward 4096 -> 14336 -> 4096, {m} token(s), x as Q8_K",
+                   "layer_copies": copies, "timing": method},
+        "us_per_call": round(ms * 1e3, 3), "us_per_call_separate_launches": round(ms_sep * 1e3, 3),
+        "parity_rel_err": rel,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
+                     "scope": "the whole FFN call (gate/up, SwiGLU + Q8_K, down)"},
+    }
+    be.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def bench_attn(args):
     """Decode attention (compute_attention, transformer.rs:301-374) at the
     Llama-3-8B head layout: 32 query heads, 8 kv heads, head_dim 128, one new
@@ -510,6 +597,8 @@ def main():
         return bench_norm(args)
     if args.attn:
         return bench_attn(args)
+    if args.ffn:
+        return bench_ffn(args)
     if args.config == 5:
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]

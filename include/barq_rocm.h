@@ -166,6 +166,29 @@ int barq_rocm_matmul(barq_rocm_handle* h, int w_type, const void* w,
                      size_t n_rows, size_t k, int act_type, const void* x,
                      size_t m, float* y, int mem);
 
+/* ---- dense FFN ------------------------------------------------------------
+ * swiglu: the SwiGLU of LlamaTransformer::feed_forward
+ *   (models/src/transformer.rs:394-399), h = (g * (1 / (1 + exp(-g)))) * u
+ *   with each operation rounded as written (the MoE expert FFN rounds
+ *   silu(g) = g / (1 + exp(-g)) instead, ops.rs:191-211), over rows x n of
+ *   gate/up f32.  out_type BARQ_TYPE_F32 writes f32 h; BARQ_TYPE_Q8_K /
+ *   BARQ_TYPE_Q8_0 write h's activation blocks for the down projection
+ *   (byte-identical to barq_rocm_quantize_act of the f32 h) without storing
+ *   it.  exp is the device's expf: h agrees with the reference to a few ulp.
+ * ffn: feed_forward (transformer.rs:378-408) of m rows of x [m x n_embd]:
+ *   out = down(swiglu(gate(x), up(x))); gate/up are [n_ff x n_embd], down
+ *   [n_embd x n_ff] GGUF weights (proj_with_in_dim, :411-442).  act:
+ *   BARQ_ACT_F32 the literal f32 arithmetic; BARQ_ACT_F32_Q8 x f32,
+ *   quantized here to gate's Q8 partner and h to down's; BARQ_TYPE_Q8_K /
+ *   BARQ_TYPE_Q8_0 x already quantized (e.g. by barq_rocm_rms_norm_quantize).
+ *   One row with Q4_K gate and up runs both projections in one launch with
+ *   the SwiGLU in its epilogue.  Uses the handle's workspace. */
+int barq_rocm_swiglu(barq_rocm_handle* h, int out_type, const float* gate, const float* up,
+                     size_t rows, size_t n, void* out, int mem);
+int barq_rocm_ffn(barq_rocm_handle* h, int gate_type, const void* gate, int up_type,
+                  const void* up, int down_type, const void* down, size_t n_embd,
+                  size_t n_ff, int act, const void* x, size_t m, float* out, int mem);
+
 /* ---- f32 BLAS ----------------------------------------------------------
  * Device arms of blas::gemm_f32 (blas.rs:103-213: C[m x n] = A[m x k]
  * B[k x n], row-major) and blas::gemv_f32 (blas.rs:229-304: y = A[m x n] x),

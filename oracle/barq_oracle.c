@@ -673,6 +673,55 @@ done:
     return rc;
 }
 
+/* ---- dense FFN (models/src/transformer.rs:378-408) ------------------------ */
+
+void orc_ffn_swiglu(const float* g, const float* u, size_t n, float* h) {
+    /* :394-399 — (g * (1.0 / (1.0 + (-g).exp()))) * u, in this order */
+    for (size_t i = 0; i < n; i++) {
+        const float r = 1.0f / (1.0f + expf(-g[i]));
+        const float a = g[i] * r;
+        h[i] = a * u[i];
+    }
+}
+
+static int q8_partner(int w_type) {
+    return (w_type == ORC_Q4_K || w_type == ORC_Q6_K) ? ORC_Q8_K : ORC_Q8_0;
+}
+
+int orc_ffn(int gate_type, const uint8_t* gate, int up_type, const uint8_t* up,
+            int down_type, const uint8_t* down, size_t n_embd, size_t n_ff,
+            int act, const void* x, size_t m, float* out) {
+    /* feed_forward: gate and up by proj_with_in_dim (:381-392, the matmul of
+       :411-442), the SwiGLU, then down (:401-407) */
+    const int lit = act == ORC_F32;
+    const int pd = q8_partner(down_type);
+    float* g = (float*)malloc(m * n_ff * sizeof(float));
+    float* u = (float*)malloc(m * n_ff * sizeof(float));
+    uint8_t* hq = NULL;
+    int rc = -1;
+    if (!g || !u) goto done;
+    if (!lit && (act != q8_partner(gate_type) || act != q8_partner(up_type))) goto done;
+    if (orc_matmul(gate_type, gate, n_ff, n_embd, act, x, m, g)) goto done;
+    if (orc_matmul(up_type, up, n_ff, n_embd, act, x, m, u)) goto done;
+    orc_ffn_swiglu(g, u, m * n_ff, g);
+    if (lit) {
+        rc = orc_matmul(down_type, down, n_embd, n_ff, ORC_F32, g, m, out);
+    } else {
+        const size_t rb = n_ff / orc_block_elems(pd) * orc_block_bytes(pd);
+        if (n_ff % orc_block_elems(pd)) goto done;
+        hq = (uint8_t*)malloc(m * rb);
+        if (!hq) goto done;
+        for (size_t r = 0; r < m; r++) {
+            if (pd == ORC_Q8_K) orc_quantize_q8_k(g + r * n_ff, n_ff, hq + r * rb);
+            else orc_quantize_q8_0(g + r * n_ff, n_ff, hq + r * rb);
+        }
+        rc = orc_matmul(down_type, down, n_embd, n_ff, pd, hq, m, out);
+    }
+done:
+    free(g); free(u); free(hq);
+    return rc;
+}
+
 struct moe_ffn_ctx {
     int gate_type, up_type, down_type, act;
     const uint8_t* const* gate;

@@ -160,6 +160,19 @@ int orc_moe_ffn(int gate_type, const uint8_t* const* gate,
                 const float* x, size_t rows, const int32_t* ids,
                 const float* weights, size_t k, int act, float* out);
 
+/* ---- dense FFN (models/src/transformer.rs:378-408) -------------------- */
+/* The SwiGLU of feed_forward (:394-399): h = (g * (1 / (1 + expf(-g)))) * u,
+   rounded in that order (h may alias g). */
+void orc_ffn_swiglu(const float* g, const float* u, size_t n, float* h);
+/* feed_forward of m rows: out[m x n_embd] = down(swiglu(gate x, up x)).
+   act = ORC_F32: x is f32 and everything stays f32 (the literal reference);
+   act = ORC_Q8_K / ORC_Q8_0: x is quantized rows (gate's and up's Q8
+   partner) and h is quantized to down's partner before the down product.
+   Returns 0, or -1 on a bad type/shape. */
+int orc_ffn(int gate_type, const uint8_t* gate, int up_type, const uint8_t* up,
+            int down_type, const uint8_t* down, size_t n_embd, size_t n_ff,
+            int act, const void* x, size_t m, float* out);
+
 /* ---- the quant crate's own Q4_K (quant/src/q4_k.rs, not GGUF) --------- */
 /* Q4_K::quantize (:23-73): blocks of 256, the last may be shorter; per
    block f32 scale_min, f32 scale_max (= max - min), ceil(len/2) nibble

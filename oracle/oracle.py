@@ -52,6 +52,8 @@ def lib():
             "orc_moe_batch_by_expert": (None, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
             "orc_moe_dispatch": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
             "orc_moe_ffn": (_i, [_i, _vp, _i, _vp, _i, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _i, _vp]),
+            "orc_ffn_swiglu": (None, [_vp, _vp, _sz, _vp]),
+            "orc_ffn": (_i, [_i, _vp, _i, _vp, _i, _vp, _sz, _sz, _i, _vp, _sz, _vp]),
             "orc_q4_k_barq_quantize": (_sz, [_vp, _sz, _vp]),
             "orc_q4_k_barq_dequantize": (_sz, [_vp, _sz, _sz, _vp]),
             "orc_rope": (None, [_vp, _sz, _sz, _sz, _sz, ctypes.c_float, _vp, _i, _vp]),
@@ -338,6 +340,29 @@ def moe_ffn(gate_type, gates, up_type, ups, down_type, downs, hidden, n_ff, x, i
                            _p(weights), ids.shape[1], act, _p(out))
     if rc:
         raise ValueError("orc_moe_ffn failed")
+    return out
+
+
+def ffn_swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """transformer.rs:394-399 elementwise."""
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    h = np.empty_like(g)
+    lib().orc_ffn_swiglu(_p(g), _p(u), g.size, _p(h))
+    return h
+
+
+def ffn(gate_type, gate, up_type, up, down_type, down, n_embd, n_ff, act, x, m) -> np.ndarray:
+    """feed_forward (transformer.rs:378-408): act F32 (x f32) or Q8_K / Q8_0
+    (x quantized rows)."""
+    gate = np.ascontiguousarray(gate, dtype=np.uint8)
+    up = np.ascontiguousarray(up, dtype=np.uint8)
+    down = np.ascontiguousarray(down, dtype=np.uint8)
+    x = np.ascontiguousarray(x)
+    out = np.empty((m, n_embd), dtype=np.float32)
+    rc = lib().orc_ffn(gate_type, _p(gate), up_type, _p(up), down_type, _p(down), n_embd, n_ff, act, _p(x), m, _p(out))
+    if rc:
+        raise ValueError("orc_ffn failed")
     return out
 
 
