@@ -53,6 +53,7 @@ EXPORTS = (
     "barq_rocm_get_stream", "barq_rocm_synchronize", "barq_rocm_abi_version",
     "barq_rocm_block_elems", "barq_rocm_block_bytes", "barq_rocm_row_bytes",
     "barq_rocm_dequantize", "barq_rocm_quantize_act", "barq_rocm_rms_norm", "barq_rocm_rms_norm_quantize",
+    "barq_rocm_add_rms_norm_quantize",
     "barq_rocm_matvec", "barq_rocm_matmul", "barq_rocm_swiglu", "barq_rocm_ffn",
     "barq_rocm_gemm_f32", "barq_rocm_gemv_f32", "barq_rocm_dequantize_split",
     "barq_rocm_quantized_matmul_split", "barq_rocm_quantize_q4_0_barq", "barq_rocm_quantize_q4_k_barq",
@@ -105,6 +106,7 @@ def _declare(lib):
         "barq_rocm_quantize_act": (_i, [_vp, _i, _vp, _sz, _sz, _vp, _i]),
         "barq_rocm_rms_norm": (_i, [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i]),
         "barq_rocm_rms_norm_quantize": (_i, [_vp, _i, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i]),
+        "barq_rocm_add_rms_norm_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _vp, _i]),
         "barq_rocm_matvec": (_i, [_vp, _i, _vp, _sz, _sz, _i, _vp, _vp, _i]),
         "barq_rocm_matmul": (_i, [_vp, _i, _vp, _sz, _sz, _i, _vp, _sz, _vp, _i]),
         "barq_rocm_swiglu": (_i, [_vp, _i, _vp, _vp, _sz, _sz, _vp, _i]),

@@ -121,6 +121,24 @@ class Backend:
             self.sync()
         return out
 
+    def add_rms_norm_quantize(self, out_type, x, d, weight, eps, sum_out=None, out=None, mem=L.MEM_DEVICE,
+                              sync=True):
+        """rms_norm(x + d) as out_type (F32 rows or Q8 blocks); x + d to sum_out."""
+        rows, n = (1, x.size if mem == L.MEM_HOST else x.numel()) if x.ndim == 1 else tuple(x.shape)
+        if out is None:
+            nbytes = rows * (n * 4 if out_type == L.F32 else n // L.BLOCK_ELEMS[out_type] * L.BLOCK_BYTES[out_type])
+            if mem == L.MEM_HOST:
+                out = np.empty((rows, n), np.float32) if out_type == L.F32 else np.empty(nbytes, np.uint8)
+            else:
+                import torch
+                out = (torch.empty((rows, n), dtype=torch.float32, device=x.device) if out_type == L.F32
+                       else torch.empty(nbytes, dtype=torch.uint8, device=x.device))
+        L.check(self._lib.barq_rocm_add_rms_norm_quantize(self.h, out_type, _ptr(x), _ptr(d), _ptr(weight), rows, n,
+                                                          eps, _ptr(sum_out), _ptr(out), mem))
+        if sync and mem == L.MEM_DEVICE:
+            self.sync()
+        return out
+
     def matvec(self, w_type, w, n_rows, k, act_type, x, sync=True):
         import torch
         y = torch.empty(n_rows, dtype=torch.float32, device=w.device)

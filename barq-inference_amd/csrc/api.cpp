@@ -305,6 +305,45 @@ int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* 
     return ok();
 }
 
+int barq_rocm_add_rms_norm_quantize(barq_rocm_handle* h, int out_type, const float* x, const float* d,
+                                    const float* weight, size_t rows, size_t n, float eps, float* sum, void* out,
+                                    int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (out_type != BARQ_TYPE_F32 && out_type != BARQ_TYPE_Q8_0 && out_type != BARQ_TYPE_Q8_K)
+        return fail(BARQ_E_UNSUPPORTED, "add_rms_norm_quantize: out_type must be F32, Q8_0 or Q8_K, got %d", out_type);
+    if (rows == 0 || n == 0) return ok();
+    if (!barq::rms_norm_supported(n) || (out_type != BARQ_TYPE_F32 && n % 256 != 0))
+        return fail(BARQ_E_DIM, "add_rms_norm_quantize: n=%zu must be a multiple of %d and at most 16384", n,
+                    out_type == BARQ_TYPE_F32 ? 4 : 256);
+    if (!x || !weight || !out) return fail(BARQ_E_INVALID, "add_rms_norm_quantize: null buffer");
+    if (sum && !d) return fail(BARQ_E_INVALID, "add_rms_norm_quantize: sum needs d (it receives x + d)");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    const size_t out_bytes = rows * (out_type == BARQ_TYPE_F32 ? n * 4 : row_bytes_of(out_type, n));
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(x, 16) || !aligned(weight, 16) || (d && !aligned(d, 16)) || (sum && !aligned(sum, 16)) ||
+            !aligned(out, out_type == BARQ_TYPE_F32 ? 16 : out_type == BARQ_TYPE_Q8_K ? 4 : 2))
+            return fail(BARQ_E_INVALID, "add_rms_norm_quantize: x, d, weight, sum 16-byte aligned; out %d-byte",
+                        out_type == BARQ_TYPE_F32 ? 16 : out_type == BARQ_TYPE_Q8_K ? 4 : 2);
+        return launched(barq::add_rms_norm_launch(out_type, x, d, weight, rows, n, eps, sum, out, h->stream),
+                        "add_rms_norm_quantize");
+    }
+    Arena a;
+    const size_t ox = a.add(rows * n * 4), od = a.add(d ? rows * n * 4 : 0), ow = a.add(n * 4),
+                 os = a.add(sum ? rows * n * 4 : 0), oo = a.add(out_bytes);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ox), x, rows * n * 4, hipMemcpyHostToDevice, h->stream));
+    if (d) BARQ_HIP(hipMemcpyAsync(at<float>(h, od), d, rows * n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ow), weight, n * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::add_rms_norm_launch(out_type, at<float>(h, ox), d ? at<float>(h, od) : nullptr,
+                                                  at<float>(h, ow), rows, n, eps, sum ? at<float>(h, os) : nullptr,
+                                                  at<uint8_t>(h, oo), h->stream), "add_rms_norm_quantize"));
+    if (sum) BARQ_HIP(hipMemcpyAsync(sum, at<float>(h, os), rows * n * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipMemcpyAsync(out, at<uint8_t>(h, oo), out_bytes, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
 // ---------------------------------------------------------------------------
 // matvec / matmul
 

@@ -37,6 +37,10 @@ hipError_t rms_norm_launch(const float* x, const float* w, size_t rows, size_t n
                            hipStream_t s);
 hipError_t rms_norm_quantize_launch(int act_type, const float* x, const float* w, size_t rows, size_t n, float eps,
                                     void* out, hipStream_t s);
+// RMSNorm of x + d (d may be null), the sum stored to `sum` when non-null;
+// out_type TYPE_F32 (f32 rows), TYPE_Q8_K or TYPE_Q8_0 (n % 256 == 0)
+hipError_t add_rms_norm_launch(int out_type, const float* x, const float* d, const float* w, size_t rows, size_t n,
+                               float eps, float* sum, void* out, hipStream_t s);
 
 // gemv.hip
 hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,

@@ -83,15 +83,19 @@ __device__ __forceinline__ void norm_q8_0_block(const float (&vv)[4], int lane, 
 // W waves, V float4 chunks per lane: chunk i of wave w is float4
 // 64 (w + W i) + lane, i.e. lane `lane` of 256-element block w + W i.
 // OUT: 0 f32 rows, 1 Q8_K, 2 Q8_0.
+// With d non-null the row normalized is x + d (add_vectors, transformer.rs:
+// 505-510, the residual adds of forward_layer :136, :143), stored to sum when
+// sum is non-null.
 template <int W, int V, int OUT>
 __global__ __launch_bounds__(64 * W)
-void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n, float eps,
-                     void* __restrict__ out) {
+void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ d, const float* __restrict__ w, int n,
+                     float eps, float* __restrict__ sum, void* __restrict__ out) {
     __shared__ float part[W];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t row = blockIdx.x;
     const int n4 = n / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + row * (size_t)n);
+    const float4* dr = d ? reinterpret_cast<const float4*>(d + row * (size_t)n) : nullptr;
     const float4* wr = reinterpret_cast<const float4*>(w);
     float4 v[V], wv[V];
     // the weight is loaded with x, so the row costs one memory round trip
@@ -100,6 +104,17 @@ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, i
         const int f = 64 * (wave + W * i) + lane;
         v[i] = f < n4 ? xr[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         wv[i] = f < n4 ? wr[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (dr) {
+        #pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int f = 64 * (wave + W * i) + lane;
+            if (f < n4) {
+                const float4 dv = dr[f];
+                v[i] = make_float4(v[i].x + dv.x, v[i].y + dv.y, v[i].z + dv.z, v[i].w + dv.w);
+                if (sum) reinterpret_cast<float4*>(sum + row * (size_t)n)[f] = v[i];
+            }
+        }
     }
     float ss = 0.0f;
     #pragma unroll
@@ -140,13 +155,13 @@ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, i
 // One wave per 256 elements up to 16 waves (short rows still spread over
 // many SIMDs), then up to four float4 chunks per lane.
 template <int W, int OUT>
-static hipError_t launch_norm_w(const float* x, const float* w, size_t rows, size_t n, float eps, void* out,
-                                hipStream_t s) {
+static hipError_t launch_norm_w(const float* x, const float* d, const float* w, size_t rows, size_t n, float eps,
+                                float* sum, void* out, hipStream_t s) {
     const size_t chunks = (n / 4 + 64 * W - 1) / (64 * W);   // float4 chunks per lane
 #define BARQ_NORM_CASE(VV) \
     if (chunks <= VV) { \
-        hipLaunchKernelGGL((rms_norm_kernel<W, VV, OUT>), dim3((unsigned)rows), dim3(64 * W), 0, s, x, w, (int)n, \
-                           eps, out); \
+        hipLaunchKernelGGL((rms_norm_kernel<W, VV, OUT>), dim3((unsigned)rows), dim3(64 * W), 0, s, x, d, w, (int)n, \
+                           eps, sum, out); \
         return hipGetLastError(); \
     }
     BARQ_NORM_CASE(1) BARQ_NORM_CASE(2) BARQ_NORM_CASE(4)
@@ -155,14 +170,14 @@ static hipError_t launch_norm_w(const float* x, const float* w, size_t rows, siz
 }
 
 template <int OUT>
-static hipError_t launch_norm(const float* x, const float* w, size_t rows, size_t n, float eps, void* out,
-                              hipStream_t s) {
+static hipError_t launch_norm(const float* x, const float* d, const float* w, size_t rows, size_t n, float eps,
+                              float* sum, void* out, hipStream_t s) {
     const size_t blocks = (n + 255) / 256;
-    if (blocks <= 1) return launch_norm_w<1, OUT>(x, w, rows, n, eps, out, s);
-    if (blocks <= 2) return launch_norm_w<2, OUT>(x, w, rows, n, eps, out, s);
-    if (blocks <= 4) return launch_norm_w<4, OUT>(x, w, rows, n, eps, out, s);
-    if (blocks <= 8) return launch_norm_w<8, OUT>(x, w, rows, n, eps, out, s);
-    return launch_norm_w<16, OUT>(x, w, rows, n, eps, out, s);
+    if (blocks <= 1) return launch_norm_w<1, OUT>(x, d, w, rows, n, eps, sum, out, s);
+    if (blocks <= 2) return launch_norm_w<2, OUT>(x, d, w, rows, n, eps, sum, out, s);
+    if (blocks <= 4) return launch_norm_w<4, OUT>(x, d, w, rows, n, eps, sum, out, s);
+    if (blocks <= 8) return launch_norm_w<8, OUT>(x, d, w, rows, n, eps, sum, out, s);
+    return launch_norm_w<16, OUT>(x, d, w, rows, n, eps, sum, out, s);
 }
 
 // rows of up to 16 waves x 4 float4 chunks per lane (16384 elements) are held in registers
@@ -171,14 +186,21 @@ bool rms_norm_supported(size_t n) { return n > 0 && n % 4 == 0 && n <= 4 * 4 * 6
 hipError_t rms_norm_launch(const float* x, const float* w, size_t rows, size_t n, float eps, float* y,
                            hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    return launch_norm<0>(x, w, rows, n, eps, y, s);
+    return launch_norm<0>(x, nullptr, w, rows, n, eps, nullptr, y, s);
 }
 
 hipError_t rms_norm_quantize_launch(int act_type, const float* x, const float* w, size_t rows, size_t n, float eps,
                                     void* out, hipStream_t s) {
+    return add_rms_norm_launch(act_type, x, nullptr, w, rows, n, eps, nullptr, out, s);
+}
+
+hipError_t add_rms_norm_launch(int out_type, const float* x, const float* d, const float* w, size_t rows, size_t n,
+                               float eps, float* sum, void* out, hipStream_t s) {
     if (rows == 0) return hipSuccess;
+    if (out_type == TYPE_F32) return launch_norm<0>(x, d, w, rows, n, eps, sum, out, s);
     if (n % 256 != 0) return hipErrorInvalidValue;
-    return act_type == TYPE_Q8_K ? launch_norm<1>(x, w, rows, n, eps, out, s) : launch_norm<2>(x, w, rows, n, eps, out, s);
+    return out_type == TYPE_Q8_K ? launch_norm<1>(x, d, w, rows, n, eps, sum, out, s)
+                                 : launch_norm<2>(x, d, w, rows, n, eps, sum, out, s);
 }
 
 }  // namespace barq

@@ -61,6 +61,8 @@ def parse():
     p.add_argument("--ffn", action="store_true",
                    help="time the dense FFN (feed_forward: gate/up Q4_K, SwiGLU, down Q6_K) at Llama-3-8B shapes")
     p.add_argument("--m", type=int, default=1, help="--ffn: tokens per call")
+    p.add_argument("--layer", action="store_true",
+                   help="time one Llama-3-8B decode layer (norm, q/k/v, RoPE + KV append, attention, o, norm, FFN)")
     p.add_argument("--probe-copy", action="store_true",
                    help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -491,6 +493,103 @@ def bench_ffn(args):
     return 0
 
 
+def bench_layer(args):
+    """One decode step of a Llama-3-8B layer (forward_layer,
+    transformer.rs:123-144) on the integer path, every launch captured in one
+    HIP graph: residual add + attn_norm -> Q8_K, q / k / v GEMVs (Q4_K, Q4_K,
+    Q6_K), RoPE(q), RoPE(k) + V transpose + KV append, attention over kv_len
+    cached positions, output projection (f32 -> Q8_K in the call), residual
+    add + ffn_norm -> Q8_K, the dense FFN (gate/up Q4_K, down Q6_K).  Steps
+    rotate over enough layer copies (weights and KV cache) that the Infinity
+    Cache cannot hold them.  Algorithmic bytes: the layer's packed weights,
+    the K and V rows attention reads, and the activations."""
+    import numpy as np
+    import torch
+
+    import barq_rocm as B
+    from barq_rocm import attention as A
+    from barq_rocm import synth
+
+    n_embd, n_head, n_kv, hd, n_ff = 4096, 32, 8, 128, 14336
+    kv_len = args.kv_len
+    mats = [("q", B.Q4_K, n_head * hd, n_embd), ("k", B.Q4_K, n_kv * hd, n_embd), ("v", B.Q6_K, n_kv * hd, n_embd),
+            ("o", B.Q4_K, n_embd, n_head * hd), ("gate", B.Q4_K, n_ff, n_embd), ("up", B.Q4_K, n_ff, n_embd),
+            ("down", B.Q6_K, n_embd, n_ff)]
+    host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
+    wbytes = sum(a.nbytes for a in host.values())
+    kv_bytes = 2 * n_kv * kv_len * hd * 4
+    copies = args.copies or max(2, -(-320 * 2 ** 20 // (wbytes + kv_bytes)))
+    be = B.Backend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    layers = [{nm: torch.from_numpy(a).cuda() for nm, a in host.items()} for _ in range(copies)]
+    norm_w = torch.from_numpy((0.01 * (1.0 + 0.1 * synth.gen_f32(n_embd, 820))).astype(np.float32)).cuda()
+    f = torch.from_numpy(np.array([np.float32(500000.0) ** np.float32(-2.0 * i / hd) for i in range(hd // 2)],
+                                  dtype=np.float32)).cuda()
+    steps = args.steps
+    kv = A.KVCache(be, kv_len + steps + 8, copies, n_kv, hd)
+    rng = np.random.default_rng(5)
+    for c in range(copies):   # kv_len - 1 cached positions per layer copy
+        kk = rng.standard_normal((n_kv, kv_len - 1, hd)).astype(np.float32)
+        kv.append(c, kk, kk * 0.5, kv_len - 1, hd, mem=B.MEM_HOST)
+    x = torch.from_numpy(synth.gen_f32(n_embd, 821)).cuda().reshape(1, n_embd)
+    prev = torch.zeros((1, n_embd), dtype=torch.float32, device="cuda")
+    res_in = torch.empty_like(x)
+    res = torch.empty_like(x)
+    xq = torch.empty((n_embd // 256) * 292, dtype=torch.uint8, device="cuda")
+    xq2 = torch.empty_like(xq)
+    q = torch.empty((1, n_head * hd), dtype=torch.float32, device="cuda")
+    k = torch.empty((1, n_kv * hd), dtype=torch.float32, device="cuda")
+    v = torch.empty((1, n_kv * hd), dtype=torch.float32, device="cuda")
+    o = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
+    ff = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    pos = [kv_len - 1] * copies
+
+    def step(i):
+        c = i % copies
+        L = layers[c]
+        be.add_rms_norm_quantize(B.Q8_K, x, prev, norm_w, 1e-5, sum_out=res_in, out=xq, sync=False)
+        be.matmul_raw(B.Q4_K, L["q"], n_head * hd, n_embd, B.Q8_K, xq, 1, q, B.MEM_DEVICE)
+        be.matmul_raw(B.Q4_K, L["k"], n_kv * hd, n_embd, B.Q8_K, xq, 1, k, B.MEM_DEVICE)
+        be.matmul_raw(B.Q6_K, L["v"], n_kv * hd, n_embd, B.Q8_K, xq, 1, v, B.MEM_DEVICE)
+        q_rope = A.apply_rope(be, q, 1, n_head, hd, pos[c], 1.0, f, A.ROPE_INTERLEAVED, sync=False)
+        kv.append_rope(c, k, v, 1, pos[c], 1.0, f, A.ROPE_INTERLEAVED)
+        attn = A.compute_attention(be, q_rope, kv, c, n_head, n_kv, hd, 1, pos[c] + 1, pos[c], sync=False)
+        pos[c] += 1
+        be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.ACT_F32_Q8, attn.reshape(1, n_embd), 1, o, B.MEM_DEVICE)
+        be.add_rms_norm_quantize(B.Q8_K, res_in, o, norm_w, 1e-5, sum_out=res, out=xq2, sync=False)
+        be.ffn(B.Q4_K, L["gate"], B.Q4_K, L["up"], B.Q6_K, L["down"], n_embd, n_ff, B.Q8_K, xq2, 1, sync=False,
+               out=ff)
+
+    # warm-up outside the graph (workspace, kernel attributes): one step per layer copy
+    for i in range(copies):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"timing {steps} decode-layer steps over {copies} layer copies "
+        f"({copies * (wbytes + kv_bytes) / 2**20:.0f} MiB of weights and KV)")
+    ms, method = time_launches(step, steps, args.eager)
+    alg = wbytes + kv_bytes + 4 * n_embd * 4 * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "Llama-3-8B decode layer (integer path) achieved HBM GB/s + us/step, 1 GPU",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": copies,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"forward_layer decode, 1 token, kv_len {kv_len}, Q4_K_M weight mix",
+                   "layer_copies": copies, "timing": method},
+        "us_per_step": round(ms * 1e3, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
+                     "scope": "the whole layer step (14 launches)"},
+    }
+    kv.close()
+    be.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def bench_attn(args):
     """Decode attention (compute_attention, transformer.rs:301-374) at the
     Llama-3-8B head layout: 32 query heads, 8 kv heads, head_dim 128, one new
@@ -599,6 +698,8 @@ def main():
         return bench_attn(args)
     if args.ffn:
         return bench_ffn(args)
+    if args.layer:
+        return bench_layer(args)
     if args.config == 5:
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]

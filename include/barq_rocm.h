@@ -144,6 +144,18 @@ int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* 
                                 const float* weight, size_t rows, size_t n, float eps,
                                 void* out_blocks, int mem);
 
+/* The residual add of forward_layer (add_vectors, transformer.rs:505-510,
+ * at :136 and :143) fused with the RMSNorm of the next sub-layer and its
+ * quantizer: per row, s = x + d (d may be NULL: s = x), stored to sum when
+ * sum is not NULL (sum needs d), then out = rms_norm(s) as out_type
+ * (BARQ_TYPE_F32 rows, or Q8_K / Q8_0 blocks as barq_rocm_rms_norm_quantize
+ * writes them).  A decode layer runs it twice: x + attention output with
+ * ffn_norm, then (as the next layer's first call) x + FFN output with
+ * attn_norm.  n % 4 == 0 (F32) or n % 256 == 0 (Q8), n <= 16384. */
+int barq_rocm_add_rms_norm_quantize(barq_rocm_handle* h, int out_type, const float* x,
+                                    const float* d, const float* weight, size_t rows, size_t n,
+                                    float eps, float* sum, void* out, int mem);
+
 /* ---- matvec / matmul ---------------------------------------------------
  * Replace blas::gemv_f32 (blas.rs:229-304; the output head,
  * transformer.rs:486) and blas::gemm_f32 (blas.rs:103-213; every

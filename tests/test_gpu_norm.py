@@ -68,3 +68,32 @@ def test_zero_row_and_eps_floor(be, orc):
     assert np.array_equal(got, orc.rms_norm(x, w, 0.0))
     q = be.rms_norm_quantize(B.Q8_K, dev(x), dev(w), 0.0).cpu().numpy()
     assert np.array_equal(q, orc.quantize_q8_k(orc.rms_norm(x, w, 0.0)))
+
+
+@pytest.mark.parametrize("out", ["F32", "Q8_K", "Q8_0"])
+@pytest.mark.parametrize("rows,n", [(1, 4096), (3, 5120), (2, 16384)])
+def test_residual_add_fused_with_norm(be, orc, out, rows, n):
+    """add_vectors (transformer.rs:505-510) fused into the next RMSNorm: the
+    stored sum is x + d bit for bit, and the output is exactly what the
+    unfused norm (or fused norm + quantizer) gives on that sum."""
+    import torch
+    t = {"F32": B.F32, "Q8_K": B.Q8_K, "Q8_0": B.Q8_0}[out]
+    x, w = inputs(rows, n, 300 + n + rows)
+    d = (synth.gen_f32(rows * n, 400 + n) * 3.0).reshape(rows, n)
+    xd, dd, wd = dev(x), dev(d), dev(w)
+    s = torch.empty_like(xd)
+    got = be.add_rms_norm_quantize(t, xd, dd, wd, 1e-5, sum_out=s).cpu().numpy()
+    assert np.array_equal(s.cpu().numpy(), x + d)
+    if t == B.F32:
+        assert np.array_equal(got, be.rms_norm(s, wd, 1e-5).cpu().numpy())
+    else:
+        assert np.array_equal(got, be.rms_norm_quantize(t, s, wd, 1e-5).cpu().numpy())
+    # without d it is the plain (fused) norm; host buffers give the same bytes
+    plain = be.add_rms_norm_quantize(t, xd, None, wd, 1e-5).cpu().numpy()
+    ref_plain = be.rms_norm(xd, wd, 1e-5).cpu().numpy() if t == B.F32 else be.rms_norm_quantize(t, xd, wd, 1e-5).cpu().numpy()
+    assert np.array_equal(plain, ref_plain)
+    s_h = np.empty((rows, n), np.float32)
+    got_h = be.add_rms_norm_quantize(t, x, d, w, 1e-5, sum_out=s_h, mem=B.MEM_HOST)
+    assert np.array_equal(s_h, x + d) and np.array_equal(np.asarray(got_h).reshape(got.shape), got)
+    with pytest.raises(B.BarqError):
+        be.add_rms_norm_quantize(t, xd, None, wd, 1e-5, sum_out=s)   # a sum needs d
