@@ -343,11 +343,19 @@ template <class P, int NX>
 static hipError_t launch_dma_default(const uint8_t* w, uint32_t rb, size_t n_rows, int nblk, const uint8_t* x,
                                      uint32_t x_bytes, uint32_t x_region, float* y, hipStream_t s) {
     // measured on MI355X: four rows per wave for the 128256-row Q6_K head
-    // (C3); for the 32-element formats one row per wave (more workgroups) up
-    // to 8192 rows (C1: 3.82 against 3.94 us), two above
-    if constexpr (P::SLICE_BLOCKS == 16) return launch_dma<P, 4, 4, 2, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
-    else if (n_rows <= 8192) return launch_dma<P, 4, 1, 1, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
-    else return launch_dma<P, 4, 2, 2, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    // (C3); eight waves of one row each for a few thousand rows (a 4096 x
+    // 14336 down projection: 9.85-9.88 against 10.24-10.31 us, alternating
+    // runs in one process; the token count of a multi-token call is not
+    // tuned); for the 32-element formats one row per wave (more workgroups)
+    // up to 8192 rows (C1: 3.82 against 3.94 us), two above
+    if constexpr (P::SLICE_BLOCKS == 16) {
+        if (NX == 1 && n_rows <= 8192) return launch_dma<P, 8, 1, 1, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+        return launch_dma<P, 4, 4, 2, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    } else if (n_rows <= 8192) {
+        return launch_dma<P, 4, 1, 1, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    } else {
+        return launch_dma<P, 4, 2, 2, NX>(w, rb, n_rows, nblk, x, x_bytes, x_region, y, s);
+    }
 }
 
 template <class P>

@@ -165,14 +165,15 @@ GEMV_VARIANTS = [dict(BARQ_GEMV_DMA=c) for c in (-1, 422, 444, 482, 822, 842, 22
 
 @pytest.mark.parametrize("w_type", [B.Q4_K, B.Q6_K, B.Q4_0, B.Q8_0])
 def test_gemv_variants(be, orc, w_type):
-    n, k = 517, 4096
-    w, xq, ref = matmul_case(orc, w_type, n, k, 1, 950 + w_type)
-    wd, xd = dev(w), dev(xq)
-    for v in GEMV_VARIANTS:
-        print("gemv variant", w_type, v, flush=True)
-        with env(**v) as b:
-            got = b.matvec(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd).cpu().numpy()
-        assert_close_1e3(got, ref.ravel())
+    # one 4096-element slice, and a down-projection-like shape of 3.5 slices
+    for n, k in [(517, 4096), (203, 14336)]:
+        w, xq, ref = matmul_case(orc, w_type, n, k, 1, 950 + w_type + k)
+        wd, xd = dev(w), dev(xq)
+        for v in GEMV_VARIANTS:
+            print("gemv variant", w_type, n, k, v, flush=True)
+            with env(**v) as b:
+                got = b.matvec(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd).cpu().numpy()
+            assert_close_1e3(got, ref.ravel())
 
 
 MOE_VARIANTS = [dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_NS=3),
