@@ -153,12 +153,25 @@ __device__ __forceinline__ h8 i16x8_to_h8(uint4 w) {
     return r;
 }
 
+// A Q4_K super-block between its MFMAs and its f32 epilogue: the two scale
+// passes' integer sums, the mins sums and the block's d / dmin (this lane's
+// weight row).
 template <int MT>
-__device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* xrow, const uint8_t* xd, int mbase,
-                                            int g2, float (&acc)[MT][16]) {
+struct KQ4Part {
+    v16i ch[MT], cl[MT];
+    f32x16 cm[MT];
+    float d, dmin;
+};
+
+template <int MT>
+__device__ __forceinline__ void kq4_mma(const uint8_t* wrow, const uint8_t* xrow, int g2, KQ4Part<MT>& p) {
     constexpr int XRS = KQ4::XRS;
     const uint4 hdr = *reinterpret_cast<const uint4*>(wrow);
-    const float d = f16_bits_to_f32(hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(hdr.x >> 16);
+    p.d = f16_bits_to_f32(hdr.x & 0xFFFFu);
+    p.dmin = f16_bits_to_f32(hdr.x >> 16);
+    // kept as an f32 register: folded into the epilogue's 32 FMAs the
+    // conversion becomes v_fma_mix_f32, which issues slower than v_fma_f32
+    asm volatile("" : "+v"(p.dmin));
     // get_scale_min_k4 (gguf.rs:825-837) for the eight sub-blocks, bytewise
     const uint32_t scA = hdr.y & 0x3F3F3F3Fu;
     const uint32_t scB = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
@@ -178,14 +191,12 @@ __device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* 
         bmin[2 * q] = m;
         bmin[2 * q + 1] = m;
     }
-    f32x16 cm[MT];
     #pragma unroll
     for (int t = 0; t < MT; t++) {
         const h8 amin = i16x8_to_h8(*reinterpret_cast<const uint4*>(xrow + 32 * t * XRS + 256));
         const f32x16 z = {};
-        cm[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, bmin, z, 0, 0, 0);
+        p.cm[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(amin, bmin, z, 0, 0, 0);
     }
-    v16i ch[MT], cl[MT];
     #pragma unroll
     for (int pr = 0; pr < 4; pr++) {
         // sub-blocks 2pr (low nibbles) and 2pr+1 (high nibbles) share qs[32pr + 16g2 .. +16)
@@ -204,21 +215,33 @@ __device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* 
             for (int t = 0; t < MT; t++) {
                 const v4i a = *reinterpret_cast<const v4i*>(xrow + 32 * t * XRS + 32 * j);
                 const v16i z = {};
-                ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? ch[t] : z, 0, 0, 0);
-                cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? cl[t] : z, 0, 0, 0);
+                p.ch[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bh, j ? p.ch[t] : z, 0, 0, 0);
+                p.cl[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bl, j ? p.cl[t] : z, 0, 0, 0);
             }
         }
     }
-    float dx[MT][16];
-    kq_dx<MT>(xd, mbase, g2, dx);
+}
+
+template <int MT>
+__device__ __forceinline__ void kq4_epilogue(const KQ4Part<MT>& p, const float (&dx)[MT][16], float (&acc)[MT][16]) {
     #pragma unroll
     for (int t = 0; t < MT; t++)
         #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int c = (ch[t][r] << 3) + cl[t][r];
-            const float v = __builtin_fmaf(-dmin, cm[t][r], d * (float)c);
+            const int c = (p.ch[t][r] << 3) + p.cl[t][r];
+            const float v = __builtin_fmaf(-p.dmin, p.cm[t][r], p.d * (float)c);
             acc[t][r] = __builtin_fmaf(dx[t][r], v, acc[t][r]);
         }
+}
+
+template <int MT>
+__device__ __forceinline__ void kq4_compute(const uint8_t* wrow, const uint8_t* xrow, const uint8_t* xd, int mbase,
+                                            int g2, float (&acc)[MT][16]) {
+    KQ4Part<MT> p;
+    kq4_mma<MT>(wrow, xrow, g2, p);
+    float dx[MT][16];
+    kq_dx<MT>(xd, mbase, g2, dx);
+    kq4_epilogue<MT>(p, dx, acc);
 }
 
 // ---- Q6_K super-block --------------------------------------------------------
@@ -476,6 +499,47 @@ __device__ __forceinline__ void kq_step(uint8_t* const (&stages)[KQ_MAX_NS], int
     kq_compute<F, BM, NW>(stages[S] + sub, KG * b + kg, wave, l, acc);
 }
 
+// The Q4_K two-K-group step with group 1's epilogue deferred: group 0 runs
+// MFMAs then its epilogue, group 1 first the epilogue of its previous
+// super-block (kept in registers with its activation scales) and then its
+// MFMAs, so on each SIMD one group's f32 epilogue runs beside the other
+// group's MFMAs.  The dx reads of every wave have landed before the barrier
+// (lgkmcnt 0), because the next loads into the stage are issued after it.
+template <int BM, int NW, int NS, int S>
+__device__ __forceinline__ void kq4_step_defer(uint8_t* const (&stages)[KQ_MAX_NS], int b, int nst, i32x4v xr,
+                                               i32x4v wr, const KQOff<KQ4, BM, NW>& off, int kg, int wave, int l,
+                                               KQ4Part<KQL<KQ4, BM, NW>::MTW>& part,
+                                               float (&dxs)[KQL<KQ4, BM, NW>::MTW][16],
+                                               float (&acc)[KQL<KQ4, BM, NW>::MTW][16]) {
+    using L = KQL<KQ4, BM, NW>;
+    constexpr int MT = L::MTW;
+    if (b >= nst) return;
+    if (b + NS - 2 < nst) wait_vmcnt<(NS - 2) * L::LOADS_MIN>();
+    else wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int sub = kg * L::STAGE;
+    const int n = l & 31, g2 = l >> 5;
+    const int slice = wave & 3, mbase = 32 * MT * (wave >> 2);
+    const uint8_t* st = stages[S] + sub;
+    if (kg == 1 && b > 0) kq4_epilogue<MT>(part, dxs, acc);
+    if (b + NS - 1 < nst) kq_issue<KQ4, BM, NW>(stages[(S + NS - 1) % NS] + sub, xr, wr, off, 2 * (b + NS - 1) + kg, wave);
+    kq4_mma<MT>(st + L::W + (32 * slice + n) * KQ4::RS, st + L::XQ + (mbase + n) * KQ4::XRS + 16 * g2, g2, part);
+    kq_dx<MT>(st + L::XD, mbase, g2, dxs);
+    if (kg == 0) kq4_epilogue<MT>(part, dxs, acc);
+}
+
+template <int BM, int NW, int NS, int... S>
+__device__ __forceinline__ void kq4_round_defer(std::integer_sequence<int, S...>, uint8_t* const (&stages)[KQ_MAX_NS],
+                                                int b, int nst, i32x4v xr, i32x4v wr, const KQOff<KQ4, BM, NW>& off,
+                                                int kg, int wave, int l, KQ4Part<KQL<KQ4, BM, NW>::MTW>& part,
+                                                float (&dxs)[KQL<KQ4, BM, NW>::MTW][16],
+                                                float (&acc)[KQL<KQ4, BM, NW>::MTW][16]) {
+    (kq4_step_defer<BM, NW, NS, S>(stages, b + S, nst, xr, wr, off, kg, wave, l, part, dxs, acc), ...);
+}
+
 // One BM x 128 output tile: rows [m0, m0 + BM) of the `count` activation rows
 // at X (row bytes xrb) against weight rows [n0, n0 + 128) of W; results to
 // Y[row * N + col].  All waves of the workgroup call it with the same values.
@@ -546,7 +610,7 @@ __device__ __forceinline__ void kq_reduce_groups(uint8_t* lds, float (&acc)[KQL<
     }
 }
 
-template <class F, int BM, int NS, int NW, int KG>
+template <class F, int BM, int NS, int NW, int KG, bool DEFER = false>
 __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], const uint8_t* W, uint32_t wrb, const uint8_t* X,
                                         uint32_t xrb, float* Y, int count, int N, int nsb, int m0, int n0, int kg,
                                         int wave, int l, int kb0 = 0) {
@@ -569,12 +633,132 @@ __device__ __forceinline__ void kq_tile(uint8_t* const (&stages)[KQ_MAX_NS], con
     #pragma unroll
     for (int s = 0; s < NS - 1; s++)
         if (s < nst) kq_issue<F, BM, NW>(stages[s] + kg * L::STAGE, xr, wr, off, KG * s + kg, wave);
-    for (int b = 0; b < nst; b += NS)
-        kq_round<F, BM, NW, NS, KG>(std::make_integer_sequence<int, NS>{}, stages, b, nst, xr, wr, off, kg, wave, l,
-                                    acc);
+    if constexpr (DEFER) {
+        static_assert(F::TYPE == TYPE_Q4_K && KG == 2 && BM >= 32, "deferred epilogue: Q4_K, two K-groups");
+        KQ4Part<MT> part;
+        float dxs[MT][16];
+        for (int b = 0; b < nst; b += NS)
+            kq4_round_defer<BM, NW, NS>(std::make_integer_sequence<int, NS>{}, stages, b, nst, xr, wr, off, kg, wave,
+                                        l, part, dxs, acc);
+        if (kg == 1 && nst > 0) kq4_epilogue<MT>(part, dxs, acc);
+    } else {
+        for (int b = 0; b < nst; b += NS)
+            kq_round<F, BM, NW, NS, KG>(std::make_integer_sequence<int, NS>{}, stages, b, nst, xr, wr, off, kg, wave,
+                                        l, acc);
+    }
 
     if constexpr (KG > 1) kq_reduce_groups<F, BM, NW, KG>(stages[0], acc, kg, wave, l);
     if (kg == 0) kq_store<F, BM, NW>(acc, Y, count, N, m0, n0, wave, l);
+}
+
+// ---- Q4_K, 64 x 128 tiles, two K-groups, weight pairs ---------------------------
+// A step's two super-blocks (one per K-group) are adjacent in each weight
+// row, so the stage takes them as one 288-byte run per row (plus a pad piece:
+// 304-byte rows keep a fragment read's 16 lanes on distinct LDS banks), loaded
+// by all eight waves and read by both groups; each group's activation rows
+// and scales keep their own part of the stage.  Per load instruction the
+// weight lanes then touch ~11 cache lines instead of ~15 for 144-byte runs
+// (measured on MI355X: the load pipeline of the C4 GEMM alone, arithmetic
+// removed in a timing copy, took 20.5 us with the 144-byte weight runs and
+// 13.3 us with fully contiguous weight runs).
+struct KQ4P {
+    using L = KQL<KQ4, 64, 4>;
+    static constexpr int X_INSTR_ALL = L::X_INSTR_ALL;           // 19
+    static constexpr int X_INSTR = L::X_INSTR;                   // per wave of a group
+    static constexpr int XD = X_INSTR_ALL * 1024;                // a group's activation scales
+    static constexpr int GROUP = XD + 256;
+    static constexpr int W = 2 * GROUP;
+    static constexpr int WRS = 304, WPIECES = 19;
+    static constexpr int W_INSTR_ALL = KQ_BN * WPIECES / 64;     // 38
+    static constexpr int W_INSTR = (W_INSTR_ALL + 7) / 8;        // per wave of the workgroup
+    static constexpr int STAGE = W + KQ_BN * WRS;
+    static_assert(KQ_BN * WPIECES % 64 == 0, "weight pairs are whole load instructions");
+    static_assert(2 * STAGE <= 163840, "two stages fit the LDS");
+};
+
+struct KQ4POff {
+    uint32_t x[KQ4P::X_INSTR];
+    uint32_t w[KQ4P::W_INSTR];
+    uint32_t xd;
+};
+
+__device__ __forceinline__ void kq4p_offsets(KQ4POff& o, uint32_t xrb, uint32_t wrb, int kg, int wave, int l) {
+    #pragma unroll
+    for (int q = 0; q < KQ4P::X_INSTR; q++) {
+        const int p = (q * 4 + wave) * 64 + l, r = p / KQ4::XC, c = p - r * KQ4::XC;
+        o.x[q] = (uint32_t)r * xrb + 4u + 16u * (uint32_t)(c < KQ4::XC - 1 ? c : 0);
+    }
+    #pragma unroll
+    for (int q = 0; q < KQ4P::W_INSTR; q++) {
+        const int p = (q * 8 + 4 * kg + wave) * 64 + l, row = p / KQ4P::WPIECES, piece = p - row * KQ4P::WPIECES;
+        o.w[q] = (uint32_t)row * wrb + 16u * (uint32_t)(piece < KQ4P::WPIECES - 1 ? piece : 0);
+    }
+    o.xd = (uint32_t)l * xrb;
+}
+
+// the loads of step b (super-blocks 2b and 2b + 1) into one stage
+__device__ __forceinline__ void kq4p_issue(uint8_t* stage, i32x4v xr, i32x4v wr, const KQ4POff& o, int b, int kg,
+                                           int wave) {
+    const uint32_t xs = (uint32_t)(2 * b + kg) * Q8_K_BYTES, ws = (uint32_t)(2 * b) * Q4_K_BYTES;
+    uint8_t* gx = stage + kg * KQ4P::GROUP;
+    #pragma unroll
+    for (int q = 0; q < KQ4P::X_INSTR; q++) {
+        const int idx = q * 4 + wave;
+        if (idx < KQ4P::X_INSTR_ALL) lds_load16(xr, gx + 1024 * idx, o.x[q], xs);
+    }
+    #pragma unroll
+    for (int q = 0; q < KQ4P::W_INSTR; q++) {
+        const int idx = q * 8 + 4 * kg + wave;
+        if (idx < KQ4P::W_INSTR_ALL) lds_load16(wr, stage + KQ4P::W + 1024 * idx, o.w[q], ws);
+    }
+    if (wave == 0) lds_load4(xr, gx + KQ4P::XD, o.xd, xs);
+}
+
+template <bool DEFER, int S>
+__device__ __forceinline__ void kq4p_step(uint8_t* const (&stages)[KQ_MAX_NS], int b, int nst, i32x4v xr, i32x4v wr,
+                                          const KQ4POff& off, int kg, int wave, int l, KQ4Part<2>& part,
+                                          float (&dxs)[2][16], float (&acc)[2][16]) {
+    if (b >= nst) return;
+    wait_vmcnt<0>();
+    if constexpr (DEFER) wait_lgkmcnt0();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int n = l & 31, g2 = l >> 5;
+    const uint8_t* st = stages[S];
+    const uint8_t* gx = st + kg * KQ4P::GROUP;
+    if (DEFER && kg == 1 && b > 0) kq4_epilogue<2>(part, dxs, acc);
+    if (b + 1 < nst) kq4p_issue(stages[S ^ 1], xr, wr, off, b + 1, kg, wave);
+    kq4_mma<2>(st + KQ4P::W + (32 * wave + n) * KQ4P::WRS + KQ4::BB * kg, gx + n * KQ4::XRS + 16 * g2, g2, part);
+    kq_dx<2>(gx + KQ4P::XD, 0, g2, dxs);
+    if (!DEFER || kg == 0) kq4_epilogue<2>(part, dxs, acc);
+}
+
+template <bool DEFER>
+__device__ __forceinline__ void kq4p_tile(uint8_t* const (&stages)[KQ_MAX_NS], const uint8_t* W, uint32_t wrb,
+                                          const uint8_t* X, uint32_t xrb, float* Y, int count, int N, int nsb, int m0,
+                                          int n0, int kg, int wave, int l, int kb0) {
+    const int nst = nsb / 2;
+    const uint32_t xk = (uint32_t)kb0 * Q8_K_BYTES, wk = (uint32_t)kb0 * Q4_K_BYTES;
+    const i32x4v xr = make_rsrc4(X + (size_t)m0 * xrb + xk, (uint32_t)((size_t)(count - m0) * xrb) - xk);
+    const i32x4v wr = make_rsrc4(W + (size_t)n0 * wrb + wk, (uint32_t)((size_t)(N - n0) * wrb) - wk);
+    float acc[2][16];
+    #pragma unroll
+    for (int t = 0; t < 2; t++)
+        #pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+    KQ4POff off;
+    kq4p_offsets(off, xrb, wrb, kg, wave, l);
+    if (nst > 0) kq4p_issue(stages[0], xr, wr, off, 0, kg, wave);
+    KQ4Part<2> part;
+    float dxs[2][16];
+    for (int b = 0; b < nst; b += 2) {
+        kq4p_step<DEFER, 0>(stages, b, nst, xr, wr, off, kg, wave, l, part, dxs, acc);
+        kq4p_step<DEFER, 1>(stages, b + 1, nst, xr, wr, off, kg, wave, l, part, dxs, acc);
+    }
+    if (DEFER && kg == 1 && nst > 0) kq4_epilogue<2>(part, dxs, acc);
+    kq_reduce_groups<KQ4, 64, 4, 2>(stages[0], acc, kg, wave, l);
+    if (kg == 0) kq_store<KQ4, 64, 4>(acc, Y, count, N, m0, n0, wave, l);
 }
 
 // ---- grouped: one pipeline across the workgroup's tiles ------------------------
@@ -741,7 +925,7 @@ struct KQExperts {
 // there: every workgroup builds the per-expert tile prefix from the device
 // offsets (lane e holds expert e) and strides over the flattened
 // (expert, m-tile, mat, n-tile) list, so no host round trip is needed.
-template <class F, int BM, int NS, int NW, int KG, bool GROUPED>
+template <class F, int BM, int NS, int NW, int KG, bool GROUPED, bool DEFER = false, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW * KG, 1)
 void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32_t xrb, float* __restrict__ Y, int M,
                int N, int nsb, int tiles_m, int tiles_n, const int32_t* __restrict__ offsets, int ne, int nmat,
@@ -749,7 +933,9 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
     static_assert(NS >= 2 && NS <= KQ_MAX_NS, "stage count");
     static_assert(KG == 1 || !GROUPED, "K-groups split one tile's super-blocks (ungrouped launches)");
     using L = KQL<F, BM, NW>;
-    constexpr int SB = KG * L::STAGE;
+    static_assert(!PAIR || (F::TYPE == TYPE_Q4_K && BM == 64 && NW == 4 && KG == 2 && NS == 2 && !GROUPED),
+                  "weight pairs: Q4_K 64 x 128 tiles, two K-groups, two stages");
+    constexpr int SB = PAIR ? KQ4P::STAGE : KG * L::STAGE;
     // one array per stage (stages beyond NS are unused 16-byte stubs)
     __shared__ __align__(16) uint8_t st0[SB];
     __shared__ __align__(16) uint8_t st1[SB];
@@ -772,8 +958,12 @@ void kq_kernel(KQWeights wt, uint32_t wrb, const uint8_t* __restrict__ X, uint32
         int tile = blockIdx.x - slice * n_tiles;
         if (xcd_order && (n_tiles & 7) == 0) tile = (tile & 7) * (n_tiles >> 3) + (tile >> 3);
         const int mt = tile % tiles_m, ntile = tile / tiles_m;
-        kq_tile<F, BM, NS, NW, KG>(stages, wt.w[0], wrb, X, xrb, Y + (size_t)slice * M * N, M, N, nsb_k, mt * BM,
-                                   ntile * KQ_BN, kg, wave, l, slice * nsb_k);
+        if constexpr (PAIR)
+            kq4p_tile<DEFER>(stages, wt.w[0], wrb, X, xrb, Y + (size_t)slice * M * N, M, N, nsb_k, mt * BM,
+                             ntile * KQ_BN, kg, wave, l, slice * nsb_k);
+        else
+            kq_tile<F, BM, NS, NW, KG, DEFER>(stages, wt.w[0], wrb, X, xrb, Y + (size_t)slice * M * N, M, N, nsb_k,
+                                              mt * BM, ntile * KQ_BN, kg, wave, l, slice * nsb_k);
     } else {
         const KQExperts<BM> ex(wt, X, xrb, Y, N, nsb, tiles_n, offsets, ne, nmat, ymat, ks, ykstride, l);
         kq_grouped_stream<F, BM, NS, NW>(stages, ex, ex.total, ex.nsb_k, xrb, wrb, N, wave, l);
@@ -808,7 +998,7 @@ struct KQArgs {
     size_t ykstride;
 };
 
-template <class F, int BM, int NS, int NW, bool GROUPED, int KG = 1>
+template <class F, int BM, int NS, int NW, bool GROUPED, int KG = 1, bool DEFER = false, bool PAIR = false>
 static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     const int tiles_n = (a.N + KQ_BN - 1) / KQ_BN;
     int tiles_m = (a.M + BM - 1) / BM;
@@ -825,7 +1015,7 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
     // ungrouped K slices: whole K-group steps, even first super-blocks
     if (!GROUPED && (a.nsb % a.ks != 0 || (a.ks > 1 && (a.nsb / a.ks) % 2 != 0))) return hipErrorInvalidValue;
     if ((GROUPED ? a.nsb : a.nsb / a.ks) % KG != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, KG, GROUPED>), dim3(grid), dim3(64 * NW * KG), 0, s, a.wt, a.wrb, a.X, a.xrb,
+    hipLaunchKernelGGL((kq_kernel<F, BM, NS, NW, KG, GROUPED, DEFER, PAIR>), dim3(grid), dim3(64 * NW * KG), 0, s, a.wt, a.wrb, a.X, a.xrb,
                        a.Y, a.M, a.N, a.nsb, tiles_m, tiles_n, a.offsets, a.ne, a.nmat, a.ymat, a.ks, a.ykstride,
                        tuning_env(TUNE_GEMM_XCD, 1));   // XCD-aware tile order (ungrouped)
     return hipGetLastError();
@@ -863,7 +1053,16 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
         if (kg == 2 && (a.nsb / a.ks) % 2 == 0) {
             if constexpr (F::TYPE == TYPE_Q4_K) {
                 if (bm == 65) return kq_launch_t<F, 64, 2, 8, GROUPED, 2>(a, s);
-                if (bm == 64) return kq_launch_t<F, 64, 2, 4, GROUPED, 2>(a, s);
+                if (bm == 64) {
+                    // BARQ_GEMM_DEFER: bit 0 defers group 1's epilogue, bit 1 loads weight
+                    // pairs; measured at C4 on MI355X (alternating runs, one process):
+                    // 24.7-24.8 us with neither, 23.7-24.3 / 24.3-24.4 with one, 23.6-23.9 with both
+                    const int mode = tuning_env(TUNE_GEMM_DEFER, 3);
+                    if (mode == 3) return kq_launch_t<F, 64, 2, 4, GROUPED, 2, true, true>(a, s);
+                    if (mode == 2) return kq_launch_t<F, 64, 2, 4, GROUPED, 2, false, true>(a, s);
+                    if (mode == 1) return kq_launch_t<F, 64, 2, 4, GROUPED, 2, true>(a, s);
+                    return kq_launch_t<F, 64, 2, 4, GROUPED, 2>(a, s);
+                }
                 return kq_launch_t<F, 32, 2, 4, GROUPED, 2>(a, s);
             } else {
                 return kq_launch_t<F, 32, 2, 4, GROUPED, 2>(a, s);
