@@ -25,7 +25,9 @@
 // order from the reference's sequential ones.
 #include "common.hpp"
 #include "launch.hpp"
+#include "mfma_common.hpp"
 
+#include <atomic>
 #include <cstdlib>
 
 namespace barq {
@@ -351,9 +353,183 @@ void attn_combine_kernel(const float* __restrict__ part, int n_split, int n_head
     }
 }
 
+// ---- prompt chunks on MFMA ----------------------------------------------------
+// For q_len >= 32 (BARQ_ATTN_MFMA_MIN_Q) and head_dim 128 a workgroup covers
+// 32 query rows of W query heads that share one kv head (one wave per head)
+// and walks the visible positions in blocks of 32 with
+// v_mfma_f32_32x32x2_f32 (f32 products and sums, as the VALU path):
+//   S^T[kv, q] = K[kv, :] . Q[q, :]   A = K rows (lane c: row c, dims 64 g ..),
+//                                     B = Q^T (lane c: query c, the same dims)
+//   online softmax per query column: a lane holds 16 positions of its query,
+//   the other 16 sit in lane c ^ 32
+//   O^T[d, q] += V[kv, d] P[q, kv]    B = P^T straight from S^T's registers
+//                                     (step s pairs positions 8(s/4) + s%4 and
+//                                     +4, which lanes c and c + 32 hold as
+//                                     register s); A = V^T with output row i of
+//                                     block b standing for dim 4 i + b, so one
+//                                     16-byte read per lane feeds the four blocks.
+// Each block's K and V rows are copied once per workgroup into LDS by
+// buffer->LDS loads one block ahead (two stages), in rows of 528 bytes (one
+// pad piece: conflict-free fragment reads); rows at or past kv_len read as
+// zero.  Exponentials are base 2 on pre-scaled scores, like the split kernel.
+typedef float f32x16a __attribute__((ext_vector_type(16)));
+constexpr int AM_RS = 528, AM_PIECES = 33, AM_BLK = 32 * AM_RS;
+constexpr int AM_INSTR = (32 * AM_PIECES + 63) / 64;   // load instructions per K or V block (17)
+
+// the buffer->LDS loads of one block (K and V) split over the workgroup's W waves
+template <int W>
+__device__ __forceinline__ void am_issue(uint8_t* stage, i32x4v kr, i32x4v vr, uint32_t soff, int wave, int l) {
+    #pragma unroll
+    for (int q = 0; q < (2 * AM_INSTR + W - 1) / W; q++) {
+        const int idx = q * W + wave;
+        if (idx < 2 * AM_INSTR) {
+            const int kvsel = idx >= AM_INSTR, ii = idx - kvsel * AM_INSTR;
+            const int p = ii * 64 + l, row = p / AM_PIECES, piece = p - row * AM_PIECES;
+            if (p < 32 * AM_PIECES) {
+                const uint32_t voff = (uint32_t)row * 512u + 16u * (uint32_t)(piece < 32 ? piece : 0);
+                lds_load16(kvsel ? vr : kr, stage + kvsel * AM_BLK + 1024 * ii, voff, soff);
+            }
+        }
+    }
+}
+
+// One 32-row query block qb of the workgroup's W heads.
+template <int W>
+__device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const float* __restrict__ q,
+                                          const float* __restrict__ kc, const float* __restrict__ vc, size_t layer_off,
+                                          size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
+                                          long long start_pos, float score_scale, float* __restrict__ out, int qb) {
+    constexpr int HD = 128;
+    const int l = threadIdx.x & 63, c = l & 31, g = l >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = (int)blockIdx.y * W + wave;
+    const int hk = (int)((long long)h * n_head_kv / n_head);   // the same for the W heads
+    const int i0 = qb * 32, qi = i0 + c;
+    const bool q_ok = qi < q_len;
+
+    const float* kh = kc + layer_off + (size_t)hk * head_stride;
+    const float* vh = vc + layer_off + (size_t)hk * head_stride;
+    const i32x4v kr = make_rsrc4(kh, (uint32_t)kv_len * 512u);
+    const i32x4v vr = make_rsrc4(vh, (uint32_t)kv_len * 512u);
+    const int i_last = min(i0 + 31, q_len - 1);
+    const long long vis_last = start_pos + i_last + 1;
+    const int j_end = (int)(vis_last < kv_len ? vis_last : kv_len);
+    const int nblk = (j_end + 31) / 32;
+    if (nblk > 0) am_issue<W>(lds[0], kr, vr, 0u, wave, l);
+
+    float qv[64];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(q + ((size_t)h * q_len + (q_ok ? qi : 0)) * HD + 64 * g);
+        #pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const float4 t = q_ok ? qp[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qv[4 * u] = t.x; qv[4 * u + 1] = t.y; qv[4 * u + 2] = t.z; qv[4 * u + 3] = t.w;
+        }
+    }
+    const long long vis_q = start_pos + qi + 1;   // this lane's query sees positions below vis_q
+
+    f32x16a o0 = {}, o1 = {}, o2 = {}, o3 = {};
+    float m = -INFINITY, lsum = 0.0f;
+    for (int b = 0; b < nblk; b++) {
+        const int j0 = 32 * b;
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        __syncthreads();   // block b is in its stage; every wave is done with the other one
+        if (b + 1 < nblk) am_issue<W>(lds[(b + 1) & 1], kr, vr, (uint32_t)(j0 + 32) * 512u, wave, l);
+        const uint8_t* ks = lds[b & 1];
+        const uint8_t* vs = ks + AM_BLK;
+        f32x16a sa = {}, sb = {};
+        #pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const float4 kk = *reinterpret_cast<const float4*>(ks + c * AM_RS + 256 * g + 16 * u);
+            sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qv[4 * u], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qv[4 * u + 1], sb, 0, 0, 0);
+            sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qv[4 * u + 2], sa, 0, 0, 0);
+            sb = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qv[4 * u + 3], sb, 0, 0, 0);
+        }
+        float sc[16];
+        float bm = -INFINITY;
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int kv = j0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            const bool vis = kv < kv_len && kv < vis_q;
+            sc[r] = vis ? (sa[r] + sb[r]) * score_scale : -INFINITY;
+            bm = fmaxf(bm, sc[r]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        // position 0 is visible to every query, so mn is finite from the first block on
+        const float mn = fmaxf(m, bm);
+        const float corr = fast_exp2(m - mn);   // 0 while m is -inf
+        m = mn;
+        float p[16];
+        float rs = 0.0f;
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            p[r] = fast_exp2(sc[r] - mn);   // 0 for masked positions
+            rs += p[r];
+        }
+        rs += __shfl_xor(rs, 32);
+        lsum = lsum * corr + rs;
+        o0 *= corr; o1 *= corr; o2 *= corr; o3 *= corr;
+        #pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const int kv = 8 * (st >> 2) + 4 * g + (st & 3);
+            const float4 vv = *reinterpret_cast<const float4*>(vs + kv * AM_RS + 16 * c);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, p[st], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, p[st], o1, 0, 0, 0);
+            o2 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, p[st], o2, 0, 0, 0);
+            o3 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[st], o3, 0, 0, 0);
+        }
+    }
+    if (q_ok) {
+        float* op = out + ((size_t)qi * n_head + h) * HD;
+        #pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int i = 8 * (r >> 2) + 4 * g + (r & 3);
+            *reinterpret_cast<float4*>(op + 4 * i) = make_float4(o0[r] / lsum, o1[r] / lsum, o2[r] / lsum, o3[r] / lsum);
+        }
+    }
+}
+
+// Causal prompts leave query block qb with qb + 1 position blocks (plus the
+// cached prefix).  PAIR: workgroup x takes the long block nqb - 1 - x and
+// then the short block x, so every workgroup has about the same work (used
+// when the pairs alone fill the CUs); otherwise the longest blocks start first.
+template <int W, bool PAIR>
+__global__ __launch_bounds__(64 * W)
+void attn_mfma_kernel(const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+                      size_t layer_off, size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
+                      long long start_pos, float score_scale, float* __restrict__ out) {
+    __shared__ __align__(16) uint8_t lds[2][2 * AM_BLK];
+    const int nqb = (q_len + 31) / 32, x = blockIdx.x;
+    const int qb_long = nqb - 1 - x;
+    am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale, out,
+                 qb_long);
+    if (PAIR && x < qb_long) {
+        __syncthreads();   // every wave is done with the stages
+        am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale,
+                     out, x);
+    }
+}
+
+static int attn_mfma_min_q() { return tuning_env(TUNE_ATTN_MFMA_MIN_Q, 32); }
+
+static int cu_count_attn() {
+    static std::atomic<int> n[64] = {};   // per device; racing callers store the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = n[dev].load(std::memory_order_relaxed);
+    if (!v) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        n[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv) {
+    if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q()) return 0;   // the MFMA path keeps no partials
     int ns = 0, chunk = 0;
     attention_plan(n_head, n_head_kv, q_len, kv_len, &ns, &chunk);
     return ns > 1 ? (size_t)ns * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
@@ -409,6 +585,24 @@ static hipError_t attn_launch_hd(const AttnArgs& a, hipStream_t s) {
 
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
     if (a.q_len == 0 || a.n_head == 0) return hipSuccess;
+    if (a.head_dim == 128 && a.q_len >= (size_t)attn_mfma_min_q()) {
+        const float scale = (1.0f / sqrtf(128.0f)) * LOG2E;
+        // W query heads per workgroup share one kv head (W divides the group size)
+        const size_t grp = (a.n_head_kv && a.n_head % a.n_head_kv == 0) ? a.n_head / a.n_head_kv : 1;
+        const int w = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1;
+        const unsigned nqb = (unsigned)((a.q_len + 31) / 32), groups = (unsigned)(a.n_head / w);
+        const bool pair = (size_t)(nqb / 2) * groups >= (size_t)cu_count_attn();
+        const dim3 grid(pair ? (nqb + 1) / 2 : nqb, groups);
+#define BARQ_AM_LAUNCH(W_, P_)                                                                                    \
+    hipLaunchKernelGGL((attn_mfma_kernel<W_, P_>), grid, dim3(64 * W_), 0, s, a.q, a.k, a.v, a.layer_off,           \
+                       a.head_stride, (int)a.n_head, (int)a.n_head_kv, (int)a.q_len, (int)a.kv_len,               \
+                       (long long)a.start_pos, scale, a.out)
+        if (w == 4) { if (pair) BARQ_AM_LAUNCH(4, true); else BARQ_AM_LAUNCH(4, false); }
+        else if (w == 2) { if (pair) BARQ_AM_LAUNCH(2, true); else BARQ_AM_LAUNCH(2, false); }
+        else { if (pair) BARQ_AM_LAUNCH(1, true); else BARQ_AM_LAUNCH(1, false); }
+#undef BARQ_AM_LAUNCH
+        return hipGetLastError();
+    }
     switch (a.head_dim) {
     case 64: return attn_launch_hd<64>(a, s);
     case 128: return attn_launch_hd<128>(a, s);

@@ -133,6 +133,17 @@ ATTN_CASES = [
     (4, 2, 64, 16, 16, 0, 16),            # a prompt from position 0
     (8, 2, 128, 3, 10, 2, 10),            # start_pos + q_len < kv_len: masked tail
     (8, 2, 128, 1, 50, 49, 80),           # kv_len below the layer length
+    # prompt chunks of 32+ rows (head_dim 128: the MFMA kernel)
+    (32, 8, 128, 32, 32, 0, 32),          # one query block from position 0
+    (32, 8, 128, 100, 150, 50, 160),      # ragged last block, chunk after a prefix
+    (8, 2, 128, 64, 64, 0, 64),
+    (12, 6, 128, 40, 300, 260, 300),      # 2 per kv head
+    (6, 4, 128, 33, 33, 0, 40),           # irregular grouping
+    (8, 2, 128, 40, 100, 20, 100),        # start_pos + q_len < kv_len: masked tail
+    (32, 8, 128, 512, 512, 0, 512),       # a Llama-3-8B prompt of 512 tokens
+    (4, 2, 64, 48, 48, 0, 48),            # head_dim 64 stays on the split kernel
+    (32, 32, 128, 512, 512, 0, 512),      # query blocks paired (long + short) per workgroup
+    (64, 64, 128, 288, 300, 12, 300),     # paired, odd block count (the middle block alone)
 ]
 
 
