@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "barq-inference_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+F32_MFMA_PEAK_TFLOPS = 157.3   # dense f32 matrix peak
 METRIC = "Q4_K GEMV achieved HBM GB/s (% of peak) + µs/call at Llama-3-8B shapes, 1 GPU"
 
 
@@ -655,10 +656,21 @@ def bench_attn(args):
         t_cpu = time.perf_counter() - t0
     err = float(np.max(np.abs(got - ref)) / np.max(np.abs(vh)))
     cpu_gbs = alg * calls / t_cpu / 1e9
+    # prompt chunks of 32+ rows run the f32-MFMA kernel: compute-bound
+    mfma = ql >= int(os.environ.get("BARQ_ATTN_MFMA_MIN_Q", "32"))
+    tflops = flops / (ms * 1e-3) / 1e12
+    if mfma:
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s (f32)",
+                "frac": round(tflops / F32_MFMA_PEAK_TFLOPS, 4), "traffic": None, "alg_flops_per_launch": flops,
+                "scope": "one call: the MFMA prompt kernel"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
+                "scope": "one call: the split kernel and the split-combine kernel"}
     result = {
         "metric": f"{'decode' if ql == 1 else 'prompt-chunk'} attention (Llama-3-8B heads, q_len {ql}, kv_len {kv}) "
-                  f"achieved HBM GB/s + us/call, 1 GPU",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                  + ("achieved f32 TFLOP/s + us/call, 1 GPU" if mfma else "achieved HBM GB/s + us/call, 1 GPU"),
+        "value": round(tflops, 2) if mfma else round(gbs, 2), "unit": "TFLOP/s" if mfma else "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"attention 32 q heads / 8 kv heads x 128, q_len {ql}, kv_len {kv}, f32 KV cache",
@@ -666,9 +678,7 @@ def bench_attn(args):
         "us_per_call": round(ms * 1e3, 3), "us_per_call_eager": round(ms_eager * 1e3, 3),
         "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
         "parity_max_err_rel_to_max_v": err,
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
-                     "scope": "one call: the split kernel and the split-combine kernel"},
+        "roofline": roof,
         "cpu_baseline": {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                          "sample": f"{calls} calls of the oracle's compute_attention restatement on layer 0",
                          "us_per_call": round(t_cpu / calls * 1e6, 1)},
