@@ -19,11 +19,11 @@ ROPE_INTERLEAVED = L.ROPE_INTERLEAVED
 ROPE_SPLIT_HALF = L.ROPE_SPLIT_HALF
 
 
-def _empty(shape, like, mem):
+def _empty(shape, like, mem, dtype="float32"):
     if mem == L.MEM_HOST:
-        return np.empty(shape, dtype=np.float32)
+        return np.empty(shape, dtype=np.dtype(dtype))
     import torch
-    return torch.empty(shape, dtype=torch.float32, device=like.device)
+    return torch.empty(shape, dtype=getattr(torch, dtype), device=like.device)
 
 
 def apply_rope(be: Backend, x, seq_len, n_heads, head_dim, start_pos, rope_freq_scale, rope_inv_freq, layout,
@@ -81,6 +81,18 @@ class KVCache:
                                                              n_tokens, start_pos, rope_freq_scale,
                                                              _ptr(rope_inv_freq), layout, mem))
 
+    def append_rope_q(self, layer, q_proj, n_head, k_proj, v_proj, n_tokens, start_pos, rope_freq_scale,
+                      rope_inv_freq, layout, mem=L.MEM_DEVICE, q_out=None):
+        """apply_rope(q) + apply_rope(k) + transpose_heads(v) + append in one
+        launch (transformer.rs:222-245); returns q rotated [n_head, n_tokens, head_dim]."""
+        if q_out is None:
+            q_out = _empty((n_head, n_tokens, self.head_dim), q_proj, mem)
+        L.check(self.be._lib.barq_rocm_kv_cache_append_rope_q(self.be.h, self.c, layer, _ptr(q_proj), n_head,
+                                                               _ptr(q_out), _ptr(k_proj), _ptr(v_proj), n_tokens,
+                                                               start_pos, rope_freq_scale, _ptr(rope_inv_freq),
+                                                               layout, mem))
+        return q_out
+
     def size(self) -> int:
         return self.be._lib.barq_rocm_kv_cache_size(self.c)
 
@@ -130,6 +142,20 @@ def compute_attention(be: Backend, q, cache: KVCache, layer, n_head, n_head_kv, 
     out = _empty((q_len, n_head, head_dim), q, mem)
     L.check(be._lib.barq_rocm_attention(be.h, _ptr(q), cache.c, layer, n_head, n_head_kv, head_dim, q_len, kv_len,
                                         start_pos, _ptr(out), mem))
+    if sync and mem == L.MEM_DEVICE:
+        be.sync()
+    return out
+
+
+def compute_attention_q8k(be: Backend, q, cache: KVCache, layer, n_head, n_head_kv, head_dim, q_len, kv_len,
+                          start_pos, mem=L.MEM_DEVICE, sync=True, out=None):
+    """compute_attention, then the Q8_K quantizer of its rows (the o
+    projection's input): uint8 [q_len, n_head*head_dim/256 * 292]."""
+    nb = n_head * head_dim // 256
+    if out is None:
+        out = _empty((q_len, nb * 292), q, mem, dtype="uint8")
+    L.check(be._lib.barq_rocm_attention_q8k(be.h, _ptr(q), cache.c, layer, n_head, n_head_kv, head_dim, q_len,
+                                            kv_len, start_pos, _ptr(out), mem))
     if sync and mem == L.MEM_DEVICE:
         be.sync()
     return out

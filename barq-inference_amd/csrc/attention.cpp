@@ -192,28 +192,40 @@ int barq_rocm_kv_cache_append(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t
     return ok();
 }
 
-int barq_rocm_kv_cache_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const float* k_proj,
-                                   const float* v_proj, size_t n_tokens, size_t start_pos, float freq_scale,
-                                   const float* inv_freq, int layout, int mem) {
+}  // extern "C"
+
+namespace {
+
+// append_rope, and with q_proj the RoPE of q into q_out ([n_head, n_tokens,
+// head_dim]) in the same launch
+int append_rope_any(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const float* q_proj, size_t n_head,
+                    float* q_out, const float* k_proj, const float* v_proj, size_t n_tokens, size_t start_pos,
+                    float freq_scale, const float* inv_freq, int layout, int mem, const char* who) {
     BARQ_CHECK(check_mem(mem));
     BARQ_CHECK(check_handle(h));
-    if (!c) return fail(BARQ_E_INVALID, "kv_cache_append_rope: null cache");
+    if (!c) return fail(BARQ_E_INVALID, "%s: null cache", who);
     BARQ_CHECK(check_rope_args(c->head_dim, layout));
-    if (layer >= c->n_layers) return ok();
+    if (q_proj && (!q_out || n_head == 0)) return fail(BARQ_E_INVALID, "%s: null q output or no query heads", who);
     if (n_tokens == 0) return ok();
-    if (!k_proj || !v_proj || !inv_freq) return fail(BARQ_E_INVALID, "kv_cache_append_rope: null buffer");
-    if (c->len[layer] + n_tokens > c->max_size)
-        return fail(BARQ_E_INVALID, "kv_cache_append_rope: layer %zu holds %zu of %zu positions, %zu more do not fit",
-                    layer, c->len[layer], c->max_size, n_tokens);
-    if (h->device != c->device) return fail(BARQ_E_INVALID, "kv_cache_append_rope: cache is on another device");
-    BARQ_CHECK(check_int_range(n_tokens * c->n_head_kv * c->head_dim, "kv_cache_append_rope: elements"));
+    if (!k_proj || !v_proj || !inv_freq) return fail(BARQ_E_INVALID, "%s: null buffer", who);
+    // an out-of-range layer appends nothing (the reference returns silently); q is still rotated
+    const bool append = layer < c->n_layers;
+    if (append && c->len[layer] + n_tokens > c->max_size)
+        return fail(BARQ_E_INVALID, "%s: layer %zu holds %zu of %zu positions, %zu more do not fit", who, layer,
+                    c->len[layer], c->max_size, n_tokens);
+    if (!append && !q_proj) return ok();
+    if (h->device != c->device) return fail(BARQ_E_INVALID, "%s: cache is on another device", who);
+    const size_t hd = c->head_dim, n = n_tokens * c->n_head_kv * hd, nq = q_proj ? n_tokens * n_head * hd : 0;
+    BARQ_CHECK(check_int_range(n, "kv_cache_append_rope: elements"));
+    BARQ_CHECK(check_int_range(n_tokens * (n_head + 2 * c->n_head_kv) * hd, "kv_cache_append_rope: elements"));
     DeviceGuard g(h);
-    const size_t hd = c->head_dim, n = n_tokens * c->n_head_kv * hd;
-    const size_t dst_off = layer * c->layer_stride() + c->len[layer] * hd;
-    const float *kp = k_proj, *vp = v_proj, *fp = inv_freq;
+    const size_t dst_off = append ? layer * c->layer_stride() + c->len[layer] * hd : 0;
+    const float *qp = q_proj, *kp = k_proj, *vp = v_proj, *fp = inv_freq;
+    float* qo = q_out;
     if (mem == BARQ_MEM_HOST) {
         Arena a;
         const size_t ok_ = a.add(n * 4), ov = a.add(n * 4), of = a.add(hd / 2 * 4);
+        const size_t oq = nq ? a.add(nq * 4) : 0, oqo = nq ? a.add(nq * 4) : 0;
         BARQ_CHECK(ensure_ws(h, a.used));
         BARQ_HIP(hipMemcpyAsync(at<float>(h, ok_), k_proj, n * 4, hipMemcpyHostToDevice, h->stream));
         BARQ_HIP(hipMemcpyAsync(at<float>(h, ov), v_proj, n * 4, hipMemcpyHostToDevice, h->stream));
@@ -221,28 +233,74 @@ int barq_rocm_kv_cache_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, s
         kp = at<float>(h, ok_);
         vp = at<float>(h, ov);
         fp = at<float>(h, of);
+        if (nq) {
+            BARQ_HIP(hipMemcpyAsync(at<float>(h, oq), q_proj, nq * 4, hipMemcpyHostToDevice, h->stream));
+            qp = at<float>(h, oq);
+            qo = at<float>(h, oqo);
+        }
     }
-    BARQ_CHECK(launched(barq::rope_launch(layout, kp, c->k + dst_off, n_tokens, c->n_head_kv, hd, start_pos, freq_scale,
-                                          fp, c->head_stride(), h->stream), "kv_cache_append_rope (k)"));
-    BARQ_CHECK(launched(barq::transpose_heads_launch(vp, c->v + dst_off, n_tokens, c->n_head_kv, hd, c->head_stride(),
-                                                     h->stream), "kv_cache_append_rope (v)"));
-    if (mem == BARQ_MEM_HOST) BARQ_HIP(hipStreamSynchronize(h->stream));
-    c->len[layer] += n_tokens;
-    if (layer == 0) c->size += n_tokens;
+    if (!q_proj) {
+        BARQ_CHECK(launched(barq::rope_launch(layout, kp, c->k + dst_off, n_tokens, c->n_head_kv, hd, start_pos,
+                                              freq_scale, fp, c->head_stride(), h->stream), "kv_cache_append_rope (k)"));
+        BARQ_CHECK(launched(barq::transpose_heads_launch(vp, c->v + dst_off, n_tokens, c->n_head_kv, hd,
+                                                         c->head_stride(), h->stream), "kv_cache_append_rope (v)"));
+    } else if (append) {
+        BARQ_CHECK(launched(barq::rope_qkv_launch(layout, qp, kp, vp, qo, c->k + dst_off, c->v + dst_off, n_tokens,
+                                                  n_head, c->n_head_kv, hd, start_pos, freq_scale, fp, c->head_stride(),
+                                                  h->stream), who));
+    } else {
+        BARQ_CHECK(launched(barq::rope_launch(layout, qp, qo, n_tokens, n_head, hd, start_pos, freq_scale, fp,
+                                              n_tokens * hd, h->stream), who));
+    }
+    if (mem == BARQ_MEM_HOST) {
+        if (nq) BARQ_HIP(hipMemcpyAsync(q_out, qo, nq * 4, hipMemcpyDeviceToHost, h->stream));
+        BARQ_HIP(hipStreamSynchronize(h->stream));
+    }
+    if (append) {
+        c->len[layer] += n_tokens;
+        if (layer == 0) c->size += n_tokens;
+    }
     return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int barq_rocm_kv_cache_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const float* k_proj,
+                                   const float* v_proj, size_t n_tokens, size_t start_pos, float freq_scale,
+                                   const float* inv_freq, int layout, int mem) {
+    return append_rope_any(h, c, layer, nullptr, 0, nullptr, k_proj, v_proj, n_tokens, start_pos, freq_scale,
+                           inv_freq, layout, mem, "kv_cache_append_rope");
+}
+
+int barq_rocm_kv_cache_append_rope_q(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const float* q_proj,
+                                     size_t n_head, float* q_out, const float* k_proj, const float* v_proj,
+                                     size_t n_tokens, size_t start_pos, float freq_scale, const float* inv_freq,
+                                     int layout, int mem) {
+    if (!q_proj) return fail(BARQ_E_INVALID, "kv_cache_append_rope_q: null q");
+    return append_rope_any(h, c, layer, q_proj, n_head, q_out, k_proj, v_proj, n_tokens, start_pos, freq_scale,
+                           inv_freq, layout, mem, "kv_cache_append_rope_q");
 }
 
 // ---------------------------------------------------------------------------
 // attention
 
-int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer, size_t n_head,
-                        size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len, size_t start_pos, float* out,
-                        int mem) {
+}  // extern "C"
+
+namespace {
+
+// attention into f32 rows (out) or Q8_K rows (out_q8)
+int attention_any(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer, size_t n_head,
+                  size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len, size_t start_pos, float* out,
+                  void* out_q8, int mem) {
     BARQ_CHECK(check_mem(mem));
     BARQ_CHECK(check_handle(h));
     if (!c) return fail(BARQ_E_INVALID, "attention: null cache");
     if (q_len == 0 || n_head == 0) return ok();
-    if (!q || !out) return fail(BARQ_E_INVALID, "attention: null buffer");
+    if (!q || (!out && !out_q8)) return fail(BARQ_E_INVALID, "attention: null buffer");
+    if (out_q8 && (n_head * head_dim) % 256 != 0)
+        return fail(BARQ_E_DIM, "attention_q8k: n_head * head_dim = %zu is not a multiple of 256", n_head * head_dim);
     if (layer >= c->n_layers) return fail(BARQ_E_INVALID, "attention: layer %zu of %zu", layer, c->n_layers);
     if (n_head_kv != c->n_head_kv || head_dim != c->head_dim)
         return fail(BARQ_E_DIM, "attention: n_head_kv %zu / head_dim %zu, cache has %zu / %zu", n_head_kv, head_dim,
@@ -259,19 +317,25 @@ int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_
     const size_t nq = n_head * q_len * head_dim;
     const size_t wsp = barq::attention_workspace(n_head, head_dim, q_len, kv_len, n_head_kv);
     Arena a;
+    const size_t nq8 = out_q8 ? q_len * (n_head * head_dim / 256) * 292 : 0;
     const size_t op = a.add(wsp ? wsp : 4);
     const size_t oq = mem == BARQ_MEM_HOST ? a.add(nq * 4) : 0;
-    const size_t oo = mem == BARQ_MEM_HOST ? a.add(nq * 4) : 0;
+    // f32 rows: the caller's, or the workspace's when they are quantized afterwards
+    const size_t oo = (mem == BARQ_MEM_HOST || out_q8) ? a.add(nq * 4) : 0;
+    const size_t oq8 = (mem == BARQ_MEM_HOST && out_q8) ? a.add(nq8) : 0;
     BARQ_CHECK(ensure_ws(h, a.used));
     barq::AttnArgs args{};
     args.q = q;
-    args.out = out;
+    args.out = out_q8 ? at<float>(h, oo) : out;
+    args.out_q8 = static_cast<uint8_t*>(out_q8);
     if (mem == BARQ_MEM_DEVICE) {
-        if (!aligned(q, 16) || !aligned(out, 4)) return fail(BARQ_E_INVALID, "attention: q must be 16-byte aligned");
+        if (!aligned(q, 16) || (out && !aligned(out, 4)) || (out_q8 && !aligned(out_q8, 4)))
+            return fail(BARQ_E_INVALID, "attention: q must be 16-byte aligned, the output 4-byte aligned");
     } else {
         BARQ_HIP(hipMemcpyAsync(at<float>(h, oq), q, nq * 4, hipMemcpyHostToDevice, h->stream));
         args.q = at<float>(h, oq);
         args.out = at<float>(h, oo);
+        if (out_q8) args.out_q8 = at<uint8_t>(h, oq8);
     }
     args.k = c->k;
     args.v = c->v;
@@ -285,11 +349,35 @@ int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_
     args.start_pos = start_pos;
     args.part = at<float>(h, op);
     BARQ_CHECK(launched(barq::attention_launch(args, h->stream), "attention"));
+    if (out_q8 && !barq::attention_q8_direct(args))
+        BARQ_CHECK(launched(barq::quantize_q8_k_launch(args.out, q_len, n_head * head_dim, args.out_q8, h->stream),
+                            "attention_q8k (quantize)"));
     if (mem == BARQ_MEM_HOST) {
-        BARQ_HIP(hipMemcpyAsync(out, args.out, nq * 4, hipMemcpyDeviceToHost, h->stream));
+        if (out_q8) BARQ_HIP(hipMemcpyAsync(out_q8, args.out_q8, nq8, hipMemcpyDeviceToHost, h->stream));
+        else BARQ_HIP(hipMemcpyAsync(out, args.out, nq * 4, hipMemcpyDeviceToHost, h->stream));
         BARQ_HIP(hipStreamSynchronize(h->stream));
     }
     return ok();
 }
+
+}  // namespace
+
+extern "C" {
+
+int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer, size_t n_head,
+                        size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len, size_t start_pos, float* out,
+                        int mem) {
+    if (!out && q_len && n_head) return fail(BARQ_E_INVALID, "attention: null buffer");
+    return attention_any(h, q, c, layer, n_head, n_head_kv, head_dim, q_len, kv_len, start_pos, out, nullptr, mem);
+}
+
+int barq_rocm_attention_q8k(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer,
+                            size_t n_head, size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len,
+                            size_t start_pos, void* out_q8k, int mem) {
+    if (!out_q8k && q_len && n_head) return fail(BARQ_E_INVALID, "attention_q8k: null buffer");
+    return attention_any(h, q, c, layer, n_head, n_head_kv, head_dim, q_len, kv_len, start_pos, nullptr, out_q8k,
+                         mem);
+}
+
 
 }  // extern "C"

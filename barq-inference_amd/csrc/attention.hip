@@ -26,6 +26,7 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "mfma_common.hpp"
+#include "q8k_block.hpp"
 
 #include <atomic>
 #include <cstdlib>
@@ -67,6 +68,62 @@ void transpose_heads_kernel(const float* __restrict__ x, float* __restrict__ out
     const size_t ph = t / hd;
     const int h = (int)(ph % heads), p = (int)(ph / heads);
     out[(size_t)h * out_head_stride + (size_t)p * hd + d] = x[t];
+}
+
+// RoPE of q, RoPE of k into the cache and the copy of v into the cache in
+// one launch (apply_rope twice and transpose_heads, transformer.rs:222-245
+// and 514-611): slot s of a position is query head s (s < n_q), kv head
+// s - n_q of k, or of v; one thread per pair of dims.  The angles and the
+// rotation are rope_kernel's, so the results are the same bits.
+template <int LAYOUT>
+__global__ __launch_bounds__(256)
+void rope_qkv_kernel(const float* __restrict__ qx, const float* __restrict__ kx, const float* __restrict__ vx,
+                     float* __restrict__ q_out, float* __restrict__ k_out, float* __restrict__ v_out, int seq, int n_q,
+                     int n_kv, int hd, long long start_pos, float freq_scale, const float* __restrict__ inv_freq,
+                     size_t cache_head_stride) {
+    const int half = hd / 2, slots = n_q + 2 * n_kv;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)seq * slots * half) return;
+    const int i = (int)(t % half);
+    const size_t ps = t / half;
+    const int sl = (int)(ps % slots), p = (int)(ps / slots);
+    if (sl >= n_q + n_kv) {   // v: transpose_heads into the cache
+        const int h = sl - n_q - n_kv;
+        const float* src = vx + ((size_t)p * n_kv + h) * hd;
+        float* dst = v_out + (size_t)h * cache_head_stride + (size_t)p * hd;
+        dst[2 * i] = src[2 * i];
+        dst[2 * i + 1] = src[2 * i + 1];
+        return;
+    }
+    const bool is_q = sl < n_q;
+    const int h = is_q ? sl : sl - n_q, heads = is_q ? n_q : n_kv;
+    const float angle = ((float)(start_pos + p) * freq_scale) * inv_freq[i];
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    const float* src = (is_q ? qx : kx) + ((size_t)p * heads + h) * hd;
+    float* dst = is_q ? q_out + ((size_t)h * seq + p) * hd : k_out + (size_t)h * cache_head_stride + (size_t)p * hd;
+    const int i0 = LAYOUT == ROPE_INTERLEAVED ? 2 * i : i;
+    const int i1 = LAYOUT == ROPE_INTERLEAVED ? 2 * i + 1 : i + half;
+    const float x0 = src[i0], x1 = src[i1];
+    dst[i0] = x0 * cs - x1 * sn;
+    dst[i1] = x0 * sn + x1 * cs;
+}
+
+hipError_t rope_qkv_launch(int layout, const float* qx, const float* kx, const float* vx, float* q_out, float* k_out,
+                           float* v_out, size_t seq, size_t n_q, size_t n_kv, size_t hd, size_t start_pos,
+                           float freq_scale, const float* inv_freq, size_t cache_head_stride, hipStream_t s) {
+    const size_t n = seq * (n_q + 2 * n_kv) * (hd / 2);
+    if (n == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (layout == ROPE_INTERLEAVED)
+        hipLaunchKernelGGL(rope_qkv_kernel<ROPE_INTERLEAVED>, dim3(grid), dim3(256), 0, s, qx, kx, vx, q_out, k_out,
+                           v_out, (int)seq, (int)n_q, (int)n_kv, (int)hd, (long long)start_pos, freq_scale, inv_freq,
+                           cache_head_stride);
+    else
+        hipLaunchKernelGGL(rope_qkv_kernel<ROPE_SPLIT_HALF>, dim3(grid), dim3(256), 0, s, qx, kx, vx, q_out, k_out,
+                           v_out, (int)seq, (int)n_q, (int)n_kv, (int)hd, (long long)start_pos, freq_scale, inv_freq,
+                           cache_head_stride);
+    return hipGetLastError();
 }
 
 hipError_t rope_launch(int layout, const float* x, float* out, size_t seq, size_t heads, size_t hd, size_t start_pos,
@@ -285,22 +342,22 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     }
 }
 
-// out[i, h, :] from the n_split partial states of (i, h): one workgroup per
-// (h, i).  The split maxima and weights are spread over the 1024 threads;
-// the output sums over 1024 / HD thread subsets of the splits, then added in
-// LDS.
 constexpr int ATT_MAX_SPLIT = 1024;
 
+// One output head: out value of dim t (t < HD) from the n_split partial
+// states at pp; every thread of the 1024 calls it (it synchronises).
 template <int HD>
-__global__ __launch_bounds__(1024)
-void attn_combine_kernel(const float* __restrict__ part, int n_split, int n_head, float* __restrict__ out) {
+struct CombineLds {
+    float w[ATT_MAX_SPLIT];
+    float red[1024 / HD][HD];
+    float wred[2][1024 / 64];
+};
+
+template <int HD>
+__device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp, int n_split, CombineLds<HD>& sm) {
     constexpr int NT = 1024, NWV = NT / 64, SUB = NT / HD, PRE = 8;
-    __shared__ float w[ATT_MAX_SPLIT];
-    __shared__ float red[SUB][HD];
-    __shared__ float wred[2][NWV];
-    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int sub = t / HD, d = t % HD;
-    const float* pp = part + ((size_t)i * n_head + h) * n_split * (HD + 2);
     // every load of the first PRE rounds is issued before any reduction
     float ov[PRE];
     #pragma unroll
@@ -316,42 +373,84 @@ void attn_combine_kernel(const float* __restrict__ part, int n_split, int n_head
     for (int s = t; s < n_split; s += NT) M = fmaxf(M, pp[(size_t)s * (HD + 2)]);
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) wred[0][wave] = M;
+    if (lane == 0) sm.wred[0][wave] = M;
     __syncthreads();
-    M = wred[0][0];
+    M = sm.wred[0][0];
     #pragma unroll
-    for (int u = 1; u < NWV; u++) M = fmaxf(M, wred[0][u]);
+    for (int u = 1; u < NWV; u++) M = fmaxf(M, sm.wred[0][u]);
     float L = 0.0f;
     for (int s = t; s < n_split; s += NT) {
         const float ms = s == t ? Ms : pp[(size_t)s * (HD + 2)];
         const float ls = s == t ? Ls : pp[(size_t)s * (HD + 2) + 1];
         const float ws = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
-        w[s] = ws;
+        sm.w[s] = ws;
         L = __builtin_fmaf(ls, ws, L);
     }
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
-    if (lane == 0) wred[1][wave] = L;
+    if (lane == 0) sm.wred[1][wave] = L;
     __syncthreads();
-    L = wred[1][0];
+    L = sm.wred[1][0];
     #pragma unroll
-    for (int u = 1; u < NWV; u++) L += wred[1][u];
+    for (int u = 1; u < NWV; u++) L += sm.wred[1][u];
     float O = 0.0f;
     #pragma unroll
     for (int u = 0; u < PRE; u++) {
         const int s = sub + SUB * u;
-        if (s < n_split) O = __builtin_fmaf(ov[u], w[s], O);
+        if (s < n_split) O = __builtin_fmaf(ov[u], sm.w[s], O);
     }
-    for (int s = sub + SUB * PRE; s < n_split; s += SUB) O = __builtin_fmaf(pp[(size_t)s * (HD + 2) + 2 + d], w[s], O);
-    red[sub][d] = O;
+    for (int s = sub + SUB * PRE; s < n_split; s += SUB) O = __builtin_fmaf(pp[(size_t)s * (HD + 2) + 2 + d], sm.w[s], O);
+    sm.red[sub][d] = O;
     __syncthreads();
+    float acc = 0.0f;
     if (t < HD) {
-        float acc = red[0][t];
+        acc = sm.red[0][t];
         #pragma unroll
-        for (int u = 1; u < SUB; u++) acc += red[u][t];
-        out[((size_t)i * n_head + h) * HD + t] = acc / L;
+        for (int u = 1; u < SUB; u++) acc += sm.red[u][t];
+        acc = acc / L;
+    }
+    return acc;
+}
+
+// out[i, h, :] from the n_split partial states of (i, h): one workgroup per
+// (h, i).  The split maxima and weights are spread over the 1024 threads;
+// the output sums over 1024 / HD thread subsets of the splits, then added in
+// LDS.
+template <int HD>
+__global__ __launch_bounds__(1024)
+void attn_combine_kernel(const float* __restrict__ part, int n_split, int n_head, float* __restrict__ out) {
+    __shared__ CombineLds<HD> sm;
+    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
+    const float v = attn_combine_head<HD>(part + ((size_t)i * n_head + h) * n_split * (HD + 2), n_split, sm);
+    if (t < HD) out[((size_t)i * n_head + h) * HD + t] = v;
+}
+
+// The same merge with the output row written as Q8_K blocks (the o
+// projection's activation): workgroup (b, i) merges the 256 / HD heads of
+// block b of row i one after another, then one wave quantizes the block
+// (q8_k_block: the bytes quantize_q8_k_kernel writes for the same values).
+template <int HD>
+__global__ __launch_bounds__(1024)
+void attn_combine_q8k_kernel(const float* __restrict__ part, int n_split, int n_head, uint8_t* __restrict__ out) {
+    constexpr int NH = 256 / HD;
+    __shared__ CombineLds<HD> sm;
+    __shared__ __align__(16) float vals[256];
+    const int b = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
+    #pragma unroll 1
+    for (int hh = 0; hh < NH; hh++) {
+        const int h = b * NH + hh;
+        const float v = attn_combine_head<HD>(part + ((size_t)i * n_head + h) * n_split * (HD + 2), n_split, sm);
+        if (t < HD) vals[hh * HD + t] = v;
+        __syncthreads();   // the merge's LDS is reused by the next head
+    }
+    if (t < 64) {
+        const float4 v4 = reinterpret_cast<const float4*>(vals)[t];
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        q8_k_block(vv, t, out + ((size_t)i * (n_head * HD / 256) + b) * Q8_K_BYTES);
     }
 }
+
+bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 
 // ---- prompt chunks on MFMA ----------------------------------------------------
 // For q_len >= 32 (BARQ_ATTN_MFMA_MIN_Q) and head_dim 128 a workgroup covers
@@ -526,8 +625,6 @@ static int cu_count_attn() {
     return v;
 }
 
-bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
-
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv) {
     if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q()) return 0;   // the MFMA path keeps no partials
     int ns = 0, chunk = 0;
@@ -557,6 +654,17 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
     *chunk = (int)ch;
 }
 
+// Whether attention_launch writes a.out_q8 itself (the split path's merge
+// emits Q8_K rows); otherwise it writes f32 rows to a.out and the caller
+// quantizes them.
+bool attention_q8_direct(const AttnArgs& a) {
+    if (a.head_dim == 128 && a.q_len >= (size_t)attn_mfma_min_q()) return false;
+    if ((a.n_head * a.head_dim) % 256 != 0) return false;
+    int ns = 0, chunk = 0;
+    attention_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len, &ns, &chunk);
+    return ns > 1;
+}
+
 template <int HD, int G>
 static hipError_t attn_launch_t(const AttnArgs& a, int ns, int chunk, int groups, hipStream_t s) {
     const float scale = (1.0f / sqrtf((float)HD)) * LOG2E;
@@ -565,8 +673,12 @@ static hipError_t attn_launch_t(const AttnArgs& a, int ns, int chunk, int groups
                        (long long)a.start_pos, chunk, scale, a.part, a.out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ns == 1) return e;
-    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(1024), 0, s, a.part,
-                       ns, (int)a.n_head, a.out);
+    if (a.out_q8 && attention_q8_direct(a))
+        hipLaunchKernelGGL(attn_combine_q8k_kernel<HD>, dim3((unsigned)(a.n_head * HD / 256), (unsigned)a.q_len),
+                           dim3(1024), 0, s, a.part, ns, (int)a.n_head, a.out_q8);
+    else
+        hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(1024), 0, s,
+                           a.part, ns, (int)a.n_head, a.out);
     return hipGetLastError();
 }
 

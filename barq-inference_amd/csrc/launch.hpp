@@ -170,7 +170,12 @@ struct AttnArgs {
     size_t n_head, n_head_kv, head_dim, q_len, kv_len, start_pos;
     float* part;              // split partials (attention_workspace bytes)
     float* out;               // [q_len, n_head, head_dim]
+    uint8_t* out_q8;          // optional: the output rows as Q8_K blocks (see attention_q8_direct)
 };
+bool attention_q8_direct(const AttnArgs& a);
+hipError_t rope_qkv_launch(int layout, const float* qx, const float* kx, const float* vx, float* q_out, float* k_out,
+                           float* v_out, size_t seq, size_t n_q, size_t n_kv, size_t hd, size_t start_pos,
+                           float freq_scale, const float* inv_freq, size_t cache_head_stride, hipStream_t s);
 bool attention_supported(size_t head_dim);
 void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len, int* n_split, int* chunk);
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv);

@@ -529,7 +529,7 @@ def bench_layer(args):
     f = torch.from_numpy(np.array([np.float32(500000.0) ** np.float32(-2.0 * i / hd) for i in range(hd // 2)],
                                   dtype=np.float32)).cuda()
     steps = args.steps
-    kv = A.KVCache(be, kv_len + steps + 8, copies, n_kv, hd)
+    kv = A.KVCache(be, kv_len + 2 * steps + 4 * copies + 8, copies, n_kv, hd)   # two timed captures
     rng = np.random.default_rng(5)
     for c in range(copies):   # kv_len - 1 cached positions per layer copy
         kk = rng.standard_normal((n_kv, kv_len - 1, hd)).astype(np.float32)
@@ -548,7 +548,12 @@ def bench_layer(args):
     torch.cuda.synchronize()
     pos = [kv_len - 1] * copies
 
-    def step(i):
+    qr = torch.empty((n_head, 1, hd), dtype=torch.float32, device="cuda")
+    aq = torch.empty((1, (n_embd // 256) * 292), dtype=torch.uint8, device="cuda")
+
+    def step_separate(i):
+        # every reference step its own launch: RoPE q, RoPE k + v into the
+        # cache, attention in f32, the o projection quantizing its input
         c = i % copies
         L = layers[c]
         be.add_rms_norm_quantize(B.Q8_K, x, prev, norm_w, 1e-5, sum_out=res_in, out=xq, sync=False)
@@ -564,12 +569,33 @@ def bench_layer(args):
         be.ffn(B.Q4_K, L["gate"], B.Q4_K, L["up"], B.Q6_K, L["down"], n_embd, n_ff, B.Q8_K, xq2, 1, sync=False,
                out=ff)
 
+    def step(i):
+        # fused: RoPE of q and k with the cache append in one launch, the
+        # attention merge writing the o projection's Q8_K rows
+        c = i % copies
+        L = layers[c]
+        be.add_rms_norm_quantize(B.Q8_K, x, prev, norm_w, 1e-5, sum_out=res_in, out=xq, sync=False)
+        be.matmul_raw(B.Q4_K, L["q"], n_head * hd, n_embd, B.Q8_K, xq, 1, q, B.MEM_DEVICE)
+        be.matmul_raw(B.Q4_K, L["k"], n_kv * hd, n_embd, B.Q8_K, xq, 1, k, B.MEM_DEVICE)
+        be.matmul_raw(B.Q6_K, L["v"], n_kv * hd, n_embd, B.Q8_K, xq, 1, v, B.MEM_DEVICE)
+        kv.append_rope_q(c, q, n_head, k, v, 1, pos[c], 1.0, f, A.ROPE_INTERLEAVED, q_out=qr)
+        A.compute_attention_q8k(be, qr, kv, c, n_head, n_kv, hd, 1, pos[c] + 1, pos[c], sync=False, out=aq)
+        pos[c] += 1
+        be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.Q8_K, aq, 1, o, B.MEM_DEVICE)
+        be.add_rms_norm_quantize(B.Q8_K, res_in, o, norm_w, 1e-5, sum_out=res, out=xq2, sync=False)
+        be.ffn(B.Q4_K, L["gate"], B.Q4_K, L["up"], B.Q6_K, L["down"], n_embd, n_ff, B.Q8_K, xq2, 1, sync=False,
+               out=ff)
+
     # warm-up outside the graph (workspace, kernel attributes): one step per layer copy
     for i in range(copies):
         step(i)
     torch.cuda.synchronize()
     log(f"timing {steps} decode-layer steps over {copies} layer copies "
         f"({copies * (wbytes + kv_bytes) / 2**20:.0f} MiB of weights and KV)")
+    ms_sep, _ = time_launches(step_separate, steps, args.eager)
+    for i in range(copies):
+        step(i)
+    torch.cuda.synchronize()
     ms, method = time_launches(step, steps, args.eager)
     alg = wbytes + kv_bytes + 4 * n_embd * 4 * 4
     gbs = alg / (ms * 1e-3) / 1e9
@@ -580,10 +606,10 @@ def bench_layer(args):
         "dtype": "int8", "data": "synthetic",
         "config": {"workload": f"forward_layer decode, 1 token, kv_len {kv_len}, Q4_K_M weight mix",
                    "layer_copies": copies, "timing": method},
-        "us_per_step": round(ms * 1e3, 3),
+        "us_per_step": round(ms * 1e3, 3), "us_per_step_separate_launches": round(ms_sep * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
-                     "scope": "the whole layer step (14 launches)"},
+                     "scope": "the whole layer step (12 launches; 15 with every reference step its own launch)"},
     }
     kv.close()
     be.close()

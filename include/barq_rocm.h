@@ -385,6 +385,18 @@ int barq_rocm_kv_cache_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, s
                                    const float* k_proj, const float* v_proj, size_t n_tokens,
                                    size_t start_pos, float freq_scale, const float* inv_freq, int layout,
                                    int mem);
+/* append_rope_q = the three steps of self_attention between the projections
+ * and compute_attention (transformer.rs:222-245: apply_rope on q, apply_rope
+ * on k and transpose_heads on v, then KVCache::append) in one launch:
+ * q_proj [n_tokens, n_head * head_dim] is rotated into q_out [n_head,
+ * n_tokens, head_dim]; k_proj and v_proj go into the cache as for
+ * append_rope.  The same bits as barq_rocm_rope on q followed by
+ * barq_rocm_kv_cache_append_rope.  An out-of-range layer appends nothing and
+ * still rotates q. */
+int barq_rocm_kv_cache_append_rope_q(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer,
+                                     const float* q_proj, size_t n_head, float* q_out, const float* k_proj,
+                                     const float* v_proj, size_t n_tokens, size_t start_pos, float freq_scale,
+                                     const float* inv_freq, int layout, int mem);
 size_t barq_rocm_kv_cache_size(const barq_rocm_kv_cache* c);
 size_t barq_rocm_kv_cache_layer_len(const barq_rocm_kv_cache* c, size_t layer);
 int barq_rocm_kv_cache_head(const barq_rocm_kv_cache* c, size_t layer, size_t head, const float** k,
@@ -403,6 +415,16 @@ int barq_rocm_kv_cache_destroy(barq_rocm_kv_cache* c);
 int barq_rocm_attention(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer,
                         size_t n_head, size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len,
                         size_t start_pos, float* out, int mem);
+/* attention_q8k = compute_attention followed by the o projection's activation
+ * quantizer (transformer.rs:255-262: the attention rows are the input of
+ * proj(wo)): out_q8k receives q_len rows of n_head * head_dim / 256 Q8_K
+ * blocks (n_head * head_dim must be a multiple of 256), the bytes
+ * barq_rocm_quantize_act(BARQ_Q8_K) writes for barq_rocm_attention's rows.
+ * When the positions are split over workgroups the merge kernel writes the
+ * blocks itself (one launch fewer). */
+int barq_rocm_attention_q8k(barq_rocm_handle* h, const float* q, const barq_rocm_kv_cache* c, size_t layer,
+                            size_t n_head, size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len,
+                            size_t start_pos, void* out_q8k, int mem);
 
 /* ---- matmul without allocation -------------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device

@@ -187,3 +187,66 @@ def test_attention_argument_errors(be):
         A.compute_attention(be, rng_f32(4, 1, 1, 80), c80, 0, 1, 1, 80, 1, 4, 3, mem=B.MEM_HOST)
     assert e.value.code == B._lib.E_UNSUPPORTED
     c80.close()
+
+
+@pytest.mark.parametrize("layout", [A.ROPE_INTERLEAVED, A.ROPE_SPLIT_HALF])
+@pytest.mark.parametrize("n_head,n_kv,hd,n", [(32, 8, 128, 1), (8, 2, 128, 6), (6, 4, 64, 3), (4, 2, 256, 2)])
+def test_append_rope_q_equals_separate_steps(be, layout, n_head, n_kv, hd, n):
+    """The fused q/k RoPE + cache append is bit-identical to barq_rocm_rope on q
+    then append_rope on k and v (device and host buffers, an out-of-range
+    layer that still rotates q)."""
+    f = inv_freq(hd)
+    qp, kp, vp = rng_f32(21, n, n_head * hd), rng_f32(22, n, n_kv * hd), rng_f32(23, n, n_kv * hd)
+    c1 = A.KVCache(be, 40, 2, n_kv, hd)
+    c2 = A.KVCache(be, 40, 2, n_kv, hd)
+    for layer in range(2):
+        q1 = c1.append_rope_q(layer, dev(qp), n_head, dev(kp), dev(vp), n, 5, 1.0, dev(f), layout)
+        be.sync()
+        q2 = A.apply_rope(be, dev(qp), n, n_head, hd, 5, 1.0, dev(f), layout)
+        c2.append_rope(layer, dev(kp), dev(vp), n, 5, 1.0, dev(f), layout)
+        assert np.array_equal(q1.cpu().numpy(), q2.cpu().numpy())
+    qh = c1.append_rope_q(1, qp, n_head, kp, vp, n, 5 + n, 1.0, f, layout, mem=B.MEM_HOST)
+    c2.append_rope(1, dev(kp), dev(vp), n, 5 + n, 1.0, dev(f), layout)
+    q2 = A.apply_rope(be, dev(qp), n, n_head, hd, 5 + n, 1.0, dev(f), layout)
+    assert np.array_equal(qh, q2.cpu().numpy())
+    q3 = c1.append_rope_q(7, dev(qp), n_head, dev(kp), dev(vp), n, 9, 1.0, dev(f), layout)   # layer out of range
+    be.sync()
+    assert np.array_equal(q3.cpu().numpy(), A.apply_rope(be, dev(qp), n, n_head, hd, 9, 1.0, dev(f), layout).cpu().numpy())
+    assert c1.size() == c2.size() == n and c1.layer_len(1) == c2.layer_len(1) == 2 * n
+    for layer in range(2):
+        for h in range(n_kv):
+            a, b = c1.get_head(layer, h), c2.get_head(layer, h)
+            assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    c1.close()
+    c2.close()
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,q_len,kv_len,start,pos", [
+    (32, 8, 128, 1, 4096, 4095, 4096),    # decode: the merge writes Q8_K blocks
+    (32, 8, 128, 1, 40, 39, 40),          # one split: attention, then the quantizer
+    (32, 8, 128, 7, 300, 293, 300),       # a chunk of 7 rows
+    (32, 8, 128, 40, 100, 60, 100),       # a prompt chunk on the MFMA kernel
+    (8, 2, 64, 1, 1000, 999, 1000),       # head_dim 64: four heads per block
+    (4, 2, 256, 1, 517, 516, 517),        # head_dim 256: one head per block
+])
+def test_attention_q8k_equals_quantized_attention(be, n_head, n_kv, hd, q_len, kv_len, start, pos):
+    """attention_q8k writes the bytes quantize_act(Q8_K) writes for the f32
+    attention rows, whichever path (merge kernel or quantizer after) runs."""
+    c, k, v = fill_cache(be, n_kv, hd, pos, n_head * 3 + kv_len)
+    q = rng_f32(kv_len + 5, n_head, q_len, hd)
+    print(f"attention_q8k case n_head={n_head} hd={hd} q_len={q_len} kv_len={kv_len}", flush=True)
+    y = A.compute_attention(be, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start)
+    ref = be.quantize_act(B.Q8_K, y.reshape(q_len, n_head * hd)).cpu().numpy().reshape(-1)
+    got = A.compute_attention_q8k(be, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start).cpu().numpy().reshape(-1)
+    assert np.array_equal(got, ref)
+    host = A.compute_attention_q8k(be, q, c, 1, n_head, n_kv, hd, q_len, kv_len, start, mem=B.MEM_HOST)
+    assert np.array_equal(host.reshape(-1), ref)
+    c.close()
+
+
+def test_attention_q8k_argument_errors(be):
+    c, k, v = fill_cache(be, 2, 64, 20, 3)
+    q = rng_f32(1, 3, 1, 64)
+    with pytest.raises(B.BarqError):   # 3 * 64 is not a multiple of 256
+        A.compute_attention_q8k(be, dev(q), c, 1, 3, 2, 64, 1, 20, 19)
+    c.close()
