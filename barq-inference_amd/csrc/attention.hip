@@ -613,6 +613,12 @@ void attn_mfma_kernel(const float* __restrict__ q, const float* __restrict__ kc,
 
 static int attn_mfma_min_q() { return tuning_env(TUNE_ATTN_MFMA_MIN_Q, 32); }
 
+// The prompt path: head_dim 128, q_len at the threshold, and a kv head's
+// rows addressable by the 32-bit buffer offsets of its K/V loads.
+static bool attn_mfma_path(const AttnArgs& a) {
+    return a.head_dim == 128 && a.q_len >= (size_t)attn_mfma_min_q() && a.kv_len < ((size_t)1 << 23);
+}
+
 static int cu_count_attn() {
     static std::atomic<int> n[64] = {};   // per device; racing callers store the same value
     int dev = 0;
@@ -626,7 +632,8 @@ static int cu_count_attn() {
 }
 
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv) {
-    if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q()) return 0;   // the MFMA path keeps no partials
+    if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q() && kv_len < ((size_t)1 << 23))
+        return 0;   // the MFMA path keeps no partials
     int ns = 0, chunk = 0;
     attention_plan(n_head, n_head_kv, q_len, kv_len, &ns, &chunk);
     return ns > 1 ? (size_t)ns * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
@@ -658,7 +665,7 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
 // emits Q8_K rows); otherwise it writes f32 rows to a.out and the caller
 // quantizes them.
 bool attention_q8_direct(const AttnArgs& a) {
-    if (a.head_dim == 128 && a.q_len >= (size_t)attn_mfma_min_q()) return false;
+    if (attn_mfma_path(a)) return false;
     if ((a.n_head * a.head_dim) % 256 != 0) return false;
     int ns = 0, chunk = 0;
     attention_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len, &ns, &chunk);
@@ -697,7 +704,7 @@ static hipError_t attn_launch_hd(const AttnArgs& a, hipStream_t s) {
 
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
     if (a.q_len == 0 || a.n_head == 0) return hipSuccess;
-    if (a.head_dim == 128 && a.q_len >= (size_t)attn_mfma_min_q()) {
+    if (attn_mfma_path(a)) {
         const float scale = (1.0f / sqrtf(128.0f)) * LOG2E;
         // W query heads per workgroup share one kv head (W divides the group size)
         const size_t grp = (a.n_head_kv && a.n_head % a.n_head_kv == 0) ? a.n_head / a.n_head_kv : 1;

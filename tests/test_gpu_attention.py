@@ -250,3 +250,37 @@ def test_attention_q8k_argument_errors(be):
     with pytest.raises(B.BarqError):   # 3 * 64 is not a multiple of 256
         A.compute_attention_q8k(be, dev(q), c, 1, 3, 2, 64, 1, 20, 19)
     c.close()
+
+
+@pytest.mark.parametrize("n_head,n_kv,q_len,kv_len,start,pos", [
+    (32, 8, 1, 300, 299, 300),    # a decode row on the MFMA kernel
+    (32, 8, 7, 40, 33, 40),       # a short chunk: one block, 25 rows unused
+    (8, 2, 16, 16, 0, 16),
+    (12, 6, 3, 10, 2, 10),        # masked tail
+])
+def test_attention_mfma_kernel_small_chunks(be, orc, n_head, n_kv, q_len, kv_len, start, pos):
+    """The MFMA prompt kernel with its threshold lowered (BARQ_ATTN_MFMA_MIN_Q,
+    read at handle creation) on chunks shorter than a query block."""
+    import os
+    hd = 128
+    c, k, v = fill_cache(be, n_kv, hd, pos, n_head * 5 + kv_len)
+    q = rng_f32(kv_len + 9, n_head, q_len, hd)
+    old = os.environ.get("BARQ_ATTN_MFMA_MIN_Q")
+    os.environ["BARQ_ATTN_MFMA_MIN_Q"] = "1"
+    try:
+        b2 = B.Backend(0)
+    finally:
+        if old is None:
+            os.environ.pop("BARQ_ATTN_MFMA_MIN_Q", None)
+        else:
+            os.environ["BARQ_ATTN_MFMA_MIN_Q"] = old
+    try:
+        got = A.compute_attention(b2, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start).cpu().numpy()
+        got_q8 = A.compute_attention_q8k(b2, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start).cpu().numpy()
+        ref_q8 = b2.quantize_act(B.Q8_K, dev(got.reshape(q_len, n_head * hd))).cpu().numpy()
+    finally:
+        b2.close()
+    ref = orc.attention(q, k, v, n_head, q_len, kv_len, start)
+    assert np.max(np.abs(got - ref)) <= 2e-5 * np.max(np.abs(v))
+    assert np.array_equal(got_q8.reshape(-1), ref_q8.reshape(-1))
+    c.close()
