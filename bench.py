@@ -61,7 +61,9 @@ def parse():
     p.add_argument("--q-len", type=int, default=1, help="--attn: new tokens per call (1 = decode; > 1 = a prompt chunk)")
     p.add_argument("--ffn", action="store_true",
                    help="time the dense FFN (feed_forward: gate/up Q4_K, SwiGLU, down Q6_K) at Llama-3-8B shapes")
-    p.add_argument("--m", type=int, default=1, help="--ffn: tokens per call")
+    p.add_argument("--m", type=int, default=1, help="--ffn: tokens per call; --prefill: prompt tokens (default 512)")
+    p.add_argument("--prefill", action="store_true",
+                   help="one Llama-3-8B layer over a --m token prompt (GEMMs, MFMA attention): tokens/s")
     p.add_argument("--layer", action="store_true",
                    help="time one Llama-3-8B decode layer (norm, q/k/v, RoPE + KV append, attention, o, norm, FFN)")
     p.add_argument("--probe-copy", action="store_true",
@@ -494,6 +496,94 @@ def bench_ffn(args):
     return 0
 
 
+def bench_prefill(args):
+    """One Llama-3-8B layer over an M-token prompt from position 0
+    (forward_layer, transformer.rs:123-144, with seq_len = M) on the integer
+    path: residual add + attn_norm -> Q8_K rows, q / k / v GEMMs (int8 MFMA),
+    RoPE of q and k with the cache append, causal attention (f32 MFMA) with
+    its rows quantized for the o GEMM, residual add + ffn_norm -> Q8_K, the
+    dense FFN (gate/up GEMMs, SwiGLU -> Q8_K, down GEMM).  Steps rotate over
+    layer copies of >= 320 MB.  Throughput: prompt tokens per second through
+    one layer; the op count is 2 M N K over the seven projections plus the
+    attention's 4 hd per visible (query, position) pair and head."""
+    import numpy as np
+    import torch
+
+    import barq_rocm as B
+    from barq_rocm import attention as A
+    from barq_rocm import synth
+
+    n_embd, n_head, n_kv, hd, n_ff = 4096, 32, 8, 128, 14336
+    m = args.m if args.m > 1 else 512
+    mats = [("q", B.Q4_K, n_head * hd, n_embd), ("k", B.Q4_K, n_kv * hd, n_embd), ("v", B.Q6_K, n_kv * hd, n_embd),
+            ("o", B.Q4_K, n_embd, n_head * hd), ("gate", B.Q4_K, n_ff, n_embd), ("up", B.Q4_K, n_ff, n_embd),
+            ("down", B.Q6_K, n_embd, n_ff)]
+    host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
+    wbytes = sum(a.nbytes for a in host.values())
+    copies = args.copies or max(2, -(-320 * 2 ** 20 // wbytes))
+    be = B.Backend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    layers = [{nm: torch.from_numpy(a).cuda() for nm, a in host.items()} for _ in range(copies)]
+    norm_w = torch.from_numpy((0.01 * (1.0 + 0.1 * synth.gen_f32(n_embd, 820))).astype(np.float32)).cuda()
+    f = torch.from_numpy(np.array([np.float32(500000.0) ** np.float32(-2.0 * i / hd) for i in range(hd // 2)],
+                                  dtype=np.float32)).cuda()
+    kv = A.KVCache(be, m, copies, n_kv, hd)
+    x = torch.from_numpy(synth.gen_f32(m * n_embd, 821).reshape(m, n_embd)).cuda()
+    prev = torch.zeros((m, n_embd), dtype=torch.float32, device="cuda")
+    res_in, res = torch.empty_like(x), torch.empty_like(x)
+    nbq = n_embd // 256 * 292
+    xq = torch.empty((m, nbq), dtype=torch.uint8, device="cuda")
+    xq2, aq = torch.empty_like(xq), torch.empty_like(xq)
+    q = torch.empty((m, n_head * hd), dtype=torch.float32, device="cuda")
+    k = torch.empty((m, n_kv * hd), dtype=torch.float32, device="cuda")
+    v = torch.empty((m, n_kv * hd), dtype=torch.float32, device="cuda")
+    qr = torch.empty((n_head, m, hd), dtype=torch.float32, device="cuda")
+    o = torch.empty((m, n_embd), dtype=torch.float32, device="cuda")
+    ff = torch.empty((m, n_embd), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i):
+        c = i % copies
+        L = layers[c]
+        kv.clear()   # host lengths only: every step writes positions 0 .. m-1 of its layer copy
+        be.add_rms_norm_quantize(B.Q8_K, x, prev, norm_w, 1e-5, sum_out=res_in, out=xq, sync=False)
+        be.matmul_raw(B.Q4_K, L["q"], n_head * hd, n_embd, B.Q8_K, xq, m, q, B.MEM_DEVICE)
+        be.matmul_raw(B.Q4_K, L["k"], n_kv * hd, n_embd, B.Q8_K, xq, m, k, B.MEM_DEVICE)
+        be.matmul_raw(B.Q6_K, L["v"], n_kv * hd, n_embd, B.Q8_K, xq, m, v, B.MEM_DEVICE)
+        kv.append_rope_q(c, q, n_head, k, v, m, 0, 1.0, f, A.ROPE_INTERLEAVED, q_out=qr)
+        A.compute_attention_q8k(be, qr, kv, c, n_head, n_kv, hd, m, m, 0, sync=False, out=aq)
+        be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.Q8_K, aq, m, o, B.MEM_DEVICE)
+        be.add_rms_norm_quantize(B.Q8_K, res_in, o, norm_w, 1e-5, sum_out=res, out=xq2, sync=False)
+        be.ffn(B.Q4_K, L["gate"], B.Q4_K, L["up"], B.Q6_K, L["down"], n_embd, n_ff, B.Q8_K, xq2, m, sync=False,
+               out=ff)
+
+    for i in range(copies):
+        step(i)
+    torch.cuda.synchronize()
+    steps = args.steps
+    log(f"timing {steps} prefill-layer steps of {m} tokens over {copies} layer copies")
+    ms, method = time_launches(step, steps, args.eager)
+    ops = 2 * m * sum(n * kk for _, _, n, kk in mats) + 2 * 2 * n_head * hd * (m * (m + 1) // 2)
+    tops = ops / (ms * 1e-3) / 1e12
+    result = {
+        "metric": f"Llama-3-8B prefill layer ({m}-token prompt, integer path) tokens/s through one layer, 1 GPU",
+        "value": round(m / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": copies,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 (GEMMs) + f32 (attention)", "data": "synthetic",
+        "config": {"workload": f"forward_layer prefill, {m} tokens from position 0, Q4_K_M weight mix",
+                   "layer_copies": copies, "timing": method},
+        "us_per_step": round(ms * 1e3, 3), "tera_ops_per_s": round(tops, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
+                     "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None, "alg_ops_per_launch": ops,
+                     "scope": "the whole layer step (13 launches); the attention's f32 ops are counted at the int8 peak"},
+    }
+    be.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def bench_layer(args):
     """One decode step of a Llama-3-8B layer (forward_layer,
     transformer.rs:123-144) on the integer path, every launch captured in one
@@ -736,6 +826,8 @@ def main():
         return bench_ffn(args)
     if args.layer:
         return bench_layer(args)
+    if args.prefill:
+        return bench_prefill(args)
     if args.config == 5:
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]
