@@ -1029,6 +1029,17 @@ static hipError_t kq_launch_t(const KQArgs& a, hipStream_t s) {
 // rows: M (ungrouped) or the expected rows per expert (grouped).  Stage
 // counts are the most that fit the 160 KiB of LDS (deeper pipelines keep
 // more HBM requests in flight per CU).
+// Q6_K prompts: 64-row tiles of four waves (each weight slice decoded once for
+// two MFMA row tiles) where the tiles fill the CUs without K slices or K is
+// long; measured on MI355X, M = 128 / 256 / 512, us per call (default against
+// these tiles): 4096 x 14336 44.9 / 78.9 / 155.4 against 38.7 / 67.3 / 119.8;
+// 4096 x 4096 19.3 / 25.9 / 49.5 against 19.5 / 27.9 / 38.3; M = 64: 27.7 and
+// 14.5 against 37.1 and 16.4.
+static bool kq6_wide_tiles(size_t m, size_t n_rows, size_t nsb) {
+    const size_t tiles = (m + 63) / 64 * ((n_rows + KQ_BN - 1) / KQ_BN);
+    return tiles >= 256 || (m >= 128 && nsb >= 32);
+}
+
 template <class F, bool GROUPED>
 static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // measured on MI355X: 64x128 tiles above 32 rows, 32-row tiles with four
@@ -1037,7 +1048,9 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // fragment is decoded once for two MFMA row tiles; 26.5-27.1 against
     // 27.6-29.0 us at C4 for eight waves of 32 x 32, bm 65)
     const int g_kq_ns = tuning_env(TUNE_GEMM_NS), g_kq_bm = tuning_env(TUNE_GEMM_BM);
-    const int bm = g_kq_bm ? g_kq_bm : (rows > 32 ? 64 : 32);
+    const int bm = g_kq_bm ? g_kq_bm
+                 : (!GROUPED && F::TYPE == TYPE_Q6_K && kq6_wide_tiles(rows, (size_t)a.N, (size_t)a.nsb)) ? 66
+                 : (rows > 32 ? 64 : 32);
     if (bm == 16) {
         if (g_kq_ns == 2) return kq_launch_t<F, 16, 2, 4, GROUPED>(a, s);
         if (g_kq_ns == 4) return kq_launch_t<F, 16, 4, 4, GROUPED>(a, s);
@@ -1046,6 +1059,11 @@ static hipError_t kq_dispatch(const KQArgs& a, size_t rows, hipStream_t s) {
     // 32-row tiles: two stages per workgroup and two workgroups per CU for
     // expert groups (measured best for C5), the deepest pipeline otherwise
     const int ns = g_kq_ns ? g_kq_ns : (GROUPED ? 2 : 0);
+    if constexpr (!GROUPED && F::TYPE == TYPE_Q6_K) {
+        // 64 x 128 tiles with four waves of 64 x 32 (each weight slice decoded
+        // once for two MFMA row tiles), one K-group, three stages
+        if (bm == 66) return kq_launch_t<F, 64, 3, 4, GROUPED>(a, s);
+    }
     if constexpr (!GROUPED) {
         // two K-groups of waves share a tile's pipeline (twice the waves per
         // SIMD for the same LDS) when the super-block count is even
@@ -1126,16 +1144,17 @@ static KQArgs kq_args(int w_type, size_t n_rows, size_t k, const void* xq, float
 // keeps an even number of super-blocks (two K-groups; Q6_K windows keep
 // their parity).  BARQ_GEMM_KS overrides (a power of two up to 16).
 // The tile height kq_dispatch picks (for an even super-block count per slice).
-static size_t kq_tile_rows(int w_type, size_t m) {
+static size_t kq_tile_rows(int w_type, size_t m, size_t n_rows, size_t nsb) {
     const int bm_env = tuning_env(TUNE_GEMM_BM);
-    const int bm = bm_env ? bm_env : (m > 32 ? 64 : 32);
+    const int bm = bm_env ? bm_env : (w_type == TYPE_Q6_K && kq6_wide_tiles(m, n_rows, nsb)) ? 66 : (m > 32 ? 64 : 32);
     if (bm == 16) return 16;
+    if (bm == 66 && w_type == TYPE_Q6_K) return 64;
     if (tuning_env(TUNE_GEMM_KG, 2) == 2) return w_type == TYPE_Q4_K && (bm == 64 || bm == 65) ? 64 : 32;
     return bm >= 64 ? 64 : 32;
 }
 
 int kq_k_slices(int w_type, size_t m, size_t n_rows, size_t k) {
-    const size_t bm = kq_tile_rows(w_type, m);
+    const size_t bm = kq_tile_rows(w_type, m, n_rows, k / 256);
     const size_t tiles = (m + bm - 1) / bm * ((n_rows + KQ_BN - 1) / KQ_BN), nsb = k / 256;
     int ks = 1;
     while (ks < 16 && tiles * ks * 2 <= 256 && nsb % (size_t)(ks * 4) == 0) ks *= 2;

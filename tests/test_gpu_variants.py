@@ -63,6 +63,7 @@ GEMM_VARIANTS = [
     dict(BARQ_GEMM_KS=2, BARQ_GEMM_BM=16), dict(BARQ_GEMM_KS=2, BARQ_GEMM_BM=65), dict(BARQ_GEMM_KS=4, BARQ_GEMM_BM=32),
     dict(BARQ_GEMM_DEFER=1), dict(BARQ_GEMM_DEFER=0), dict(BARQ_GEMM_DEFER=1, BARQ_GEMM_KS=2),
     dict(BARQ_GEMM_DEFER=2), dict(BARQ_GEMM_DEFER=3), dict(BARQ_GEMM_DEFER=3, BARQ_GEMM_KS=2), dict(BARQ_GEMM_DEFER=2, BARQ_GEMM_KS=4),
+    dict(BARQ_GEMM_BM=66), dict(BARQ_GEMM_BM=66, BARQ_GEMM_KS=2),
 ]
 
 
@@ -117,7 +118,8 @@ def test_gemm_k_slices(be, orc, w_type):
     makes (one to eight), device and host buffers, and f32 activations
     quantized in the call (the quantized rows and the partials share the
     workspace)."""
-    for n, k, m in [(1000, 4096, 16), (130, 2048, 17), (300, 1024, 40), (4100, 512, 33), (129, 4096, 100)]:
+    for n, k, m in [(1000, 4096, 16), (130, 2048, 17), (300, 1024, 40), (4100, 512, 33), (129, 4096, 100),
+                    (256, 8192, 128)]:   # the last: Q6_K's 64-row four-wave tiles by default (long K)
         w, xq, ref = matmul_case(orc, w_type, n, k, m, 700 + n + m)
         print(f"k slices {w_type} n={n} k={k} m={m}", flush=True)
         got = be.matmul(w_type, dev(w), n, k, B.Q8_PARTNER[w_type], dev(xq), m).cpu().numpy()
