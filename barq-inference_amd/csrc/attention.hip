@@ -450,6 +450,40 @@ void attn_combine_q8k_kernel(const float* __restrict__ part, int n_split, int n_
     }
 }
 
+// The merge for a few splits (the prompt kernel's): one thread per output
+// value, 256 per workgroup (the 256 / HD heads of one Q8_K block of row i);
+// Q8 writes the block's Q8_K bytes (q8_k_block) instead of the f32 values.
+template <int HD, bool Q8>
+__global__ __launch_bounds__(256)
+void attn_combine_few_kernel(const float* __restrict__ part, int n_split, int n_head, float* __restrict__ out,
+                             uint8_t* __restrict__ out_q8) {
+    __shared__ __align__(16) float vals[256];
+    const int b = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
+    const int h = b * (256 / HD) + t / HD, d = t % HD;
+    const float* pp = part + ((size_t)i * n_head + h) * n_split * (HD + 2);
+    float M = -INFINITY;
+    for (int sp = 0; sp < n_split; sp++) M = fmaxf(M, pp[(size_t)sp * (HD + 2)]);
+    float L = 0.0f, O = 0.0f;
+    for (int sp = 0; sp < n_split; sp++) {
+        const float ms = pp[(size_t)sp * (HD + 2)];
+        const float w = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
+        L = __builtin_fmaf(pp[(size_t)sp * (HD + 2) + 1], w, L);
+        O = __builtin_fmaf(pp[(size_t)sp * (HD + 2) + 2 + d], w, O);
+    }
+    const float v = O / L;
+    if constexpr (!Q8) {
+        out[((size_t)i * n_head + h) * HD + d] = v;
+    } else {
+        vals[t] = v;
+        __syncthreads();
+        if (t < 64) {
+            const float4 v4 = reinterpret_cast<const float4*>(vals)[t];
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+            q8_k_block(vv, t, out_q8 + ((size_t)i * (n_head * HD / 256) + b) * Q8_K_BYTES);
+        }
+    }
+}
+
 bool attention_supported(size_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 
 // ---- prompt chunks on MFMA ----------------------------------------------------
@@ -492,12 +526,17 @@ __device__ __forceinline__ void am_issue(uint8_t* stage, i32x4v kr, i32x4v vr, u
     }
 }
 
-// One 32-row query block qb of the workgroup's W heads.
+// One 32-row query block qb of the workgroup's W heads.  With n_split > 1
+// the workgroup takes split `split` of the block's visible positions (a
+// contiguous run of 32-position blocks) and stores its partial state (max in
+// log2 units, sum, unnormalised output) in the split kernel's layout for the
+// merge kernels; an empty run stores (-inf, 0, 0).
 template <int W>
 __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const float* __restrict__ q,
                                           const float* __restrict__ kc, const float* __restrict__ vc, size_t layer_off,
                                           size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
-                                          long long start_pos, float score_scale, float* __restrict__ out, int qb) {
+                                          long long start_pos, float score_scale, float* __restrict__ out, int qb,
+                                          int n_split = 1, int split = 0, float* __restrict__ part = nullptr) {
     constexpr int HD = 128;
     const int l = threadIdx.x & 63, c = l & 31, g = l >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -513,8 +552,10 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
     const int i_last = min(i0 + 31, q_len - 1);
     const long long vis_last = start_pos + i_last + 1;
     const int j_end = (int)(vis_last < kv_len ? vis_last : kv_len);
-    const int nblk = (j_end + 31) / 32;
-    if (nblk > 0) am_issue<W>(lds[0], kr, vr, 0u, wave, l);
+    const int nblk_all = (j_end + 31) / 32;
+    const int per = (nblk_all + n_split - 1) / n_split;
+    const int b_lo = min(split * per, nblk_all), nblk = min(b_lo + per, nblk_all);
+    if (b_lo < nblk) am_issue<W>(lds[0], kr, vr, (uint32_t)b_lo * 32u * 512u, wave, l);
 
     float qv[64];
     {
@@ -529,13 +570,13 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
 
     f32x16a o0 = {}, o1 = {}, o2 = {}, o3 = {};
     float m = -INFINITY, lsum = 0.0f;
-    for (int b = 0; b < nblk; b++) {
+    for (int b = b_lo; b < nblk; b++) {
         const int j0 = 32 * b;
         wait_vmcnt<0>();
         asm volatile("" ::: "memory");
         __syncthreads();   // block b is in its stage; every wave is done with the other one
-        if (b + 1 < nblk) am_issue<W>(lds[(b + 1) & 1], kr, vr, (uint32_t)(j0 + 32) * 512u, wave, l);
-        const uint8_t* ks = lds[b & 1];
+        if (b + 1 < nblk) am_issue<W>(lds[(b + 1 - b_lo) & 1], kr, vr, (uint32_t)(j0 + 32) * 512u, wave, l);
+        const uint8_t* ks = lds[(b - b_lo) & 1];
         const uint8_t* vs = ks + AM_BLK;
         f32x16a sa = {}, sb = {};
         #pragma unroll
@@ -556,15 +597,20 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
             bm = fmaxf(bm, sc[r]);
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32));
-        // position 0 is visible to every query, so mn is finite from the first block on
+        // Position 0 is visible to every query, so without a split mn is
+        // finite from the first block on; a split that starts later can hold
+        // blocks a query sees none of (mn = -inf): exponents then use 0 as
+        // the reference, so they are 0 instead of NaN and the state stays
+        // (-inf, 0, 0).
         const float mn = fmaxf(m, bm);
-        const float corr = fast_exp2(m - mn);   // 0 while m is -inf
+        const float mref = mn == -INFINITY ? 0.0f : mn;
+        const float corr = fast_exp2(m - mref);   // 0 while m is -inf
         m = mn;
         float p[16];
         float rs = 0.0f;
         #pragma unroll
         for (int r = 0; r < 16; r++) {
-            p[r] = fast_exp2(sc[r] - mn);   // 0 for masked positions
+            p[r] = fast_exp2(sc[r] - mref);   // 0 for masked positions
             rs += p[r];
         }
         rs += __shfl_xor(rs, 32);
@@ -579,6 +625,23 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
             o2 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, p[st], o2, 0, 0, 0);
             o3 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[st], o3, 0, 0, 0);
         }
+    }
+    if (n_split > 1) {
+        if (q_ok) {
+            float* pp = part + (((size_t)qi * n_head + h) * n_split + split) * (HD + 2);
+            if (g == 0) {
+                pp[0] = m;
+                pp[1] = lsum;
+            }
+            #pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int i = 8 * (r >> 2) + 4 * g + (r & 3);
+                float* d = pp + 2 + 4 * i;   // 8-byte aligned rows: two float2 stores
+                *reinterpret_cast<float2*>(d) = make_float2(o0[r], o1[r]);
+                *reinterpret_cast<float2*>(d + 2) = make_float2(o2[r], o3[r]);
+            }
+        }
+        return;
     }
     if (q_ok) {
         float* op = out + ((size_t)qi * n_head + h) * HD;
@@ -598,12 +661,12 @@ template <int W, bool PAIR>
 __global__ __launch_bounds__(64 * W)
 void attn_mfma_kernel(const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
                       size_t layer_off, size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
-                      long long start_pos, float score_scale, float* __restrict__ out) {
+                      long long start_pos, float score_scale, float* __restrict__ out, float* __restrict__ part) {
     __shared__ __align__(16) uint8_t lds[2][2 * AM_BLK];
     const int nqb = (q_len + 31) / 32, x = blockIdx.x;
     const int qb_long = nqb - 1 - x;
     am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale, out,
-                 qb_long);
+                 qb_long, (int)gridDim.z, (int)blockIdx.z, part);
     if (PAIR && x < qb_long) {
         __syncthreads();   // every wave is done with the stages
         am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale,
@@ -619,6 +682,37 @@ static bool attn_mfma_path(const AttnArgs& a) {
     return a.head_dim == 128 && a.q_len >= (size_t)attn_mfma_min_q() && a.kv_len < ((size_t)1 << 23);
 }
 
+static int cu_count_attn();
+
+// Launch plan of the prompt kernel: W query heads per workgroup (W divides
+// the GQA group), query-block pairing when the pairs alone fill the CUs, and
+// otherwise a split of the positions (partial states merged by
+// attn_combine_few_kernel) until about one workgroup per CU runs.
+struct AmPlan {
+    int w, n_split;
+    bool pair;
+    unsigned nqb, groups;
+};
+
+static AmPlan attn_mfma_plan(size_t n_head, size_t n_head_kv, size_t q_len) {
+    AmPlan p{};
+    const size_t grp = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
+    p.w = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1;
+    p.nqb = (unsigned)((q_len + 31) / 32);
+    p.groups = (unsigned)(n_head / p.w);
+    const size_t cus = (size_t)cu_count_attn(), wgs = (size_t)p.nqb * p.groups;
+    p.pair = (size_t)(p.nqb / 2) * p.groups >= cus;
+    p.n_split = 1;
+    // measured on MI355X (Llama-3-8B heads, us per call for 1 / 2 / 4 / 8
+    // splits): 256 tokens 45.6 / 34.6 / 31.3 / 38.9, 512 tokens 85.0 / 60.1 /
+    // 68.4 / 83.9, 1024 tokens 164 / 174 / 190 / 224: about one workgroup per CU
+    if (!p.pair)
+        while (p.n_split < 8 && wgs * (size_t)p.n_split * 2 <= cus) p.n_split *= 2;
+    const int ovr = tuning_env(TUNE_ATTN_MFMA_SPLIT);
+    if (ovr > 0 && !p.pair) p.n_split = ovr < ATT_MAX_SPLIT ? ovr : ATT_MAX_SPLIT;
+    return p;
+}
+
 static int cu_count_attn() {
     static std::atomic<int> n[64] = {};   // per device; racing callers store the same value
     int dev = 0;
@@ -632,8 +726,10 @@ static int cu_count_attn() {
 }
 
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv) {
-    if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q() && kv_len < ((size_t)1 << 23))
-        return 0;   // the MFMA path keeps no partials
+    if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q() && kv_len < ((size_t)1 << 23)) {
+        const AmPlan p = attn_mfma_plan(n_head, n_head_kv, q_len);
+        return p.n_split > 1 ? (size_t)p.n_split * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
+    }
     int ns = 0, chunk = 0;
     attention_plan(n_head, n_head_kv, q_len, kv_len, &ns, &chunk);
     return ns > 1 ? (size_t)ns * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
@@ -665,8 +761,8 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
 // emits Q8_K rows); otherwise it writes f32 rows to a.out and the caller
 // quantizes them.
 bool attention_q8_direct(const AttnArgs& a) {
-    if (attn_mfma_path(a)) return false;
     if ((a.n_head * a.head_dim) % 256 != 0) return false;
+    if (attn_mfma_path(a)) return attn_mfma_plan(a.n_head, a.n_head_kv, a.q_len).n_split > 1;
     int ns = 0, chunk = 0;
     attention_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len, &ns, &chunk);
     return ns > 1;
@@ -706,20 +802,32 @@ hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
     if (a.q_len == 0 || a.n_head == 0) return hipSuccess;
     if (attn_mfma_path(a)) {
         const float scale = (1.0f / sqrtf(128.0f)) * LOG2E;
-        // W query heads per workgroup share one kv head (W divides the group size)
-        const size_t grp = (a.n_head_kv && a.n_head % a.n_head_kv == 0) ? a.n_head / a.n_head_kv : 1;
-        const int w = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1;
-        const unsigned nqb = (unsigned)((a.q_len + 31) / 32), groups = (unsigned)(a.n_head / w);
-        const bool pair = (size_t)(nqb / 2) * groups >= (size_t)cu_count_attn();
-        const dim3 grid(pair ? (nqb + 1) / 2 : nqb, groups);
+        const AmPlan p = attn_mfma_plan(a.n_head, a.n_head_kv, a.q_len);
+        const int w = p.w;
+        const bool pair = p.pair;
+        const dim3 grid(pair ? (p.nqb + 1) / 2 : p.nqb, p.groups, (unsigned)p.n_split);
 #define BARQ_AM_LAUNCH(W_, P_)                                                                                    \
     hipLaunchKernelGGL((attn_mfma_kernel<W_, P_>), grid, dim3(64 * W_), 0, s, a.q, a.k, a.v, a.layer_off,           \
                        a.head_stride, (int)a.n_head, (int)a.n_head_kv, (int)a.q_len, (int)a.kv_len,               \
-                       (long long)a.start_pos, scale, a.out)
+                       (long long)a.start_pos, scale, a.out, a.part)
         if (w == 4) { if (pair) BARQ_AM_LAUNCH(4, true); else BARQ_AM_LAUNCH(4, false); }
         else if (w == 2) { if (pair) BARQ_AM_LAUNCH(2, true); else BARQ_AM_LAUNCH(2, false); }
         else { if (pair) BARQ_AM_LAUNCH(1, true); else BARQ_AM_LAUNCH(1, false); }
 #undef BARQ_AM_LAUNCH
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || p.n_split == 1) return e;
+        if ((a.n_head * 128) % 256 == 0) {
+            const dim3 cg((unsigned)(a.n_head * 128 / 256), (unsigned)a.q_len);
+            if (a.out_q8)
+                hipLaunchKernelGGL((attn_combine_few_kernel<128, true>), cg, dim3(256), 0, s, a.part, p.n_split,
+                                   (int)a.n_head, a.out, a.out_q8);
+            else
+                hipLaunchKernelGGL((attn_combine_few_kernel<128, false>), cg, dim3(256), 0, s, a.part, p.n_split,
+                                   (int)a.n_head, a.out, a.out_q8);
+        } else {
+            hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(1024), 0, s,
+                               a.part, p.n_split, (int)a.n_head, a.out);
+        }
         return hipGetLastError();
     }
     switch (a.head_dim) {
