@@ -124,6 +124,29 @@ def test_attention_graph_replays(be):
     c.close()
 
 
+@pytest.mark.parametrize("q_len", [512, 100])
+def test_prompt_attention_graph_replays(be, q_len):
+    """The MFMA prompt kernel captured: 512 tokens (position splits, the
+    one-thread merge) and a ragged 100-token chunk after a prefix."""
+    import torch
+    n_head, n_kv, hd = 32, 8, 128
+    kv = q_len + 40
+    c = A.KVCache(be, kv, 2, n_kv, hd)
+    rng = np.random.default_rng(9)
+    for layer in range(2):
+        c.append(layer, dev(rng.standard_normal((n_kv, kv, hd)).astype(np.float32)),
+                 dev(rng.standard_normal((n_kv, kv, hd)).astype(np.float32)), kv, hd)
+    q = dev(rng.standard_normal((n_head, q_len, hd)).astype(np.float32))
+    out = torch.empty((q_len, n_head, hd), dtype=torch.float32, device="cuda")
+    out2 = torch.empty_like(out)
+
+    def call(layer, o):
+        B._lib.check(be._lib.barq_rocm_attention(be.h, q.data_ptr(), c.c, layer, n_head, n_kv, hd, q_len, kv, 40,
+                                                 o.data_ptr(), B.MEM_DEVICE))
+    replays_match(be, lambda: call(1, out), out, lambda: call(0, out2))
+    c.close()
+
+
 def test_graph_replay_after_workspace_growth(be):
     """A graph captured around a call that uses the workspace keeps working
     after a later, larger call grows the workspace: the old buffer is
