@@ -62,6 +62,8 @@ def parse():
     p.add_argument("--ffn", action="store_true",
                    help="time the dense FFN (feed_forward: gate/up Q4_K, SwiGLU, down Q6_K) at Llama-3-8B shapes")
     p.add_argument("--m", type=int, default=1, help="--ffn: tokens per call; --prefill: prompt tokens (default 512)")
+    p.add_argument("--decode", action="store_true",
+                   help="a whole Llama-3-8B decode token (32 layers, output norm, LM head) over --kv-len cached positions")
     p.add_argument("--prefill", action="store_true",
                    help="one Llama-3-8B layer over a --m token prompt (GEMMs, MFMA attention): tokens/s")
     p.add_argument("--layer", action="store_true",
@@ -496,6 +498,112 @@ def bench_ffn(args):
     return 0
 
 
+def bench_decode(args):
+    """One decode token of a Llama-3-8B-shaped model (LlamaTransformer::forward
+    for one token: 32 x forward_layer, transformer.rs:123-144, then the output
+    norm and final_output :468-498) on the integer path, all 386 launches of
+    a token captured in one HIP graph.  Each layer runs the decode-layer
+    chain of --layer (12 launches) over its own KV cache of --kv-len cached
+    positions; the layers' weights rotate over three distinct copies of a
+    Q4_K_M layer (417 MB, more than the Infinity Cache holds), the LM head
+    is Q6_K 128256 x 4096.  Synthetic weights and activations."""
+    import numpy as np
+    import torch
+
+    import barq_rocm as B
+    from barq_rocm import attention as A
+    from barq_rocm import synth
+
+    n_embd, n_head, n_kv, hd, n_ff, n_layer, n_vocab = 4096, 32, 8, 128, 14336, 32, 128256
+    kv_len = args.kv_len
+    tokens = args.steps if args.steps <= 16 else 4
+    mats = [("q", B.Q4_K, n_head * hd, n_embd), ("k", B.Q4_K, n_kv * hd, n_embd), ("v", B.Q6_K, n_kv * hd, n_embd),
+            ("o", B.Q4_K, n_embd, n_head * hd), ("gate", B.Q4_K, n_ff, n_embd), ("up", B.Q4_K, n_ff, n_embd),
+            ("down", B.Q6_K, n_embd, n_ff)]
+    log("generating the synthetic layer and LM-head weights")
+    host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
+    head_h = synth.gen_weights(B.Q6_K, n_vocab, n_embd, 880)
+    wbytes = sum(a.nbytes for a in host.values())
+    copies = 3
+    be = B.Backend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    layers = [{nm: torch.from_numpy(a).cuda() for nm, a in host.items()} for _ in range(copies)]
+    head = torch.from_numpy(head_h).cuda()
+    del host, head_h
+    norm_w = torch.from_numpy((0.01 * (1.0 + 0.1 * synth.gen_f32(n_embd, 820))).astype(np.float32)).cuda()
+    f = torch.from_numpy(np.array([np.float32(500000.0) ** np.float32(-2.0 * i / hd) for i in range(hd // 2)],
+                                  dtype=np.float32)).cuda()
+    kv = A.KVCache(be, kv_len + 3 * tokens + 8, n_layer, n_kv, hd)
+    rng = np.random.default_rng(5)
+    kk = rng.standard_normal((n_kv, kv_len - 1, hd)).astype(np.float32)
+    kkd = torch.from_numpy(kk).cuda()
+    for layer in range(n_layer):   # kv_len - 1 cached positions per layer
+        kv.append(layer, kkd, kkd * 0.5, kv_len - 1, hd)
+    del kkd
+    x0 = torch.from_numpy(synth.gen_f32(n_embd, 821)).cuda().reshape(1, n_embd)
+    zero = torch.zeros((1, n_embd), dtype=torch.float32, device="cuda")
+    bufA, bufB = torch.empty_like(x0), torch.empty_like(x0)
+    nbq = (n_embd // 256) * 292
+    xq, xq2, aq = (torch.empty((1, nbq), dtype=torch.uint8, device="cuda") for _ in range(3))
+    q = torch.empty((1, n_head * hd), dtype=torch.float32, device="cuda")
+    k = torch.empty((1, n_kv * hd), dtype=torch.float32, device="cuda")
+    v = torch.empty((1, n_kv * hd), dtype=torch.float32, device="cuda")
+    qr = torch.empty((n_head, 1, hd), dtype=torch.float32, device="cuda")
+    o = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
+    ff = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
+    logits = torch.empty((1, n_vocab), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    pos = [kv_len - 1]
+
+    def token(i):
+        p0 = pos[0]
+        h, prev = x0, zero
+        for layer in range(n_layer):
+            L = layers[layer % copies]
+            # residual stream: bufB = h + previous FFN output, bufA = bufB + attention output
+            be.add_rms_norm_quantize(B.Q8_K, h, prev, norm_w, 1e-5, sum_out=bufB, out=xq, sync=False)
+            be.matmul_raw(B.Q4_K, L["q"], n_head * hd, n_embd, B.Q8_K, xq, 1, q, B.MEM_DEVICE)
+            be.matmul_raw(B.Q4_K, L["k"], n_kv * hd, n_embd, B.Q8_K, xq, 1, k, B.MEM_DEVICE)
+            be.matmul_raw(B.Q6_K, L["v"], n_kv * hd, n_embd, B.Q8_K, xq, 1, v, B.MEM_DEVICE)
+            kv.append_rope_q(layer, q, n_head, k, v, 1, p0, 1.0, f, A.ROPE_INTERLEAVED, q_out=qr)
+            A.compute_attention_q8k(be, qr, kv, layer, n_head, n_kv, hd, 1, p0 + 1, p0, sync=False, out=aq)
+            be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.Q8_K, aq, 1, o, B.MEM_DEVICE)
+            be.add_rms_norm_quantize(B.Q8_K, bufB, o, norm_w, 1e-5, sum_out=bufA, out=xq2, sync=False)
+            be.ffn(B.Q4_K, L["gate"], B.Q4_K, L["up"], B.Q6_K, L["down"], n_embd, n_ff, B.Q8_K, xq2, 1, sync=False,
+                   out=ff)
+            h, prev = bufA, ff
+        # output norm of the last residual + FFN output, then the LM head
+        be.add_rms_norm_quantize(B.Q8_K, h, prev, norm_w, 1e-5, sum_out=bufB, out=xq, sync=False)
+        be.matmul_raw(B.Q6_K, head, n_vocab, n_embd, B.Q8_K, xq, 1, logits, B.MEM_DEVICE)
+        pos[0] += 1
+
+    token(0)   # warm-up outside the graph (workspace, kernel attributes)
+    torch.cuda.synchronize()
+    log(f"timing {tokens} decode tokens ({n_layer} layers, kv_len {kv_len})")
+    ms, method = time_launches(token, tokens, args.eager)
+    kv_bytes = 2 * n_kv * kv_len * hd * 4
+    alg = n_layer * (wbytes + kv_bytes) + head.numel()
+    gbs = alg / (ms * 1e-3) / 1e9
+    result = {
+        "metric": f"Llama-3-8B-shaped decode (batch 1, kv_len {kv_len}) tokens/s, 1 GPU",
+        "value": round(1e3 / ms, 2), "unit": "tokens/s", "n_gpus": 1, "steps": tokens, "warmup": 1,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"LlamaTransformer forward, 1 token, {n_layer} layers (Q4_K_M mix, 3 distinct layer copies), "
+                               f"kv_len {kv_len}, LM head Q6_K {n_vocab} x {n_embd}", "timing": method},
+        "ms_per_token": round(ms, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
+                     "scope": "one token: 32 layers' weights and K/V rows, the LM head, activations not counted"},
+    }
+    kv.close()
+    be.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def bench_prefill(args):
     """One Llama-3-8B layer over an M-token prompt from position 0
     (forward_layer, transformer.rs:123-144, with seq_len = M) on the integer
@@ -828,6 +936,8 @@ def main():
         return bench_layer(args)
     if args.prefill:
         return bench_prefill(args)
+    if args.decode:
+        return bench_decode(args)
     if args.config == 5:
         return bench_moe(args)
     cfg = synth.CONFIGS[args.config]
