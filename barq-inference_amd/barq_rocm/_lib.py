@@ -65,7 +65,7 @@ EXPORTS = (
     "barq_rocm_rope", "barq_rocm_transpose_heads", "barq_rocm_kv_cache_create", "barq_rocm_kv_cache_append",
     "barq_rocm_kv_cache_append_rope", "barq_rocm_kv_cache_size", "barq_rocm_kv_cache_layer_len",
     "barq_rocm_kv_cache_head", "barq_rocm_kv_cache_clear", "barq_rocm_kv_cache_destroy", "barq_rocm_attention",
-    "barq_rocm_kv_cache_append_rope_q", "barq_rocm_attention_q8k",
+    "barq_rocm_kv_cache_append_rope_q", "barq_rocm_attention_q8k", "barq_rocm_matvec_group",
     "barq_rocm_matmul_noalloc",
 )
 
@@ -110,6 +110,7 @@ def _declare(lib):
         "barq_rocm_add_rms_norm_quantize": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _vp, _i]),
         "barq_rocm_matvec": (_i, [_vp, _i, _vp, _sz, _sz, _i, _vp, _vp, _i]),
         "barq_rocm_matmul": (_i, [_vp, _i, _vp, _sz, _sz, _i, _vp, _sz, _vp, _i]),
+        "barq_rocm_matvec_group": (_i, [_vp, _sz, _vp, _vp, _vp, _sz, _i, _vp, _vp, _i]),
         "barq_rocm_swiglu": (_i, [_vp, _i, _vp, _vp, _sz, _sz, _vp, _i]),
         "barq_rocm_ffn": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _sz, _sz, _i, _vp, _sz, _vp, _i]),
         "barq_rocm_gemm_f32": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _i]),

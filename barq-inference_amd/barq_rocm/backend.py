@@ -72,6 +72,15 @@ class Backend:
     def matmul_raw(self, w_type, w, n_rows, k, act_type, x, m, y, mem):
         L.check(self._lib.barq_rocm_matmul(self.h, w_type, _ptr(w), n_rows, k, act_type, _ptr(x), m, _ptr(y), mem))
 
+    def matvec_group_raw(self, w_types, ws, n_rows, k, act_type, x, ys, mem):
+        """barq_rocm_matvec_group: ys[i] = ws[i] . x for every matrix (one launch where supported)."""
+        n = len(ws)
+        tarr = (ctypes.c_int * n)(*w_types)
+        warr = (ctypes.c_void_p * n)(*[_ptr(w) for w in ws])
+        rarr = (ctypes.c_size_t * n)(*n_rows)
+        yarr = (ctypes.c_void_p * n)(*[_ptr(y) for y in ys])
+        L.check(self._lib.barq_rocm_matvec_group(self.h, n, tarr, warr, rarr, k, act_type, _ptr(x), yarr, mem))
+
     def matmul_noalloc_raw(self, w_type, w, n_rows, k, act_type, x, m, y):
         """barq_rocm_matmul_noalloc: device buffers, the fixed per-GPU scratch."""
         L.check(self._lib.barq_rocm_matmul_noalloc(self.h, w_type, _ptr(w), n_rows, k, act_type, _ptr(x), m, _ptr(y)))

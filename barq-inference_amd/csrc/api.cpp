@@ -500,6 +500,27 @@ int barq_rocm_matmul(barq_rocm_handle* h, int w_type, const void* w, size_t n_ro
     return matmul_any(h, w_type, w, n_rows, k, act_type, x, m, y, mem, "matmul");
 }
 
+int barq_rocm_matvec_group(barq_rocm_handle* h, size_t n_mats, const int* w_types, const void* const* w,
+                           const size_t* n_rows, size_t k, int act_type, const void* x, float* const* y, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (n_mats == 0) return ok();
+    if (!w_types || !w || !n_rows || !y) return fail(BARQ_E_INVALID, "matvec_group: null array");
+    for (size_t i = 0; i < n_mats; i++)
+        BARQ_CHECK(check_matmul_args(w_types[i], n_rows[i], k, act_type, w[i], x, 1, y[i], "matvec_group"));
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    // one launch for Q4_K matrices (and a last Q6_K one) on device Q8_K rows
+    if (mem == BARQ_MEM_DEVICE && act_type == BARQ_TYPE_Q8_K && aligned(x, 4) &&
+        barq::gemv_group_supported(n_mats, w_types, w, n_rows, k)) {
+        for (size_t i = 0; i < n_mats; i++)
+            if (!aligned(y[i], 4)) return fail(BARQ_E_INVALID, "matvec_group: y must be 4-byte aligned");
+        return launched(barq::gemv_group_launch(n_mats, w_types, w, n_rows, k, x, y, h->stream), "matvec_group");
+    }
+    for (size_t i = 0; i < n_mats; i++)
+        BARQ_CHECK(matmul_any(h, w_types[i], w[i], n_rows[i], k, act_type, x, 1, y[i], mem, "matvec_group"));
+    return ok();
+}
+
 // ---------------------------------------------------------------------------
 // dense FFN (LlamaTransformer::feed_forward, transformer.rs:378-408)
 

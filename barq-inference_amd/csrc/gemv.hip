@@ -43,14 +43,11 @@ __device__ __forceinline__ int wg_rows_remap(int id, int G) {
 // next to their uses), so each wave has R rows of HBM traffic in flight.
 // ONE: k <= 4096, a single 4096-element chunk (no loop: fewer VGPRs, so more
 // waves per SIMD; C2's 7168 waves of two rows are then all resident at once).
-template <class F, int R, int WAVES, bool ONE>
-__global__ __launch_bounds__(WAVES * 64)
-void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
-                    float* __restrict__ y, int n_rows, int k) {
-    const int l = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
-    if (row0 >= n_rows) return;
+// R rows from row0 (of n_rows) of W by this wave.
+template <class F, int R, bool ONE>
+__device__ __forceinline__ void gemv_q8_rows(const uint8_t* __restrict__ W, size_t row_bytes,
+                                             const uint8_t* __restrict__ xq, float* __restrict__ y, int row0,
+                                             int n_rows, int k, int l) {
     const typename F::Lane c = F::lane(l);
     const int nblk = k / F::ROW_BLOCK_ELEMS;
     const int n_it = ONE ? 1 : (k + 4095) / 4096;
@@ -82,6 +79,58 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
             const int rr = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
             if (rr < R && rr <= last) y[row0 + rr] = v;
         }
+    }
+}
+
+template <class F, int R, int WAVES, bool ONE>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8_t* __restrict__ xq,
+                    float* __restrict__ y, int n_rows, int k) {
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
+    if (row0 >= n_rows) return;
+    gemv_q8_rows<F, R, ONE>(W, row_bytes, xq, y, row0, n_rows, k, l);
+}
+
+// Several projections of one activation row in one launch (the q, k and v
+// projections of self_attention, transformer.rs:212-220, all on the same
+// normalized x): matrices 0 .. NA-1 are in format FA (RA rows per wave),
+// matrix NA (if NB) in format FB (RB rows per wave); the first workgroups
+// take FA's rows, the rest FB's.  One launch pays the ramp-up and drain of a
+// memory-bound kernel once for all of them (the k and v projections of
+// Llama-3-8B are 1024 rows each: alone they leave most CUs idle).
+struct GemvGroupArgs {
+    const uint8_t* w[4];
+    float* y[4];
+    int rows[4];
+    int n_a;              // matrices in format FA
+    int wg_a;             // workgroups of the FA matrices (each matrix's rows padded to whole workgroups)
+    size_t rb_a, rb_b;    // row bytes
+};
+
+template <class FA, int RA, class FB, int RB, int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q8_group_kernel(GemvGroupArgs g, const uint8_t* __restrict__ xq, int k) {
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int id = blockIdx.x;
+    if (id < g.wg_a) {
+        int mi = 0;
+        #pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const int wg = (g.rows[mi] + RA * WAVES - 1) / (RA * WAVES);
+            if (mi + 1 < g.n_a && id >= wg) {
+                id -= wg;
+                mi++;
+            }
+        }
+        const int row0 = (id * WAVES + wave) * RA;
+        if (row0 < g.rows[mi]) gemv_q8_rows<FA, RA, true>(g.w[mi], g.rb_a, xq, g.y[mi], row0, g.rows[mi], k, l);
+    } else {
+        id -= g.wg_a;
+        const int row0 = (id * WAVES + wave) * RB;
+        if (row0 < g.rows[g.n_a]) gemv_q8_rows<FB, RB, true>(g.w[g.n_a], g.rb_b, xq, g.y[g.n_a], row0, g.rows[g.n_a], k, l);
     }
 }
 
@@ -483,6 +532,53 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
     }
 }
 
+
+// The grouped launch: up to three Q4_K matrices, optionally followed by one
+// Q4_K or Q6_K matrix, k <= 4096 (one chunk), Q8_K activation; four waves
+// per workgroup, two rows per wave for Q4_K and one for Q6_K (the register
+// GEMV's Q4_K and Q6_K lane slicing).
+bool gemv_group_supported(size_t n, const int* types, const void* const* W, const size_t* rows, size_t k) {
+    if (n < 2 || n > 4 || k == 0 || k > 4096 || k % 256) return false;
+    size_t total = 0;
+    for (size_t i = 0; i < n; i++) {
+        const bool last = i + 1 == n;
+        if (types[i] != TYPE_Q4_K && !(last && types[i] == TYPE_Q6_K)) return false;
+        if (rows[i] == 0 || rows[i] > (size_t)INT32_MAX) return false;
+        if (types[i] == TYPE_Q4_K && (reinterpret_cast<uintptr_t>(W[i]) & 15)) return false;
+        if (types[i] == TYPE_Q6_K && (reinterpret_cast<uintptr_t>(W[i]) & 1)) return false;
+        total += rows[i];
+    }
+    return total <= (size_t)INT32_MAX;
+}
+
+hipError_t gemv_group_launch(size_t n, const int* types, const void* const* W, const size_t* rows, size_t k,
+                             const void* xq, float* const* y, hipStream_t s) {
+    constexpr int WAVES = 4, RA = 2, RB6 = 1;
+    GemvGroupArgs g{};
+    const bool b6 = types[n - 1] == TYPE_Q6_K;
+    g.n_a = (int)(b6 ? n - 1 : n);
+    int wg_a = 0;
+    for (size_t i = 0; i < n; i++) {
+        g.w[i] = static_cast<const uint8_t*>(W[i]);
+        g.y[i] = y[i];
+        g.rows[i] = (int)rows[i];
+        if ((int)i < g.n_a) wg_a += (int)((rows[i] + RA * WAVES - 1) / (RA * WAVES));
+    }
+    g.wg_a = wg_a;
+    g.rb_a = k / 256 * Q4_K_BYTES;
+    g.rb_b = k / 256 * (b6 ? Q6_K_BYTES : Q4_K_BYTES);
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+    if (b6) {
+        const unsigned grid = (unsigned)(wg_a + (rows[n - 1] + RB6 * WAVES - 1) / (RB6 * WAVES));
+        hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ4K, RA, FmtQ6K, RB6, WAVES>), dim3(grid), dim3(WAVES * 64), 0, s,
+                           g, x, (int)k);
+    } else {
+        // every matrix in the FA part (n_a = n); no FB part
+        hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ4K, RA, FmtQ4K, RA, WAVES>), dim3((unsigned)wg_a),
+                           dim3(WAVES * 64), 0, s, g, x, (int)k);
+    }
+    return hipGetLastError();
+}
 
 bool gemv_glu_supported(int w_type, const void* G, const void* U, size_t n_rows, size_t k) {
     return w_type == TYPE_Q4_K && k % 256 == 0 && k > 0 && n_rows > 0 && n_rows <= (size_t)INT32_MAX &&

@@ -173,6 +173,9 @@ struct AttnArgs {
     uint8_t* out_q8;          // optional: the output rows as Q8_K blocks (see attention_q8_direct)
 };
 bool attention_q8_direct(const AttnArgs& a);
+bool gemv_group_supported(size_t n, const int* types, const void* const* W, const size_t* rows, size_t k);
+hipError_t gemv_group_launch(size_t n, const int* types, const void* const* W, const size_t* rows, size_t k,
+                             const void* xq, float* const* y, hipStream_t s);
 hipError_t rope_qkv_launch(int layout, const float* qx, const float* kx, const float* vx, float* q_out, float* k_out,
                            float* v_out, size_t seq, size_t n_q, size_t n_kv, size_t hd, size_t start_pos,
                            float freq_scale, const float* inv_freq, size_t cache_head_stride, hipStream_t s);

@@ -178,6 +178,19 @@ int barq_rocm_matmul(barq_rocm_handle* h, int w_type, const void* w,
                      size_t n_rows, size_t k, int act_type, const void* x,
                      size_t m, float* y, int mem);
 
+/* matvec_group = n_mats matvecs of one activation row (the q, k and v
+ * projections of LlamaTransformer::self_attention, transformer.rs:212-220,
+ * all read the same normalized x): y[i] = W[i] . x for i < n_mats, each
+ * within barq_rocm_matvec's bar.  On device buffers with a Q8_K row,
+ * k <= 4096, Q4_K matrices and optionally a last Q6_K one (2 to 4
+ * matrices), all of them run in one launch of the register GEMV (each
+ * output bit-identical to that GEMV on its matrix alone; a Q6_K matvec on
+ * its own takes the LDS-streamed GEMV, whose summation order differs);
+ * any other case runs the matvecs one after another. */
+int barq_rocm_matvec_group(barq_rocm_handle* h, size_t n_mats, const int* w_types, const void* const* w,
+                           const size_t* n_rows, size_t k, int act_type, const void* x, float* const* y,
+                           int mem);
+
 /* ---- dense FFN ------------------------------------------------------------
  * swiglu: the SwiGLU of LlamaTransformer::feed_forward
  *   (models/src/transformer.rs:394-399), h = (g * (1 / (1 + exp(-g)))) * u
