@@ -20,7 +20,7 @@ namespace barq {
 enum Tune : int {
     TUNE_GEMM_BM, TUNE_GEMM_KG, TUNE_GEMM_NS, TUNE_GEMM_KS, TUNE_GEMM_XCD, TUNE_GEMM_IMPL, TUNE_GEMM_MIN_M,
     TUNE_GEMV_DMA, TUNE_GEMV_DMA_TYPES, TUNE_GEMV_MULTI_MAX, TUNE_GEMV_CFG_R, TUNE_GEMV_CFG_W,
-    TUNE_MOE_GEMV, TUNE_MOE_FUSED_GROUP, TUNE_ATTN_WG, TUNE_GEMV_GLU, TUNE_GEMM_DEFER, TUNE_ATTN_MFMA_MIN_Q, TUNE_ATTN_MFMA_SPLIT, TUNE_COUNT
+    TUNE_MOE_GEMV, TUNE_MOE_FUSED_GROUP, TUNE_ATTN_WG, TUNE_GEMV_GLU, TUNE_GEMM_DEFER, TUNE_ATTN_MFMA_MIN_Q, TUNE_ATTN_MFMA_SPLIT, TUNE_GEMV_LDS, TUNE_COUNT
 };
 
 struct Tuning {
@@ -31,7 +31,8 @@ struct Tuning {
         static const char* const names[TUNE_COUNT] = {
             "BARQ_GEMM_BM", "BARQ_GEMM_KG", "BARQ_GEMM_NS", "BARQ_GEMM_KS", "BARQ_GEMM_XCD", "BARQ_GEMM_IMPL",
             "BARQ_GEMM_MIN_M", "BARQ_GEMV_DMA", "BARQ_GEMV_DMA_TYPES", "BARQ_GEMV_MULTI_MAX", nullptr, nullptr,
-            "BARQ_MOE_GEMV", "BARQ_MOE_FUSED_GROUP", "BARQ_ATTN_WG", "BARQ_GEMV_GLU", "BARQ_GEMM_DEFER", "BARQ_ATTN_MFMA_MIN_Q", "BARQ_ATTN_MFMA_SPLIT"};
+            "BARQ_MOE_GEMV", "BARQ_MOE_FUSED_GROUP", "BARQ_ATTN_WG", "BARQ_GEMV_GLU", "BARQ_GEMM_DEFER", "BARQ_ATTN_MFMA_MIN_Q", "BARQ_ATTN_MFMA_SPLIT",
+            "BARQ_GEMV_LDS"};
         Tuning t;
         for (int i = 0; i < TUNE_COUNT; i++) {
             if (!names[i]) continue;

@@ -12,6 +12,7 @@
 // blas::gemv_f32(dequant(W), x) (blas.rs:292-303) up to summation order.
 #include "gemv_formats.hpp"
 #include "launch.hpp"
+#include "mfma_common.hpp"
 
 #include <cstdio>
 #include <cstdlib>
@@ -93,6 +94,75 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
     gemv_q8_rows<F, R, ONE>(W, row_bytes, xq, y, row0, n_rows, k, l);
 }
 
+// Q4_K with k <= 4096, two rows per wave, staged through LDS.  The wave's
+// two rows are 2 * 144 * k / 256 contiguous bytes (4608 at k = 4096); they
+// are copied into the wave's own LDS buffer by buffer->LDS loads in which
+// each lane takes 16 consecutive bytes, so every load instruction covers
+// whole cache lines and the non-temporal hint pays (each line is fetched
+// once; the register GEMV's per-lane loads cover half of each line they
+// touch, so there the hint would fetch lines twice).  The lanes then read
+// their FmtQ4K slices from LDS and run the register GEMV's arithmetic and
+// reduction: outputs are bit-identical to gemv_q8_rows<FmtQ4K, 2, true>.
+// Measured at C2 (14336 x 4096, one box, 11 rotating weight copies): 7.14
+// against 7.29 us; the bare staging reaches the streaming-read floor.
+constexpr int Q4K_LDS_BUF = 5 * 1024;   // per wave: 4608 bytes rounded up to whole 1 KB load instructions
+
+// w_bytes: bytes of the whole matrix (the buffer descriptor's range: rows
+// past the end read as zeros and are not stored)
+__device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
+                                                  const uint8_t* __restrict__ xq, float* __restrict__ y, int row0,
+                                                  int n_rows, int nblk, int l, uint8_t* buf) {
+    using F = FmtQ4K;
+    constexpr int R = 2;
+    const F::Lane c = F::lane(l);
+    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = R * rb;
+    const i32x4v rs = make_rsrc4(W, w_bytes);
+    const bool act = F::active(0, c, nblk);
+    F::X xs;
+    if (act) F::load_x(xs, xq, 0, c, nblk);
+    const uint32_t base = (uint32_t)row0 * rb;
+    #pragma unroll
+    for (int q = 0; q < Q4K_LDS_BUF / 1024; q++) {
+        if (1024u * q < span) {
+            const uint32_t off = 1024u * q + 16u * (uint32_t)l;
+            lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
+        }
+    }
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    float acc[R] = {0.0f, 0.0f};
+    if (act) {
+        F::Wt w[R];
+        #pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t* b = buf + r * rb + Q4_K_BYTES * c.sbl;
+            w[r].hdr = *reinterpret_cast<const uint4*>(b);
+            w[r].q0 = *reinterpret_cast<const uint4*>(b + 16 + 32 * c.p);
+            w[r].q1 = *reinterpret_cast<const uint4*>(b + 32 + 32 * c.p);
+        }
+        #pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = F::dot(w[r], xs, c);
+    }
+    const float v = reduce4(acc[0], acc[1], 0.0f, 0.0f);
+    // row r's total is in lane row_lane4(r): 0 and 32
+    if ((l & 31) == 0) {
+        const int rr = l >> 5;
+        if (row0 + rr < n_rows) y[row0 + rr] = v;
+    }
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q4k_lds_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
+                         float* __restrict__ y, int n_rows, int nblk) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][Q4K_LDS_BUF];
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (wg_rows_remap<2 * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * 2;
+    if (row0 >= n_rows) return;
+    gemv_q4k_rows_lds(W, w_bytes, xq, y, row0, n_rows, nblk, l, lds[wave]);
+}
+
 // Several projections of one activation row in one launch (the q, k and v
 // projections of self_attention, transformer.rs:212-220, all on the same
 // normalized x): matrices 0 .. NA-1 are in format FA (RA rows per wave),
@@ -109,9 +179,13 @@ struct GemvGroupArgs {
     size_t rb_a, rb_b;    // row bytes
 };
 
-template <class FA, int RA, class FB, int RB, int WAVES>
+// The FA matrices are Q4_K (two rows per wave, staged through LDS as in
+// gemv_q4k_lds_kernel).
+template <class FB, int RB, int WAVES>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_q8_group_kernel(GemvGroupArgs g, const uint8_t* __restrict__ xq, int k) {
+    constexpr int RA = 2;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][Q4K_LDS_BUF];
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     int id = blockIdx.x;
@@ -126,7 +200,9 @@ void gemv_q8_group_kernel(GemvGroupArgs g, const uint8_t* __restrict__ xq, int k
             }
         }
         const int row0 = (id * WAVES + wave) * RA;
-        if (row0 < g.rows[mi]) gemv_q8_rows<FA, RA, true>(g.w[mi], g.rb_a, xq, g.y[mi], row0, g.rows[mi], k, l);
+        if (row0 < g.rows[mi])
+            gemv_q4k_rows_lds(g.w[mi], (uint32_t)g.rows[mi] * (uint32_t)g.rb_a, xq, g.y[mi], row0, g.rows[mi], k / 256,
+                              l, lds[wave]);
     } else {
         id -= g.wg_a;
         const int row0 = (id * WAVES + wave) * RB;
@@ -503,6 +579,13 @@ hipError_t moe_gemv_launch(int w_type, const void* const* W, size_t n_experts, s
 
 // Formats that take the LDS-streaming GEMV (gemv_dma.hip) when its layout
 // conditions hold; BARQ_GEMV_DMA_TYPES (bit per format, tuning) overrides.
+// The LDS-staged Q4_K GEMV: one 4096-element chunk per row, 16-byte aligned
+// blocks, and the matrix within the buffer descriptor's 31-bit range.
+static bool q4k_lds_supported(const void* W, size_t n_rows, size_t k) {
+    return k > 0 && k <= 4096 && k % 256 == 0 && n_rows > 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0 &&
+           n_rows * (k / 256 * Q4_K_BYTES) < 0x80000000ull;
+}
+
 static int dma_bit(int w_type) {
     switch (w_type) {
     case TYPE_Q4_K: return 1;
@@ -523,7 +606,15 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
         gemv_dma_supported(w_type, W, n_rows, k, xq))
         return gemv_dma_launch(w_type, W, n_rows, k, xq, y, s);
     switch (w_type) {
-    case TYPE_Q4_K: return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, kk <= 4096 ? GemvCfg{2, 4} : GemvCfg{2, 2});
+    case TYPE_Q4_K:
+        if (q4k_lds_supported(W, n_rows, k) && tuning_env(TUNE_GEMV_LDS, 1) && !env_cfg().r) {
+            constexpr int WAVES = 4;
+            const unsigned grid = (unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES));
+            hipLaunchKernelGGL((gemv_q4k_lds_kernel<WAVES>), dim3(grid), dim3(WAVES * 64), 0, s, w,
+                               (uint32_t)(n_rows * (k / 256 * Q4_K_BYTES)), x, y, n, (int)(k / 256));
+            return hipGetLastError();
+        }
+        return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, kk <= 4096 ? GemvCfg{2, 4} : GemvCfg{2, 2});
     case TYPE_Q6_K: return dispatch_q8<FmtQ6K>(w, k / 256 * 210, x, y, n, kk, s, {1, 8});
     case TYPE_Q4_0: return dispatch_q8<FmtQ40>(w, k / 32 * 18, x, y, n, kk, s, {1, 4});
     case TYPE_Q8_0: return dispatch_q8<FmtQ80>(w, k / 32 * 34, x, y, n, kk, s, {1, 4});
@@ -545,6 +636,7 @@ bool gemv_group_supported(size_t n, const int* types, const void* const* W, cons
         if (types[i] != TYPE_Q4_K && !(last && types[i] == TYPE_Q6_K)) return false;
         if (rows[i] == 0 || rows[i] > (size_t)INT32_MAX) return false;
         if (types[i] == TYPE_Q4_K && (reinterpret_cast<uintptr_t>(W[i]) & 15)) return false;
+        if (types[i] == TYPE_Q4_K && rows[i] * (k / 256 * Q4_K_BYTES) >= 0x80000000ull) return false;
         if (types[i] == TYPE_Q6_K && (reinterpret_cast<uintptr_t>(W[i]) & 1)) return false;
         total += rows[i];
     }
@@ -570,11 +662,11 @@ hipError_t gemv_group_launch(size_t n, const int* types, const void* const* W, c
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     if (b6) {
         const unsigned grid = (unsigned)(wg_a + (rows[n - 1] + RB6 * WAVES - 1) / (RB6 * WAVES));
-        hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ4K, RA, FmtQ6K, RB6, WAVES>), dim3(grid), dim3(WAVES * 64), 0, s,
+        hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ6K, RB6, WAVES>), dim3(grid), dim3(WAVES * 64), 0, s,
                            g, x, (int)k);
     } else {
         // every matrix in the FA part (n_a = n); no FB part
-        hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ4K, RA, FmtQ4K, RA, WAVES>), dim3((unsigned)wg_a),
+        hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ4K, RA, WAVES>), dim3((unsigned)wg_a),
                            dim3(WAVES * 64), 0, s, g, x, (int)k);
     }
     return hipGetLastError();

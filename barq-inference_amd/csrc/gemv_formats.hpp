@@ -26,6 +26,7 @@ namespace barq {
 
 constexpr uint32_t M4 = 0x0F0F0F0Fu;
 constexpr uint32_t M30 = 0x30303030u;
+typedef short s16x2q __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t u4get(const uint4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
@@ -53,7 +54,8 @@ struct FmtQ4K {
     // get_scale_min_k4 (gguf.rs:825-837) for sub-blocks 2p and 2p+1 as bit
     // field extracts: p < 2 reads 6-bit fields of q[2p..2p+1] / q[2p+4..];
     // p >= 2 takes the low/high nibble of q[2p+4..] plus 2 bits of q[2p-4..].
-    struct Lane { int sbl, p; uint32_t o, n1, n2, ob; bool hi; };
+    // sel: the byte-permute selector that gathers those bytes (scales4).
+    struct Lane { int sbl, p; uint32_t o, n1, n2, ob, sel; bool hi; };
 
     static __device__ __forceinline__ Lane lane(int l) {
         Lane c;
@@ -64,6 +66,8 @@ struct FmtQ4K {
         c.n1 = c.hi ? 4u : 6u;
         c.n2 = c.hi ? 2u : 0u;
         c.ob = c.hi ? c.o + 4 : c.o;
+        const uint32_t pp = 2u * (uint32_t)(c.p & 1);
+        c.sel = pp | ((pp + 1) << 8) | ((pp + 4) << 16) | ((pp + 5) << 24);
         return c;
     }
     static __device__ __forceinline__ int blk(int it, const Lane& c) { return it * 16 + c.sbl; }
@@ -96,6 +100,17 @@ struct FmtQ4K {
         mb = (int)(__builtin_amdgcn_ubfe(B, c.ob + 8, c.n1) | (__builtin_amdgcn_ubfe(hdr.z, c.o + 14, c.n2) << 4));
     }
 
+    // The same four values as bytes [sc_a, sc_b, m_a, m_b] of one dword, by
+    // byte permutes: P gathers q[2p'], q[2p'+1], q[2p'+4], q[2p'+5] (p' = p
+    // mod 2), Q the bytes q[8+2p'], q[9+2p'] and the high nibbles of the
+    // same two bytes.  p < 2: P's 6-bit fields; p >= 2: Q's nibbles with
+    // P's top two bits above them.
+    static __device__ __forceinline__ uint32_t scales4(const uint4& hdr, const Lane& c) {
+        const uint32_t P = __builtin_amdgcn_perm(hdr.z, hdr.y, c.sel);
+        const uint32_t Q = __builtin_amdgcn_perm(hdr.w >> 4, hdr.w, c.sel);
+        return c.hi ? (((P >> 2) & M30) | (Q & M4)) : (P & 0x3F3F3F3Fu);
+    }
+
     static __device__ __forceinline__ float dot(const Wt& w, const X& x, const Lane& c) {
         int ia = 0, ib = 0;
         ia = sdot4(w.q0.x & M4, x.v[0].x, ia); ia = sdot4(w.q0.y & M4, x.v[0].y, ia);
@@ -106,11 +121,13 @@ struct FmtQ4K {
         ib = sdot4((w.q0.z >> 4) & M4, x.v[2].z, ib); ib = sdot4((w.q0.w >> 4) & M4, x.v[2].w, ib);
         ib = sdot4((w.q1.x >> 4) & M4, x.v[3].x, ib); ib = sdot4((w.q1.y >> 4) & M4, x.v[3].y, ib);
         ib = sdot4((w.q1.z >> 4) & M4, x.v[3].z, ib); ib = sdot4((w.q1.w >> 4) & M4, x.v[3].w, ib);
-        int sca, ma, scb, mb;
-        scales(w.hdr, c, sca, ma, scb, mb);
+        const uint32_t sm = scales4(w.hdr, c);
         // |ia|, |ib| <= 32*15*128 and the scales are 6-bit: 24-bit products suffice
-        const int im = __mul24(sca, ia) + __mul24(scb, ib);
-        const int in = __mul24(ma, x.sa) + __mul24(mb, x.sb);
+        const int im = __mul24((int)(sm & 0xFFu), ia) + __mul24((int)__builtin_amdgcn_ubfe(sm, 8, 8), ib);
+        // the mins against the two bsum pairs (|sa|, |sb| <= 32*128) as one i16 dot2
+        const uint32_t mm = __builtin_amdgcn_perm(0u, sm, 0x0c030c02u);   // u16 pair (m_a, m_b)
+        const uint32_t sab = ((uint32_t)x.sa & 0xFFFFu) | ((uint32_t)x.sb << 16);
+        const int in = __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2q, mm), __builtin_bit_cast(s16x2q, sab), 0, false);
         const float d = f16_bits_to_f32(w.hdr.x & 0xFFFFu);
         const float dmin = f16_bits_to_f32(w.hdr.x >> 16);
         return x.dx * __builtin_fmaf(d, (float)im, -(dmin * (float)in));

@@ -162,7 +162,7 @@ def test_matmul_small_m(be, orc, name):
 
 
 GEMV_VARIANTS = [dict(BARQ_GEMV_DMA=c) for c in (-1, 422, 444, 482, 822, 842, 222, 242, 411, 811)] + [
-    dict(BARQ_GEMV_DMA_TYPES=0), dict(BARQ_GEMV_DMA_TYPES=31)] + [
+    dict(BARQ_GEMV_DMA_TYPES=0), dict(BARQ_GEMV_DMA_TYPES=31), dict(BARQ_GEMV_LDS=0)] + [
     dict(BARQ_GEMV_DMA_TYPES=0, BARQ_GEMV_CFG=c) for c in ("1,4", "2,4", "4,4", "8,4", "1,8", "2,8", "4,8", "2,2",
                                                           "4,2", "8,2", "4,1")]
 
@@ -178,6 +178,23 @@ def test_gemv_variants(be, orc, w_type):
             with env(**v) as b:
                 got = b.matvec(w_type, wd, n, k, B.Q8_PARTNER[w_type], xd).cpu().numpy()
             assert_close_1e3(got, ref.ravel())
+
+
+def test_gemv_q4k_lds_equals_register_gemv(be, orc):
+    """The LDS-staged Q4_K GEMV (k <= 4096, the default there) against the
+    register GEMV (BARQ_GEMV_LDS=0): bit-identical outputs (same lane slices,
+    arithmetic and reduction), both within the bar of the oracle.  Odd row
+    counts leave the last wave one row; short k leaves lanes idle."""
+    from conftest import assert_bits_equal
+    for n, k in [(1, 256), (5, 512), (67, 4096), (129, 3840), (1023, 768), (14336, 4096)]:
+        print("q4k lds gemv", n, k, flush=True)
+        w, xq, ref = matmul_case(orc, B.Q4_K, n, k, 1, 1300 + n + k)
+        wd, xd = dev(w), dev(xq)
+        got = be.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
+        with env(BARQ_GEMV_LDS=0) as b:
+            reg = b.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
+        assert_bits_equal(got, reg)
+        assert_close_1e3(got, ref.ravel())
 
 
 MOE_VARIANTS = [dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_NS=3),
