@@ -66,7 +66,7 @@ EXPORTS = (
     "barq_rocm_kv_cache_append_rope", "barq_rocm_kv_cache_size", "barq_rocm_kv_cache_layer_len",
     "barq_rocm_kv_cache_head", "barq_rocm_kv_cache_clear", "barq_rocm_kv_cache_destroy", "barq_rocm_attention",
     "barq_rocm_kv_cache_append_rope_q", "barq_rocm_attention_q8k", "barq_rocm_matvec_group",
-    "barq_rocm_matmul_noalloc",
+    "barq_rocm_qkv_append_rope", "barq_rocm_matmul_noalloc",
 )
 
 # bytes of the fixed per-GPU scratch behind barq_rocm_matmul_noalloc
@@ -156,6 +156,8 @@ def _declare(lib):
         "barq_rocm_attention_q8k": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _i]),
         "barq_rocm_kv_cache_append_rope_q": (_i, [_vp, _vp, _sz, _vp, _sz, _vp, _vp, _vp, _sz, _sz, ctypes.c_float,
                                                   _vp, _i, _i]),
+        "barq_rocm_qkv_append_rope": (_i, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _i, _vp, _vp, _sz, ctypes.c_float, _vp,
+                                           _i, _i]),
         "barq_rocm_matmul_noalloc": (_i, [_vp, _i, _vp, _sz, _sz, _i, _vp, _sz, _vp]),
     }
     for name, (res, args) in P.items():

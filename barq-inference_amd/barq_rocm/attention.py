@@ -93,6 +93,20 @@ class KVCache:
                                                                layout, mem))
         return q_out
 
+    def qkv_append_rope(self, layer, w_types, ws, n_head, k, act_type, x, start_pos, rope_freq_scale, rope_inv_freq,
+                        layout, mem=L.MEM_DEVICE, q_out=None):
+        """The q/k/v projections of one token, apply_rope(q), apply_rope(k)
+        and the append (transformer.rs:212-245) in one call; returns q rotated
+        [n_head, 1, head_dim]."""
+        if q_out is None:
+            q_out = _empty((n_head, 1, self.head_dim), x, mem)
+        tarr = (ctypes.c_int * 3)(*w_types)
+        warr = (ctypes.c_void_p * 3)(*[_ptr(w) for w in ws])
+        L.check(self.be._lib.barq_rocm_qkv_append_rope(self.be.h, self.c, layer, tarr, warr, n_head, k, act_type,
+                                                        _ptr(x), _ptr(q_out), start_pos, rope_freq_scale,
+                                                        _ptr(rope_inv_freq), layout, mem))
+        return q_out
+
     def size(self) -> int:
         return self.be._lib.barq_rocm_kv_cache_size(self.c)
 

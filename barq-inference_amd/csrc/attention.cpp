@@ -283,6 +283,59 @@ int barq_rocm_kv_cache_append_rope_q(barq_rocm_handle* h, barq_rocm_kv_cache* c,
                            inv_freq, layout, mem, "kv_cache_append_rope_q");
 }
 
+int barq_rocm_qkv_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const int* w_types,
+                              const void* const* w, size_t n_head, size_t k, int act_type, const void* x,
+                              float* q_out, size_t start_pos, float freq_scale, const float* inv_freq, int layout,
+                              int mem) {
+    const char* who = "qkv_append_rope";
+    BARQ_CHECK(check_mem(mem));
+    BARQ_CHECK(check_handle(h));
+    if (!c) return fail(BARQ_E_INVALID, "%s: null cache", who);
+    if (!w_types || !w || !x || !q_out || !inv_freq) return fail(BARQ_E_INVALID, "%s: null buffer", who);
+    for (int i = 0; i < 3; i++)
+        if (!w[i]) return fail(BARQ_E_INVALID, "%s: null weight %d", who, i);
+    if (n_head == 0) return fail(BARQ_E_INVALID, "%s: no query heads", who);
+    BARQ_CHECK(check_rope_args(c->head_dim, layout));
+    if (h->device != c->device) return fail(BARQ_E_INVALID, "%s: cache is on another device", who);
+    const size_t hd = c->head_dim, nq = n_head * hd, nkv = c->n_head_kv * hd;
+    BARQ_CHECK(check_int_range(nq + 2 * nkv, "qkv_append_rope: rows"));
+    const bool append = layer < c->n_layers;
+    if (append && c->len[layer] + 1 > c->max_size)
+        return fail(BARQ_E_INVALID, "%s: layer %zu holds %zu of %zu positions, one more does not fit", who, layer,
+                    c->len[layer], c->max_size);
+    const size_t rows[3] = {nq, nkv, nkv};
+    if (mem == BARQ_MEM_DEVICE && act_type == BARQ_TYPE_Q8_K && layout == BARQ_ROPE_INTERLEAVED && append &&
+        aligned(x, 4) && aligned(q_out, 4) && barq::qkv_rope_supported(w_types, w, nq, nkv, k, hd)) {
+        DeviceGuard g(h);
+        const size_t dst_off = layer * c->layer_stride() + c->len[layer] * hd;
+        BARQ_CHECK(launched(barq::qkv_rope_launch(w_types, w, nq, nkv, k, x, hd, q_out, c->k + dst_off, c->v + dst_off,
+                                                  c->head_stride(), start_pos, freq_scale, inv_freq, h->stream),
+                            who));
+        c->len[layer] += 1;
+        if (layer == 0) c->size += 1;
+        return ok();
+    }
+    // the two calls the launch above fuses
+    if (mem == BARQ_MEM_HOST) {
+        std::vector<float> q(nq), kk(nkv), vv(nkv);
+        float* ys[3] = {q.data(), kk.data(), vv.data()};
+        BARQ_CHECK(barq_rocm_matvec_group(h, 3, w_types, w, rows, k, act_type, x, ys, mem));
+        return append_rope_any(h, c, layer, q.data(), n_head, q_out, kk.data(), vv.data(), 1, start_pos, freq_scale,
+                               inv_freq, layout, mem, who);
+    }
+    // device buffers: the projections go to the workspace, which the Q8_K
+    // matvecs and the device append do not use themselves
+    if (act_type != BARQ_TYPE_Q8_K)
+        return fail(BARQ_E_UNSUPPORTED, "%s: device buffers take a Q8_K activation row (act_type %d)", who, act_type);
+    Arena a;
+    const size_t oq = a.add(nq * 4), ok_ = a.add(nkv * 4), ov = a.add(nkv * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    float* ys[3] = {at<float>(h, oq), at<float>(h, ok_), at<float>(h, ov)};
+    BARQ_CHECK(barq_rocm_matvec_group(h, 3, w_types, w, rows, k, act_type, x, ys, mem));
+    return append_rope_any(h, c, layer, ys[0], n_head, q_out, ys[1], ys[2], 1, start_pos, freq_scale, inv_freq,
+                           layout, mem, who);
+}
+
 // ---------------------------------------------------------------------------
 // attention
 

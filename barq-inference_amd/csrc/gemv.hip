@@ -108,10 +108,11 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
 constexpr int Q4K_LDS_BUF = 5 * 1024;   // per wave: 4608 bytes rounded up to whole 1 KB load instructions
 
 // w_bytes: bytes of the whole matrix (the buffer descriptor's range: rows
-// past the end read as zeros and are not stored)
-__device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
-                                                  const uint8_t* __restrict__ xq, float* __restrict__ y, int row0,
-                                                  int n_rows, int nblk, int l, uint8_t* buf) {
+// past the end read as zeros).  Returns the two rows' results, row0's in
+// lane 0 and row0 + 1's in lane 32.
+__device__ __forceinline__ float gemv_q4k_pair_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
+                                                   const uint8_t* __restrict__ xq, int row0, int nblk, int l,
+                                                   uint8_t* buf) {
     using F = FmtQ4K;
     constexpr int R = 2;
     const F::Lane c = F::lane(l);
@@ -143,8 +144,14 @@ __device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W,
         #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = F::dot(w[r], xs, c);
     }
-    const float v = reduce4(acc[0], acc[1], 0.0f, 0.0f);
     // row r's total is in lane row_lane4(r): 0 and 32
+    return reduce4(acc[0], acc[1], 0.0f, 0.0f);
+}
+
+__device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
+                                                  const uint8_t* __restrict__ xq, float* __restrict__ y, int row0,
+                                                  int n_rows, int nblk, int l, uint8_t* buf) {
+    const float v = gemv_q4k_pair_lds(W, w_bytes, xq, row0, nblk, l, buf);
     if ((l & 31) == 0) {
         const int rr = l >> 5;
         if (row0 + rr < n_rows) y[row0 + rr] = v;
@@ -161,6 +168,95 @@ void gemv_q4k_lds_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const 
     const int row0 = (wg_rows_remap<2 * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * 2;
     if (row0 >= n_rows) return;
     gemv_q4k_rows_lds(W, w_bytes, xq, y, row0, n_rows, nblk, l, lds[wave]);
+}
+
+// One row of W by this wave with the single-chunk lane slicing (k <= 4096):
+// gemv_q8_rows<F, 1, true>'s arithmetic, the result in lane 0.
+template <class F>
+__device__ __forceinline__ float gemv_q8_row1(const uint8_t* __restrict__ W, size_t row_bytes,
+                                              const uint8_t* __restrict__ xq, int row, int k, int l) {
+    const typename F::Lane c = F::lane(l);
+    const int nblk = k / F::ROW_BLOCK_ELEMS;
+    float acc = 0.0f;
+    if (F::active(0, c, nblk)) {
+        typename F::X xs;
+        F::load_x(xs, xq, 0, c, nblk);
+        typename F::Wt w;
+        F::load_w(w, W + (size_t)row * row_bytes, 0, c, nblk);
+        __builtin_amdgcn_sched_barrier(0);
+        acc += F::dot(w, xs, c);
+    }
+    return reduce4(acc, 0.0f, 0.0f, 0.0f);
+}
+
+// The q, k and v projections of one token with RoPE and the cache append in
+// their epilogue (self_attention for one token, transformer.rs:212-245):
+// workgroups 0 .. wg_q - 1 take q's rows, then k's, then v's.  A wave's two
+// Q4_K rows 2i and 2i + 1 of a head are one rotary pair of the interleaved
+// layout, so the wave rotates them itself with rope_qkv_kernel's angle and
+// products (the same bits) and writes q_out or the cache row; v's rows go to
+// the cache as they are.  The pair's angle is computed before the rows'
+// loads land.
+struct QkvRopeArgs {
+    const uint8_t* w[3];
+    uint32_t bytes[3];        // matrix bytes (the buffer descriptors' ranges)
+    int rows[3];
+    int wg_q, wg_k;
+    int hd;
+    float* q_out;             // [n_head][hd]
+    float* k_dst;             // cache row of the new position, kv head 0; head h at + h * head_stride
+    float* v_dst;
+    size_t head_stride;
+    long long start_pos;
+    float freq_scale;
+    const float* inv_freq;
+};
+
+template <bool V6, int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_qkv_rope_kernel(QkvRopeArgs a, const uint8_t* __restrict__ xq, int k) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][Q4K_LDS_BUF];
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int id = blockIdx.x, mat = 0;
+    if (id >= a.wg_q) {
+        id -= a.wg_q;
+        mat = 1;
+        if (id >= a.wg_k) {
+            id -= a.wg_k;
+            mat = 2;
+        }
+    }
+    if (mat == 2 && V6) {
+        const int row = id * WAVES + wave;
+        if (row >= a.rows[2]) return;
+        const float v = gemv_q8_row1<FmtQ6K>(a.w[2], (size_t)(k / 256) * Q6_K_BYTES, xq, row, k, l);
+        if (l == 0) a.v_dst[(size_t)(row / a.hd) * a.head_stride + row % a.hd] = v;
+        return;
+    }
+    const int row0 = (id * WAVES + wave) * 2;
+    if (row0 >= a.rows[mat]) return;
+    float sn = 0.0f, cs = 1.0f;
+    if (mat < 2) {
+        // (abs_pos as f32 * rope_freq_scale) * rope_inv_freq[i], as rope_qkv_kernel
+        const float angle = ((float)a.start_pos * a.freq_scale) * a.inv_freq[(row0 % a.hd) / 2];
+        sincosf(angle, &sn, &cs);
+    }
+    const float v = gemv_q4k_pair_lds(a.w[mat], a.bytes[mat], xq, row0, k / 256, l, lds[wave]);
+    const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    if (l == 0) {
+        const int h = row0 / a.hd, d0 = row0 % a.hd;
+        if (mat == 2) {
+            float* dst = a.v_dst + (size_t)h * a.head_stride + d0;
+            dst[0] = x0;
+            dst[1] = x1;
+        } else {
+            float* dst = mat == 0 ? a.q_out + (size_t)h * a.hd + d0 : a.k_dst + (size_t)h * a.head_stride + d0;
+            dst[0] = x0 * cs - x1 * sn;
+            dst[1] = x0 * sn + x1 * cs;
+        }
+    }
 }
 
 // Several projections of one activation row in one launch (the q, k and v
@@ -669,6 +765,55 @@ hipError_t gemv_group_launch(size_t n, const int* types, const void* const* W, c
         hipLaunchKernelGGL((gemv_q8_group_kernel<FmtQ4K, RA, WAVES>), dim3((unsigned)wg_a),
                            dim3(WAVES * 64), 0, s, g, x, (int)k);
     }
+    return hipGetLastError();
+}
+
+// The fused q/k/v + RoPE + append launch: Q4_K q and k (16-byte aligned),
+// Q4_K or Q6_K v, k <= 4096, every matrix within the 31-bit buffer range,
+// head_dim even (rows of a head pair up).
+bool qkv_rope_supported(const int* types, const void* const* W, size_t n_q_rows, size_t n_kv_rows, size_t k,
+                        size_t hd) {
+    if (k == 0 || k > 4096 || k % 256 || hd == 0 || hd % 2 || n_q_rows == 0 || n_kv_rows == 0) return false;
+    const size_t rows[3] = {n_q_rows, n_kv_rows, n_kv_rows};
+    for (int i = 0; i < 3; i++) {
+        const bool v6 = i == 2 && types[i] == TYPE_Q6_K;
+        if (types[i] != TYPE_Q4_K && !v6) return false;
+        const size_t bytes = rows[i] * (k / 256) * (v6 ? Q6_K_BYTES : Q4_K_BYTES);
+        if (bytes >= 0x80000000ull) return false;
+        if ((reinterpret_cast<uintptr_t>(W[i]) & (v6 ? 1 : 15)) != 0) return false;
+    }
+    return true;
+}
+
+hipError_t qkv_rope_launch(const int* types, const void* const* W, size_t n_q_rows, size_t n_kv_rows, size_t k,
+                           const void* xq, size_t hd, float* q_out, float* k_dst, float* v_dst, size_t head_stride,
+                           size_t start_pos, float freq_scale, const float* inv_freq, hipStream_t s) {
+    constexpr int WAVES = 4;
+    QkvRopeArgs a{};
+    const size_t rows[3] = {n_q_rows, n_kv_rows, n_kv_rows};
+    const bool v6 = types[2] == TYPE_Q6_K;
+    for (int i = 0; i < 3; i++) {
+        a.w[i] = static_cast<const uint8_t*>(W[i]);
+        a.rows[i] = (int)rows[i];
+        a.bytes[i] = (uint32_t)(rows[i] * (k / 256) * (i == 2 && v6 ? Q6_K_BYTES : Q4_K_BYTES));
+    }
+    a.wg_q = (int)((n_q_rows + 2 * WAVES - 1) / (2 * WAVES));
+    a.wg_k = (int)((n_kv_rows + 2 * WAVES - 1) / (2 * WAVES));
+    const int wg_v = (int)(v6 ? (n_kv_rows + WAVES - 1) / WAVES : (n_kv_rows + 2 * WAVES - 1) / (2 * WAVES));
+    a.hd = (int)hd;
+    a.q_out = q_out;
+    a.k_dst = k_dst;
+    a.v_dst = v_dst;
+    a.head_stride = head_stride;
+    a.start_pos = (long long)start_pos;
+    a.freq_scale = freq_scale;
+    a.inv_freq = inv_freq;
+    const dim3 grid((unsigned)(a.wg_q + a.wg_k + wg_v));
+    const uint8_t* x = static_cast<const uint8_t*>(xq);
+    if (v6)
+        hipLaunchKernelGGL((gemv_qkv_rope_kernel<true, WAVES>), grid, dim3(WAVES * 64), 0, s, a, x, (int)k);
+    else
+        hipLaunchKernelGGL((gemv_qkv_rope_kernel<false, WAVES>), grid, dim3(WAVES * 64), 0, s, a, x, (int)k);
     return hipGetLastError();
 }
 

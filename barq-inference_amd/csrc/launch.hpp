@@ -174,6 +174,11 @@ struct AttnArgs {
 };
 bool attention_q8_direct(const AttnArgs& a);
 bool gemv_group_supported(size_t n, const int* types, const void* const* W, const size_t* rows, size_t k);
+bool qkv_rope_supported(const int* types, const void* const* W, size_t n_q_rows, size_t n_kv_rows, size_t k,
+                        size_t hd);
+hipError_t qkv_rope_launch(const int* types, const void* const* W, size_t n_q_rows, size_t n_kv_rows, size_t k,
+                           const void* xq, size_t hd, float* q_out, float* k_dst, float* v_dst, size_t head_stride,
+                           size_t start_pos, float freq_scale, const float* inv_freq, hipStream_t s);
 hipError_t gemv_group_launch(size_t n, const int* types, const void* const* W, const size_t* rows, size_t k,
                              const void* xq, float* const* y, hipStream_t s);
 hipError_t rope_qkv_launch(int layout, const float* qx, const float* kx, const float* vx, float* q_out, float* k_out,

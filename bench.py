@@ -556,7 +556,7 @@ def bench_decode(args):
     logits = torch.empty((1, n_vocab), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     pos = [kv_len - 1]
-    qkv_types, qkv_rows = [B.Q4_K, B.Q4_K, B.Q6_K], [n_head * hd, n_kv * hd, n_kv * hd]
+    qkv_types = [B.Q4_K, B.Q4_K, B.Q6_K]
 
     def token(i):
         p0 = pos[0]
@@ -565,9 +565,8 @@ def bench_decode(args):
             L = layers[layer % copies]
             # residual stream: bufB = h + previous FFN output, bufA = bufB + attention output
             be.add_rms_norm_quantize(B.Q8_K, h, prev, norm_w, 1e-5, sum_out=bufB, out=xq, sync=False)
-            be.matvec_group_raw(qkv_types, [L["q"], L["k"], L["v"]], qkv_rows, n_embd, B.Q8_K, xq, [q, k, v],
-                                B.MEM_DEVICE)
-            kv.append_rope_q(layer, q, n_head, k, v, 1, p0, 1.0, f, A.ROPE_INTERLEAVED, q_out=qr)
+            kv.qkv_append_rope(layer, qkv_types, [L["q"], L["k"], L["v"]], n_head, n_embd, B.Q8_K, xq, p0, 1.0, f,
+                               A.ROPE_INTERLEAVED, q_out=qr)
             A.compute_attention_q8k(be, qr, kv, layer, n_head, n_kv, hd, 1, p0 + 1, p0, sync=False, out=aq)
             be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.Q8_K, aq, 1, o, B.MEM_DEVICE)
             be.add_rms_norm_quantize(B.Q8_K, bufB, o, norm_w, 1e-5, sum_out=bufA, out=xq2, sync=False)
@@ -745,7 +744,7 @@ def bench_layer(args):
     ff = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     pos = [kv_len - 1] * copies
-    qkv_types, qkv_rows = [B.Q4_K, B.Q4_K, B.Q6_K], [n_head * hd, n_kv * hd, n_kv * hd]
+    qkv_types = [B.Q4_K, B.Q4_K, B.Q6_K]
 
     qr = torch.empty((n_head, 1, hd), dtype=torch.float32, device="cuda")
     aq = torch.empty((1, (n_embd // 256) * 292), dtype=torch.uint8, device="cuda")
@@ -769,15 +768,13 @@ def bench_layer(args):
                out=ff)
 
     def step(i):
-        # fused: the q/k/v projections in one launch, RoPE of q and k with
-        # the cache append in one launch, the attention merge writing the o
-        # projection's Q8_K rows
+        # fused: the q/k/v projections with RoPE and the cache append in one
+        # launch, the attention merge writing the o projection's Q8_K rows
         c = i % copies
         L = layers[c]
         be.add_rms_norm_quantize(B.Q8_K, x, prev, norm_w, 1e-5, sum_out=res_in, out=xq, sync=False)
-        be.matvec_group_raw(qkv_types, [L["q"], L["k"], L["v"]], qkv_rows, n_embd, B.Q8_K, xq, [q, k, v],
-                            B.MEM_DEVICE)
-        kv.append_rope_q(c, q, n_head, k, v, 1, pos[c], 1.0, f, A.ROPE_INTERLEAVED, q_out=qr)
+        kv.qkv_append_rope(c, qkv_types, [L["q"], L["k"], L["v"]], n_head, n_embd, B.Q8_K, xq, pos[c], 1.0, f,
+                           A.ROPE_INTERLEAVED, q_out=qr)
         A.compute_attention_q8k(be, qr, kv, c, n_head, n_kv, hd, 1, pos[c] + 1, pos[c], sync=False, out=aq)
         pos[c] += 1
         be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.Q8_K, aq, 1, o, B.MEM_DEVICE)
@@ -808,7 +805,7 @@ def bench_layer(args):
         "us_per_step": round(ms * 1e3, 3), "us_per_step_separate_launches": round(ms_sep * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,
-                     "scope": "the whole layer step (12 launches; 15 with every reference step its own launch)"},
+                     "scope": "the whole layer step (9 launches; 15 with every reference step its own launch)"},
     }
     kv.close()
     be.close()

@@ -410,6 +410,22 @@ int barq_rocm_kv_cache_append_rope_q(barq_rocm_handle* h, barq_rocm_kv_cache* c,
                                      const float* q_proj, size_t n_head, float* q_out, const float* k_proj,
                                      const float* v_proj, size_t n_tokens, size_t start_pos, float freq_scale,
                                      const float* inv_freq, int layout, int mem);
+/* qkv_append_rope = self_attention from the normalized row to the cache for
+ * ONE token (transformer.rs:212-245): the q, k and v projections of x (one
+ * activation row of act_type; w_types[3] / w[3] are W_q [n_head * head_dim
+ * rows], W_k and W_v [n_head_kv * head_dim rows], k columns), apply_rope on
+ * q into q_out [n_head, 1, head_dim], apply_rope on k and v appended to the
+ * cache at layer `layer`.  The same bits as barq_rocm_matvec_group followed
+ * by barq_rocm_kv_cache_append_rope_q (n_tokens = 1).  On device buffers
+ * with a Q8_K row, Q4_K W_q and W_k, a Q4_K or Q6_K W_v, k <= 4096 and the
+ * interleaved layout it is one launch (each wave rotates its own rotary
+ * pair and writes the cache); otherwise those two calls run (device buffers
+ * then need act_type BARQ_TYPE_Q8_K).  An out-of-range layer appends
+ * nothing and still writes q_out. */
+int barq_rocm_qkv_append_rope(barq_rocm_handle* h, barq_rocm_kv_cache* c, size_t layer, const int* w_types,
+                              const void* const* w, size_t n_head, size_t k, int act_type, const void* x,
+                              float* q_out, size_t start_pos, float freq_scale, const float* inv_freq, int layout,
+                              int mem);
 size_t barq_rocm_kv_cache_size(const barq_rocm_kv_cache* c);
 size_t barq_rocm_kv_cache_layer_len(const barq_rocm_kv_cache* c, size_t layer);
 int barq_rocm_kv_cache_head(const barq_rocm_kv_cache* c, size_t layer, size_t head, const float** k,

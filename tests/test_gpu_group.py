@@ -90,3 +90,96 @@ def test_matvec_group_argument_errors(be):
         be.matvec_group_raw([B.Q4_K, B.Q4_K], [w, None], [4, 4], k, B.Q8_K, xq, [y, y], B.MEM_DEVICE)
     # zero matrices: nothing to do
     be.matvec_group_raw([], [], [], k, B.Q8_K, xq, [], B.MEM_DEVICE)
+
+
+# ---- the q/k/v projections + RoPE + cache append of one token -------------
+
+QKV_CASES = [
+    # (n_head, n_kv, hd, k, v_type, layout, mem)
+    (32, 8, 128, 4096, B.Q6_K, "interleaved", "device"),   # Llama-3-8B: one launch
+    (32, 8, 128, 4096, B.Q4_K, "interleaved", "device"),
+    (8, 2, 64, 512, B.Q6_K, "interleaved", "device"),
+    (6, 3, 64, 256, B.Q4_K, "interleaved", "device"),
+    (8, 2, 64, 512, B.Q6_K, "split_half", "device"),       # the two separate calls
+    (8, 2, 64, 4352, B.Q6_K, "interleaved", "device"),     # k > 4096: the two separate calls
+    (4, 2, 64, 512, B.Q6_K, "interleaved", "host"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(QKV_CASES)))
+def test_qkv_append_rope_equals_separate_calls(be, case):
+    """barq_rocm_qkv_append_rope against barq_rocm_matvec_group followed by
+    barq_rocm_kv_cache_append_rope_q on a second cache with the same prefix:
+    q_out and every cached K/V row bit for bit, two tokens in a row."""
+    import torch
+    from barq_rocm import attention as A
+    from test_gpu_attention import fill_cache, inv_freq
+    n_head, n_kv, hd, k, vt, layout, mem = QKV_CASES[case]
+    lay = A.ROPE_INTERLEAVED if layout == "interleaved" else A.ROPE_SPLIT_HALF
+    types = [B.Q4_K, B.Q4_K, vt]
+    rows = [n_head * hd, n_kv * hd, n_kv * hd]
+    print(f"qkv_append_rope n_head={n_head} n_kv={n_kv} hd={hd} k={k} v={vt} {layout} {mem}", flush=True)
+    ws = [synth.gen_weights(t, n, k, 900 + 7 * i + case) for i, (t, n) in enumerate(zip(types, rows))]
+    pos = 9
+    c_ref, _, _ = fill_cache(be, n_kv, hd, pos, 40 + case)
+    c_got, _, _ = fill_cache(be, n_kv, hd, pos, 40 + case)
+    f = inv_freq(hd)
+    for step in range(2):
+        x = synth.gen_f32(k, 70 + 3 * case + step)
+        xq = be.quantize_act(B.Q8_K, dev(x))
+        if mem == "device":
+            wd = [dev(w) for w in ws]
+            ys = [torch.empty(n, dtype=torch.float32, device="cuda") for n in rows]
+            be.matvec_group_raw(types, wd, rows, k, B.Q8_K, xq, ys, B.MEM_DEVICE)
+            q_ref = c_ref.append_rope_q(1, ys[0], n_head, ys[1], ys[2], 1, pos + step, 1.0, dev(f), lay)
+            q_got = c_got.qkv_append_rope(1, types, wd, n_head, k, B.Q8_K, xq, pos + step, 1.0, dev(f), lay)
+            be.sync()
+            q_ref, q_got = host(q_ref), host(q_got)
+        else:
+            xh = host(xq)
+            ys = [np.empty(n, np.float32) for n in rows]
+            be.matvec_group_raw(types, ws, rows, k, B.Q8_K, xh, ys, B.MEM_HOST)
+            q_ref = c_ref.append_rope_q(1, ys[0], n_head, ys[1], ys[2], 1, pos + step, 1.0, f, lay, mem=B.MEM_HOST)
+            q_got = c_got.qkv_append_rope(1, types, ws, n_head, k, B.Q8_K, xh, pos + step, 1.0, f, lay,
+                                          mem=B.MEM_HOST)
+        assert_bits_equal(np.asarray(q_got).reshape(-1), np.asarray(q_ref).reshape(-1))
+        assert c_got.layer_len(1) == c_ref.layer_len(1) == pos + step + 1
+        for hk in range(n_kv):
+            kg, vg = c_got.get_head(1, hk)
+            kr, vr = c_ref.get_head(1, hk)
+            assert_bits_equal(kg.reshape(-1), kr.reshape(-1))
+            assert_bits_equal(vg.reshape(-1), vr.reshape(-1))
+    c_ref.close()
+    c_got.close()
+
+
+def test_qkv_append_rope_edge_cases(be):
+    """An out-of-range layer appends nothing and still writes q; a full
+    layer and null buffers are errors; f32 rows on device buffers are not
+    taken."""
+    from barq_rocm import attention as A
+    from test_gpu_attention import fill_cache, inv_freq
+    n_head, n_kv, hd, k = 4, 2, 64, 256
+    types = [B.Q4_K, B.Q4_K, B.Q6_K]
+    rows = [n_head * hd, n_kv * hd, n_kv * hd]
+    wd = [dev(synth.gen_weights(t, n, k, 5 + i)) for i, (t, n) in enumerate(zip(types, rows))]
+    x = synth.gen_f32(k, 6)
+    xq = be.quantize_act(B.Q8_K, dev(x))
+    f = dev(inv_freq(hd))
+    c, _, _ = fill_cache(be, n_kv, hd, 4, 7)   # max_size 9, layers 0 and 1 hold 4 positions
+    q5 = c.qkv_append_rope(5, types, wd, n_head, k, B.Q8_K, xq, 4, 1.0, f, A.ROPE_INTERLEAVED)
+    be.sync()
+    q1 = c.qkv_append_rope(1, types, wd, n_head, k, B.Q8_K, xq, 4, 1.0, f, A.ROPE_INTERLEAVED)
+    be.sync()
+    assert_bits_equal(host(q5).reshape(-1), host(q1).reshape(-1))
+    assert c.layer_len(1) == 5 and c.layer_len(0) == 4
+    for _ in range(4):
+        c.qkv_append_rope(1, types, wd, n_head, k, B.Q8_K, xq, 5, 1.0, f, A.ROPE_INTERLEAVED)
+    assert c.layer_len(1) == 9
+    with pytest.raises(B.BarqError):   # the layer is full
+        c.qkv_append_rope(1, types, wd, n_head, k, B.Q8_K, xq, 9, 1.0, f, A.ROPE_INTERLEAVED)
+    with pytest.raises(B.BarqError):   # f32 rows on device buffers
+        c.qkv_append_rope(0, types, wd, n_head, k, B.ACT_F32, dev(x), 4, 1.0, f, A.ROPE_INTERLEAVED)
+    with pytest.raises(B.BarqError):
+        c.qkv_append_rope(0, types, [wd[0], None, wd[2]], n_head, k, B.Q8_K, xq, 4, 1.0, f, A.ROPE_INTERLEAVED)
+    c.close()
