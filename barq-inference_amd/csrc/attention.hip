@@ -193,6 +193,7 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     static_assert(LPR == 8 || LPR == 16 || LPR == 32, "head_dim 64, 128 or 256");
     __shared__ float red_o[R][G][HD];
     __shared__ float red_ml[R][G][2];
+    __shared__ float red_ms[G][2];
 
     const int t = threadIdx.x, c = t % LPR, r = t / LPR;
     const int split = blockIdx.x, grp = blockIdx.y, i = blockIdx.z, n_split = gridDim.x;
@@ -316,17 +317,29 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
         }
     }
     __syncthreads();
-    for (int e = t; e < G * HD; e += ATT_THREADS) {
-        const int g = e / HD, d = e % HD;
+    // each row state's weight exp2(m_rr - M) once per (row, head), in place
+    // of its max (then the same sums in the same order for every dim)
+    if (t < G) {
+        const int g = t;
         float M = -INFINITY;
         for (int rr = 0; rr < R; rr++) M = fmaxf(M, red_ml[rr][g][0]);
-        float L = 0.0f, O = 0.0f;
+        float L = 0.0f;
+        for (int rr = 0; rr < R; rr++) {
+            const float w = M == -INFINITY ? 0.0f : fast_exp2(red_ml[rr][g][0] - M);
+            L = __builtin_fmaf(red_ml[rr][g][1], w, L);
+            red_ml[rr][g][0] = w;
+        }
+        red_ms[g][0] = M;
+        red_ms[g][1] = L;
+    }
+    __syncthreads();
+    for (int e = t; e < G * HD; e += ATT_THREADS) {
+        const int g = e / HD, d = e % HD;
+        const float M = red_ms[g][0], L = red_ms[g][1];
+        float O = 0.0f;
         if (M != -INFINITY) {
-            for (int rr = 0; rr < R; rr++) {
-                const float w = fast_exp2(red_ml[rr][g][0] - M);
-                L = __builtin_fmaf(red_ml[rr][g][1], w, L);
-                O = __builtin_fmaf(red_o[rr][g][d], w, O);
-            }
+            #pragma unroll
+            for (int rr = 0; rr < R; rr++) O = __builtin_fmaf(red_o[rr][g][d], red_ml[rr][g][0], O);
         }
         const int h = G > 1 ? grp * G + g : grp;
         if (n_split == 1) {
