@@ -40,7 +40,7 @@ def test_q6_k_fields():
 
 
 def test_sizes_match_baseline_configs():
-    # BASELINE.md roofline table bytes
+    # packed weight bytes of the five configs' matrices (C1-C3 and C5's down projection)
     assert B.row_bytes(B.Q4_0, 4096) * 4096 == 9437184
     assert B.row_bytes(B.Q4_K, 4096) * 14336 == 33030144
     assert B.row_bytes(B.Q6_K, 4096) * 128256 == 430940160
