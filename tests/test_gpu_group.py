@@ -103,6 +103,8 @@ QKV_CASES = [
     (8, 2, 64, 512, B.Q6_K, "split_half", "device"),       # the two separate calls
     (8, 2, 64, 4352, B.Q6_K, "interleaved", "device"),     # k > 4096: the two separate calls
     (4, 2, 64, 512, B.Q6_K, "interleaved", "host"),
+    (4, 4, 256, 1024, B.Q6_K, "interleaved", "device"),       # head_dim 256, one query head per kv head
+    (16, 2, 128, 2048, B.Q4_K, "interleaved", "device"),      # GQA 8
 ]
 
 
@@ -124,6 +126,8 @@ def test_qkv_append_rope_equals_separate_calls(be, case):
     c_ref, _, _ = fill_cache(be, n_kv, hd, pos, 40 + case)
     c_got, _, _ = fill_cache(be, n_kv, hd, pos, 40 + case)
     f = inv_freq(hd)
+    # the rotation angle of the new position (large positions take sincosf's long argument reduction)
+    rope_pos = [pos, pos + 1] if case % 2 == 0 else [100000, 131071]
     for step in range(2):
         x = synth.gen_f32(k, 70 + 3 * case + step)
         xq = be.quantize_act(B.Q8_K, dev(x))
@@ -131,16 +135,17 @@ def test_qkv_append_rope_equals_separate_calls(be, case):
             wd = [dev(w) for w in ws]
             ys = [torch.empty(n, dtype=torch.float32, device="cuda") for n in rows]
             be.matvec_group_raw(types, wd, rows, k, B.Q8_K, xq, ys, B.MEM_DEVICE)
-            q_ref = c_ref.append_rope_q(1, ys[0], n_head, ys[1], ys[2], 1, pos + step, 1.0, dev(f), lay)
-            q_got = c_got.qkv_append_rope(1, types, wd, n_head, k, B.Q8_K, xq, pos + step, 1.0, dev(f), lay)
+            q_ref = c_ref.append_rope_q(1, ys[0], n_head, ys[1], ys[2], 1, rope_pos[step], 1.0, dev(f), lay)
+            q_got = c_got.qkv_append_rope(1, types, wd, n_head, k, B.Q8_K, xq, rope_pos[step], 1.0, dev(f), lay)
             be.sync()
             q_ref, q_got = host(q_ref), host(q_got)
         else:
             xh = host(xq)
             ys = [np.empty(n, np.float32) for n in rows]
             be.matvec_group_raw(types, ws, rows, k, B.Q8_K, xh, ys, B.MEM_HOST)
-            q_ref = c_ref.append_rope_q(1, ys[0], n_head, ys[1], ys[2], 1, pos + step, 1.0, f, lay, mem=B.MEM_HOST)
-            q_got = c_got.qkv_append_rope(1, types, ws, n_head, k, B.Q8_K, xh, pos + step, 1.0, f, lay,
+            q_ref = c_ref.append_rope_q(1, ys[0], n_head, ys[1], ys[2], 1, rope_pos[step], 1.0, f, lay,
+                                        mem=B.MEM_HOST)
+            q_got = c_got.qkv_append_rope(1, types, ws, n_head, k, B.Q8_K, xh, rope_pos[step], 1.0, f, lay,
                                           mem=B.MEM_HOST)
         assert_bits_equal(np.asarray(q_got).reshape(-1), np.asarray(q_ref).reshape(-1))
         assert c_got.layer_len(1) == c_ref.layer_len(1) == pos + step + 1
