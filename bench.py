@@ -503,12 +503,13 @@ def bench_ffn(args):
 def bench_decode(args):
     """One decode token of a Llama-3-8B-shaped model (LlamaTransformer::forward
     for one token: 32 x forward_layer, transformer.rs:123-144, then the output
-    norm and final_output :468-498) on the integer path, all 386 launches of
+    norm and final_output :468-498) on the integer path, all 290 launches of
     a token captured in one HIP graph.  Each layer runs the decode-layer
-    chain of --layer (12 launches) over its own KV cache of --kv-len cached
-    positions; the layers' weights rotate over three distinct copies of a
-    Q4_K_M layer (417 MB, more than the Infinity Cache holds), the LM head
-    is Q6_K 128256 x 4096.  Synthetic weights and activations."""
+    chain of --layer (9 launches) over its own KV cache of --kv-len cached
+    positions and its own copy of a Q4_K_M layer's weights (32 copies of the
+    same synthetic contents at distinct addresses, 4.4 GB: no cache holds
+    them across layers); the LM head is Q6_K 128256 x 4096.  Synthetic
+    weights and activations."""
     import numpy as np
     import torch
 
@@ -526,7 +527,7 @@ def bench_decode(args):
     host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
     head_h = synth.gen_weights(B.Q6_K, n_vocab, n_embd, 880)
     wbytes = sum(a.nbytes for a in host.values())
-    copies = 3
+    copies = n_layer
     be = B.Backend(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -592,7 +593,7 @@ def bench_decode(args):
         "value": round(1e3 / ms, 2), "unit": "tokens/s", "n_gpus": 1, "steps": tokens, "warmup": 1,
         "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
-        "config": {"workload": f"LlamaTransformer forward, 1 token, {n_layer} layers (Q4_K_M mix, 3 distinct layer copies), "
+        "config": {"workload": f"LlamaTransformer forward, 1 token, {n_layer} layers (Q4_K_M mix, one weight copy per layer), "
                                f"kv_len {kv_len}, LM head Q6_K {n_vocab} x {n_embd}", "timing": method},
         "ms_per_token": round(ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
