@@ -4,7 +4,7 @@
 Headline (BASELINE.json metric): Q4_K x Q8_K batch-1 GEMV at the Llama-3-8B
 FFN up/gate shape (config 2: 14336 x 4096), achieved HBM GB/s against the
 8 TB/s peak and us/call.  A step is one GEMV call.  Weights rotate over
-enough distinct copies (> 300 MB) that the 256 MB Infinity Cache cannot
+enough distinct copies (>= 1 GiB) that the 256 MB Infinity Cache cannot
 hold them, activations are quantized once beforehand (their kernel is timed
 on its own line) and all inputs are resident in HBM before timing starts.
 
@@ -47,7 +47,7 @@ def parse():
     p.add_argument("--config", type=int, default=2, help="BASELINE.json config: 1-4 linear, 5 MoE")
     p.add_argument("--w-type", default=None, choices=["Q4_0", "Q8_0", "Q4_0_BARQ", "Q4_K", "Q6_K"],
                    help="configs 1-4: another weight format at the same shape (e.g. --config 4 --w-type Q4_0)")
-    p.add_argument("--copies", type=int, default=0, help="distinct weight copies (default: >= 320 MB)")
+    p.add_argument("--copies", type=int, default=0, help="distinct weight copies (default: >= 1 GiB of them)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
@@ -114,6 +114,12 @@ def time_launches(launch, K, eager):
     t1.synchronize()
     return t0.elapsed_time(t1) / K, "eager"
 
+
+# Timed calls rotate over distinct copies of their weights (and KV caches)
+# totalling at least this many bytes.  The 256 MB Infinity Cache must not
+# serve them: with 363 MB of C2 copies the GEMV measured ~1.7 % faster than
+# with 1-2 GB, and a decode layer ~4.5 % faster with 2 copies than with 6.
+ROTATE_BYTES = 1 << 30
 
 # dominant kernel of each config (config 5: every kernel of the MoE step)
 # (Q4_K GEMVs with k <= 4096 run the LDS-staged kernel unless BARQ_GEMV_LDS=0)
@@ -423,7 +429,7 @@ def bench_ffn(args):
     fused RMSNorm -> Q8_K of the layer writes them).  One token runs gate and
     up in one launch with the SwiGLU in its epilogue; beside it the same work
     as two separate GEMVs and the SwiGLU quantizer.  Layers rotate over
-    enough weight copies (> 320 MB) that the Infinity Cache cannot hold them."""
+    enough weight copies (>= 1 GiB) that the Infinity Cache cannot hold them."""
     import numpy as np
     import torch
 
@@ -437,7 +443,7 @@ def bench_ffn(args):
     down = synth.gen_q6_k(n_embd, n_ff, synth.sub_seed(s0, 42))
     x = synth.gen_f32(m * n_embd, synth.sub_seed(s0, 43)).reshape(m, n_embd)
     wbytes = gate.nbytes + up.nbytes + down.nbytes
-    copies = args.copies or max(2, -(-320 * 2 ** 20 // wbytes))
+    copies = args.copies or max(2, -(-ROTATE_BYTES // wbytes))
     be = B.Backend(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -613,7 +619,7 @@ def bench_prefill(args):
     RoPE of q and k with the cache append, causal attention (f32 MFMA) with
     its rows quantized for the o GEMM, residual add + ffn_norm -> Q8_K, the
     dense FFN (gate/up GEMMs, SwiGLU -> Q8_K, down GEMM).  Steps rotate over
-    layer copies of >= 320 MB.  Throughput: prompt tokens per second through
+    layer copies of >= 1 GiB.  Throughput: prompt tokens per second through
     one layer; the op count is 2 M N K over the seven projections plus the
     attention's 4 hd per visible (query, position) pair and head."""
     import numpy as np
@@ -630,7 +636,7 @@ def bench_prefill(args):
             ("down", B.Q6_K, n_embd, n_ff)]
     host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
     wbytes = sum(a.nbytes for a in host.values())
-    copies = args.copies or max(2, -(-320 * 2 ** 20 // wbytes))
+    copies = args.copies or max(2, -(-ROTATE_BYTES // wbytes))
     be = B.Backend(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -719,7 +725,7 @@ def bench_layer(args):
     host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
     wbytes = sum(a.nbytes for a in host.values())
     kv_bytes = 2 * n_kv * kv_len * hd * 4
-    copies = args.copies or max(2, -(-320 * 2 ** 20 // (wbytes + kv_bytes)))
+    copies = args.copies or max(2, -(-ROTATE_BYTES // (wbytes + kv_bytes)))
     be = B.Backend(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -821,7 +827,7 @@ def bench_attn(args):
     Llama-3-8B head layout: 32 query heads, 8 kv heads, head_dim 128, one new
     token against kv_len cached positions in f32.  HBM-bound: every call
     reads the layer's K and V rows once (2 * 8 * kv_len * 128 * 4 bytes).
-    Calls rotate over enough cache layers (> 320 MB) that the Infinity Cache
+    Calls rotate over enough cache layers (>= 1 GiB) that the Infinity Cache
     cannot hold them.  The CPU leg times the oracle's restatement of
     compute_attention (one core) on a bounded number of calls."""
     import numpy as np
@@ -837,7 +843,7 @@ def bench_attn(args):
     n_head, n_kv, hd, kv, ql = 32, 8, 128, args.kv_len, args.q_len
     assert 1 <= ql <= kv
     layer_bytes = 2 * n_kv * kv * hd * 4
-    layers = max(2, -(-320 * 2**20 // layer_bytes))
+    layers = max(2, -(-ROTATE_BYTES // layer_bytes))
     log(f"attention: {n_head} heads / {n_kv} kv heads x {hd}, kv_len {kv}, {layers} cache layers "
         f"({layers * layer_bytes / 2**20:.0f} MiB)")
     cache = A.KVCache(be, kv, layers, n_kv, hd)
@@ -955,7 +961,7 @@ def main():
                     + (f"batch 1, x->{act_name}" if m == 1 else f"M={m}, X->{act_name}"))
     at = B.Q8_PARTNER[w_type]
     wbytes = w.nbytes
-    copies = args.copies or max(2, -(-320 * 2 ** 20 // wbytes))
+    copies = args.copies or max(2, -(-ROTATE_BYTES // wbytes))
     be = B.Backend(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
