@@ -107,20 +107,62 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
 // against 7.29 us; the bare staging reaches the streaming-read floor.
 constexpr int Q4K_LDS_BUF = 5 * 1024;   // per wave: 4608 bytes rounded up to whole 1 KB load instructions
 
-// w_bytes: bytes of the whole matrix (the buffer descriptor's range: rows
-// past the end read as zeros).  Returns the two rows' results, row0's in
-// lane 0 and row0 + 1's in lane 32.
-__device__ __forceinline__ float gemv_q4k_pair_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
-                                                   const uint8_t* __restrict__ xq, int row0, int nblk, int l,
-                                                   uint8_t* buf) {
-    using F = FmtQ4K;
-    constexpr int R = 2;
-    const F::Lane c = F::lane(l);
-    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = R * rb;
+// The lane's Q8_K activation slice for the LDS-staged Q4_K rows (FmtQ4K's
+// lane slicing), loaded by inline-asm global loads.  The compiler counts
+// only the loads it emits itself, so with the buffer->LDS copies (also
+// inline asm) issued after these it would wait for everything (vmcnt(0))
+// before its first use of an activation register; loaded by asm, nothing
+// waits until gemv_q4k_pair_finish's explicit waits, which can then let row
+// 0's arithmetic run while row 1's copies are still in flight.  No code
+// reads these registers before q4k_x_ready (checked in the built ISA: the
+// registers are read first after the wait).
+typedef int i32x2v __attribute__((ext_vector_type(2)));
+struct Q4KXRaw {
+    i32x4v v[4];
+    i32x2v bs;
+    int dx;
+};
+
+__device__ __forceinline__ void q4k_x_issue(Q4KXRaw& r, const uint8_t* __restrict__ xq, int blk, int p) {
+    const uint8_t* b = xq + (size_t)blk * 292;
+    const uint8_t* bq = b + 64 * p;   // quants of this lane at +4 + 64 p + 16 i
+    const uint8_t* bs = b + 8 * p;    // its two bsum pairs at +260 + 8 p
+    asm volatile("global_load_dword %0, %1, off" : "=v"(r.dx) : "v"(b));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:4" : "=v"(r.v[0]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:20" : "=v"(r.v[1]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:36" : "=v"(r.v[2]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:52" : "=v"(r.v[3]) : "v"(bq));
+    asm volatile("global_load_dwordx2 %0, %1, off offset:260" : "=v"(r.bs) : "v"(bs));
+}
+
+// After the wait for q4k_x_issue's loads: FmtQ4K::load_x's values.
+__device__ __forceinline__ void q4k_x_ready(Q4KXRaw& r, FmtQ4K::X& x) {
+    asm volatile("" : "+v"(r.v[0]), "+v"(r.v[1]), "+v"(r.v[2]), "+v"(r.v[3]), "+v"(r.bs), "+v"(r.dx));
+    #pragma unroll
+    for (int i = 0; i < 4; i++)
+        x.v[i] = make_uint4((uint32_t)r.v[i].x, (uint32_t)r.v[i].y, (uint32_t)r.v[i].z, (uint32_t)r.v[i].w);
+    x.dx = __builtin_bit_cast(float, r.dx);
+    const uint32_t b0 = (uint32_t)r.bs.x, b1 = (uint32_t)r.bs.y;
+    x.sa = sext16(b0, 0) + sext16(b0, 16);
+    x.sb = sext16(b1, 0) + sext16(b1, 16);
+}
+
+// The lane's activation slice and the wave's buffer->LDS copies of rows
+// row0 and row0 + 1 (2 * 144 * nblk contiguous bytes, in 1 KB instructions),
+// issued in that order with nothing waiting in between: the activation is an
+// L2 hit that lands ahead of the rows (loads return in order), and the
+// copies start without waiting for it.  Issued after the copies instead, the
+// activation's latency came after the rows' in every wave (C2 7.8 against
+// 7.3 us); waited for before the copies, it delays each wave's stream by an
+// L2 round trip (7.3 against 7.1 us).  w_bytes: bytes of the whole matrix
+// (the buffer descriptor's range: rows past the end read as zeros).
+__device__ __forceinline__ void gemv_q4k_pair_issue(const uint8_t* __restrict__ W, uint32_t w_bytes,
+                                                    const uint8_t* __restrict__ xq, int row0, int nblk, int l,
+                                                    uint8_t* buf, Q4KXRaw& xr) {
+    // every lane loads (lanes past the last block re-read it and ignore it)
+    q4k_x_issue(xr, xq, min(l >> 2, nblk - 1), l & 3);
+    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = 2 * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
-    const bool act = F::active(0, c, nblk);
-    F::X xs;
-    if (act) F::load_x(xs, xq, 0, c, nblk);
     const uint32_t base = (uint32_t)row0 * rb;
     #pragma unroll
     for (int q = 0; q < Q4K_LDS_BUF / 1024; q++) {
@@ -129,23 +171,54 @@ __device__ __forceinline__ float gemv_q4k_pair_lds(const uint8_t* __restrict__ W
             lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
         }
     }
+}
+
+// Waits for gemv_q4k_pair_issue's loads and returns the two rows' results,
+// row0's in lane 0 and row0 + 1's in lane 32.  Row 0's arithmetic starts
+// once its copies have landed (loads complete in order; 0-2 copies of row 1
+// may still be in flight), so only row 1's is left after the last byte.
+__device__ __forceinline__ float gemv_q4k_pair_finish(int nblk, int l, const uint8_t* buf, Q4KXRaw& xr) {
+    using F = FmtQ4K;
+    const F::Lane c = F::lane(l);
+    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES;
+    const bool act = F::active(0, c, nblk);
+    // copies issued after the last one row 0 needs
+    const uint32_t later = (2 * rb + 1023) / 1024 - (rb + 1023) / 1024;
+    if (later >= 2) wait_vmcnt<2>();
+    else if (later == 1) wait_vmcnt<1>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    F::X xs;
+    q4k_x_ready(xr, xs);
+    float acc0 = 0.0f, acc1 = 0.0f;
+    const uint8_t* b = buf + Q4_K_BYTES * c.sbl;
+    if (act) {
+        F::Wt w;
+        w.hdr = *reinterpret_cast<const uint4*>(b);
+        w.q0 = *reinterpret_cast<const uint4*>(b + 16 + 32 * c.p);
+        w.q1 = *reinterpret_cast<const uint4*>(b + 32 + 32 * c.p);
+        acc0 = F::dot(w, xs, c);
+    }
     wait_vmcnt<0>();
     asm volatile("" ::: "memory");
-    float acc[R] = {0.0f, 0.0f};
     if (act) {
-        F::Wt w[R];
-        #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint8_t* b = buf + r * rb + Q4_K_BYTES * c.sbl;
-            w[r].hdr = *reinterpret_cast<const uint4*>(b);
-            w[r].q0 = *reinterpret_cast<const uint4*>(b + 16 + 32 * c.p);
-            w[r].q1 = *reinterpret_cast<const uint4*>(b + 32 + 32 * c.p);
-        }
-        #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = F::dot(w[r], xs, c);
+        F::Wt w;
+        w.hdr = *reinterpret_cast<const uint4*>(b + rb);
+        w.q0 = *reinterpret_cast<const uint4*>(b + rb + 16 + 32 * c.p);
+        w.q1 = *reinterpret_cast<const uint4*>(b + rb + 32 + 32 * c.p);
+        acc1 = F::dot(w, xs, c);
     }
     // row r's total is in lane row_lane4(r): 0 and 32
-    return reduce4(acc[0], acc[1], 0.0f, 0.0f);
+    return reduce4(acc0, acc1, 0.0f, 0.0f);
+}
+
+__device__ __forceinline__ float gemv_q4k_pair_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
+                                                   const uint8_t* __restrict__ xq, int row0, int nblk, int l,
+                                                   uint8_t* buf) {
+    Q4KXRaw xr;
+    gemv_q4k_pair_issue(W, w_bytes, xq, row0, nblk, l, buf, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    return gemv_q4k_pair_finish(nblk, l, buf, xr);
 }
 
 __device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
@@ -236,13 +309,22 @@ void gemv_qkv_rope_kernel(QkvRopeArgs a, const uint8_t* __restrict__ xq, int k) 
     }
     const int row0 = (id * WAVES + wave) * 2;
     if (row0 >= a.rows[mat]) return;
+    Q4KXRaw xr;
+    gemv_q4k_pair_issue(a.w[mat], a.bytes[mat], xq, row0, k / 256, l, lds[wave], xr);
+    __builtin_amdgcn_sched_barrier(0);
     float sn = 0.0f, cs = 1.0f;
     if (mat < 2) {
-        // (abs_pos as f32 * rope_freq_scale) * rope_inv_freq[i], as rope_qkv_kernel
-        const float angle = ((float)a.start_pos * a.freq_scale) * a.inv_freq[(row0 % a.hd) / 2];
+        // (abs_pos as f32 * rope_freq_scale) * rope_inv_freq[i], as rope_qkv_kernel.
+        // The frequency is a scalar load (lgkmcnt): a vector load's wait
+        // would also wait for the row copies in flight.
+        const int i = __builtin_amdgcn_readfirstlane((row0 % a.hd) / 2);
+        const float f = *reinterpret_cast<const __attribute__((address_space(4))) float*>(
+            reinterpret_cast<uintptr_t>(a.inv_freq + i));
+        const float angle = ((float)a.start_pos * a.freq_scale) * f;
         sincosf(angle, &sn, &cs);
     }
-    const float v = gemv_q4k_pair_lds(a.w[mat], a.bytes[mat], xq, row0, k / 256, l, lds[wave]);
+    __builtin_amdgcn_sched_barrier(0);
+    const float v = gemv_q4k_pair_finish(k / 256, l, lds[wave], xr);
     const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
     const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     if (l == 0) {
