@@ -105,14 +105,32 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
 // reduction: outputs are bit-identical to gemv_q8_rows<FmtQ4K, 2, true>.
 // Measured at C2 (14336 x 4096, one box, 11 rotating weight copies): 7.14
 // against 7.29 us; the bare staging reaches the streaming-read floor.
-constexpr int Q4K_LDS_BUF = 5 * 1024;   // per wave: 4608 bytes rounded up to whole 1 KB load instructions
+// per wave: R rows of 2304 bytes (k = 4096) rounded up to whole 1 KB load instructions
+template <int R>
+constexpr int q4k_lds_buf = (R * 16 * Q4_K_BYTES + 1023) / 1024 * 1024;
+constexpr int Q4K_LDS_BUF = q4k_lds_buf<2>;
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 8]
+__device__ __forceinline__ void wait_vmcnt_upto8(uint32_t n) {
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    default: wait_vmcnt<8>(); break;
+    }
+}
 
 // The lane's Q8_K activation slice for the LDS-staged Q4_K rows (FmtQ4K's
 // lane slicing), loaded by inline-asm global loads.  The compiler counts
 // only the loads it emits itself, so with the buffer->LDS copies (also
 // inline asm) issued after these it would wait for everything (vmcnt(0))
 // before its first use of an activation register; loaded by asm, nothing
-// waits until gemv_q4k_pair_finish's explicit waits, which can then let row
+// waits until gemv_q4k_rows_finish's explicit waits, which can then let row
 // 0's arithmetic run while row 1's copies are still in flight.  No code
 // reads these registers before q4k_x_ready (checked in the built ISA: the
 // registers are read first after the wait).
@@ -148,24 +166,26 @@ __device__ __forceinline__ void q4k_x_ready(Q4KXRaw& r, FmtQ4K::X& x) {
 }
 
 // The lane's activation slice and the wave's buffer->LDS copies of rows
-// row0 and row0 + 1 (2 * 144 * nblk contiguous bytes, in 1 KB instructions),
-// issued in that order with nothing waiting in between: the activation is an
-// L2 hit that lands ahead of the rows (loads return in order), and the
-// copies start without waiting for it.  Issued after the copies instead, the
-// activation's latency came after the rows' in every wave (C2 7.8 against
-// 7.3 us); waited for before the copies, it delays each wave's stream by an
-// L2 round trip (7.3 against 7.1 us).  w_bytes: bytes of the whole matrix
-// (the buffer descriptor's range: rows past the end read as zeros).
-__device__ __forceinline__ void gemv_q4k_pair_issue(const uint8_t* __restrict__ W, uint32_t w_bytes,
+// row0 .. row0 + R - 1 (R * 144 * nblk contiguous bytes, in 1 KB
+// instructions), issued in that order with nothing waiting in between: the
+// activation is an L2 hit that lands ahead of the rows (loads return in
+// order), and the copies start without waiting for it.  Issued after the
+// copies instead, the activation's latency came after the rows' in every
+// wave (C2 7.8 against 7.3 us); waited for before the copies, it delays each
+// wave's stream by an L2 round trip (7.3 against 7.1 us).  w_bytes: bytes of
+// the whole matrix (the buffer descriptor's range: rows past the end read as
+// zeros).
+template <int R>
+__device__ __forceinline__ void gemv_q4k_rows_issue(const uint8_t* __restrict__ W, uint32_t w_bytes,
                                                     const uint8_t* __restrict__ xq, int row0, int nblk, int l,
                                                     uint8_t* buf, Q4KXRaw& xr) {
     // every lane loads (lanes past the last block re-read it and ignore it)
     q4k_x_issue(xr, xq, min(l >> 2, nblk - 1), l & 3);
-    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = 2 * rb;
+    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = R * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
     #pragma unroll
-    for (int q = 0; q < Q4K_LDS_BUF / 1024; q++) {
+    for (int q = 0; q < q4k_lds_buf<R> / 1024; q++) {
         if (1024u * q < span) {
             const uint32_t off = 1024u * q + 16u * (uint32_t)l;
             lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
@@ -173,52 +193,46 @@ __device__ __forceinline__ void gemv_q4k_pair_issue(const uint8_t* __restrict__ 
     }
 }
 
-// Waits for gemv_q4k_pair_issue's loads and returns the two rows' results,
-// row0's in lane 0 and row0 + 1's in lane 32.  Row 0's arithmetic starts
-// once its copies have landed (loads complete in order; 0-2 copies of row 1
-// may still be in flight), so only row 1's is left after the last byte.
-__device__ __forceinline__ float gemv_q4k_pair_finish(int nblk, int l, const uint8_t* buf, Q4KXRaw& xr) {
+// Waits for gemv_q4k_rows_issue's loads and returns the R rows' results in
+// lanes 0, 32, 16, 48 (reduce4's order).  Row r's arithmetic starts once its
+// copies have landed (loads complete in order; the later rows' copies may
+// still be in flight), so only the last row's is left after the last byte.
+template <int R>
+__device__ __forceinline__ float gemv_q4k_rows_finish(int nblk, int l, const uint8_t* buf, Q4KXRaw& xr) {
+    static_assert(R == 2 || R == 4, "two or four rows per wave");
     using F = FmtQ4K;
     const F::Lane c = F::lane(l);
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES;
+    const uint32_t n_all = (R * rb + 1023) / 1024;   // copies issued
     const bool act = F::active(0, c, nblk);
-    // copies issued after the last one row 0 needs
-    const uint32_t later = (2 * rb + 1023) / 1024 - (rb + 1023) / 1024;
-    if (later >= 2) wait_vmcnt<2>();
-    else if (later == 1) wait_vmcnt<1>();
-    else wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    F::X xs;
-    q4k_x_ready(xr, xs);
-    float acc0 = 0.0f, acc1 = 0.0f;
     const uint8_t* b = buf + Q4_K_BYTES * c.sbl;
-    if (act) {
-        F::Wt w;
-        w.hdr = *reinterpret_cast<const uint4*>(b);
-        w.q0 = *reinterpret_cast<const uint4*>(b + 16 + 32 * c.p);
-        w.q1 = *reinterpret_cast<const uint4*>(b + 32 + 32 * c.p);
-        acc0 = F::dot(w, xs, c);
+    F::X xs;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+    for (int r = 0; r < R; r++) {
+        // copies issued after the last one row r needs
+        wait_vmcnt_upto8(n_all - (rb * (r + 1) + 1023) / 1024);
+        asm volatile("" ::: "memory");
+        if (r == 0) q4k_x_ready(xr, xs);
+        if (act) {
+            F::Wt w;
+            w.hdr = *reinterpret_cast<const uint4*>(b + r * rb);
+            w.q0 = *reinterpret_cast<const uint4*>(b + r * rb + 16 + 32 * c.p);
+            w.q1 = *reinterpret_cast<const uint4*>(b + r * rb + 32 + 32 * c.p);
+            acc[r] = F::dot(w, xs, c);
+        }
     }
-    wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    if (act) {
-        F::Wt w;
-        w.hdr = *reinterpret_cast<const uint4*>(b + rb);
-        w.q0 = *reinterpret_cast<const uint4*>(b + rb + 16 + 32 * c.p);
-        w.q1 = *reinterpret_cast<const uint4*>(b + rb + 32 + 32 * c.p);
-        acc1 = F::dot(w, xs, c);
-    }
-    // row r's total is in lane row_lane4(r): 0 and 32
-    return reduce4(acc0, acc1, 0.0f, 0.0f);
+    return reduce4(acc[0], acc[1], acc[2], acc[3]);
 }
 
+// Two rows (row0's result in lane 0, row0 + 1's in lane 32)
 __device__ __forceinline__ float gemv_q4k_pair_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
                                                    const uint8_t* __restrict__ xq, int row0, int nblk, int l,
                                                    uint8_t* buf) {
     Q4KXRaw xr;
-    gemv_q4k_pair_issue(W, w_bytes, xq, row0, nblk, l, buf, xr);
+    gemv_q4k_rows_issue<2>(W, w_bytes, xq, row0, nblk, l, buf, xr);
     __builtin_amdgcn_sched_barrier(0);
-    return gemv_q4k_pair_finish(nblk, l, buf, xr);
+    return gemv_q4k_rows_finish<2>(nblk, l, buf, xr);
 }
 
 __device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W, uint32_t w_bytes,
@@ -231,16 +245,23 @@ __device__ __forceinline__ void gemv_q4k_rows_lds(const uint8_t* __restrict__ W,
     }
 }
 
-template <int WAVES>
+template <int WAVES, int R>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_q4k_lds_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
                          float* __restrict__ y, int n_rows, int nblk) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][Q4K_LDS_BUF];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][q4k_lds_buf<R>];
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row0 = (wg_rows_remap<2 * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * 2;
+    const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
     if (row0 >= n_rows) return;
-    gemv_q4k_rows_lds(W, w_bytes, xq, y, row0, n_rows, nblk, l, lds[wave]);
+    Q4KXRaw xr;
+    gemv_q4k_rows_issue<R>(W, w_bytes, xq, row0, nblk, l, lds[wave], xr);
+    __builtin_amdgcn_sched_barrier(0);
+    const float v = gemv_q4k_rows_finish<R>(nblk, l, lds[wave], xr);
+    if ((l & 15) == 0) {
+        const int rr = l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3;
+        if (rr < R && row0 + rr < n_rows) y[row0 + rr] = v;
+    }
 }
 
 // One row of W by this wave with the single-chunk lane slicing (k <= 4096):
@@ -310,7 +331,7 @@ void gemv_qkv_rope_kernel(QkvRopeArgs a, const uint8_t* __restrict__ xq, int k) 
     const int row0 = (id * WAVES + wave) * 2;
     if (row0 >= a.rows[mat]) return;
     Q4KXRaw xr;
-    gemv_q4k_pair_issue(a.w[mat], a.bytes[mat], xq, row0, k / 256, l, lds[wave], xr);
+    gemv_q4k_rows_issue<2>(a.w[mat], a.bytes[mat], xq, row0, k / 256, l, lds[wave], xr);
     __builtin_amdgcn_sched_barrier(0);
     float sn = 0.0f, cs = 1.0f;
     if (mat < 2) {
@@ -324,7 +345,7 @@ void gemv_qkv_rope_kernel(QkvRopeArgs a, const uint8_t* __restrict__ xq, int k) 
         sincosf(angle, &sn, &cs);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const float v = gemv_q4k_pair_finish(k / 256, l, lds[wave], xr);
+    const float v = gemv_q4k_rows_finish<2>(k / 256, l, lds[wave], xr);
     const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
     const float x1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     if (l == 0) {
@@ -787,9 +808,16 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
     case TYPE_Q4_K:
         if (q4k_lds_supported(W, n_rows, k) && tuning_env(TUNE_GEMV_LDS, 1) && !env_cfg().r) {
             constexpr int WAVES = 4;
-            const unsigned grid = (unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES));
-            hipLaunchKernelGGL((gemv_q4k_lds_kernel<WAVES>), dim3(grid), dim3(WAVES * 64), 0, s, w,
-                               (uint32_t)(n_rows * (k / 256 * Q4_K_BYTES)), x, y, n, (int)(k / 256));
+            const uint32_t bytes = (uint32_t)(n_rows * (k / 256 * Q4_K_BYTES));
+            if (tuning_env(TUNE_GEMV_LDS, 1) == 4) {
+                const unsigned grid = (unsigned)((n_rows + 4 * WAVES - 1) / (4 * WAVES));
+                hipLaunchKernelGGL((gemv_q4k_lds_kernel<WAVES, 4>), dim3(grid), dim3(WAVES * 64), 0, s, w, bytes, x,
+                                   y, n, (int)(k / 256));
+            } else {
+                const unsigned grid = (unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES));
+                hipLaunchKernelGGL((gemv_q4k_lds_kernel<WAVES, 2>), dim3(grid), dim3(WAVES * 64), 0, s, w, bytes, x,
+                                   y, n, (int)(k / 256));
+            }
             return hipGetLastError();
         }
         return dispatch_q8<FmtQ4K>(w, k / 256 * 144, x, y, n, kk, s, kk <= 4096 ? GemvCfg{2, 4} : GemvCfg{2, 2});

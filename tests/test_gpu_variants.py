@@ -182,18 +182,24 @@ def test_gemv_variants(be, orc, w_type):
 
 def test_gemv_q4k_lds_equals_register_gemv(be, orc):
     """The LDS-staged Q4_K GEMV (k <= 4096, the default there) against the
-    register GEMV (BARQ_GEMV_LDS=0): bit-identical outputs (same lane slices,
-    arithmetic and reduction), both within the bar of the oracle.  Odd row
-    counts leave the last wave one row; short k leaves lanes idle."""
+    register GEMV (BARQ_GEMV_LDS=0), with two and four rows per wave
+    (BARQ_GEMV_LDS=4): bit-identical outputs (same lane slices, arithmetic
+    and reduction), all within the bar of the oracle.  Row counts that are
+    not a multiple of the rows per wave leave the last wave short; short k
+    leaves lanes idle and changes how many copies each row's wait skips."""
     from conftest import assert_bits_equal
-    for n, k in [(1, 256), (5, 512), (67, 4096), (129, 3840), (1023, 768), (14336, 4096)]:
+    for n, k in [(1, 256), (5, 512), (67, 4096), (129, 3840), (1023, 768), (14336, 4096), (3, 4096), (30, 2304)]:
         print("q4k lds gemv", n, k, flush=True)
         w, xq, ref = matmul_case(orc, B.Q4_K, n, k, 1, 1300 + n + k)
         wd, xd = dev(w), dev(xq)
         got = be.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
         with env(BARQ_GEMV_LDS=0) as b:
             reg = b.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
+        # four rows per wave: the same per-row arithmetic and reduction
+        with env(BARQ_GEMV_LDS=4) as b:
+            quad = b.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
         assert_bits_equal(got, reg)
+        assert_bits_equal(quad, reg)
         assert_close_1e3(got, ref.ravel())
 
 
