@@ -383,6 +383,9 @@ MOE_CASES = {
     # through one pipeline: gate/up 8 x 2 x 64 tiles; down 24 x 32 tiles
     "multi_tile_gate_up": dict(ne=8, hid=512, nff=8192, rows=16, k=2),
     "multi_tile_down": dict(ne=24, hid=4096, nff=512, rows=24, k=2),
+    # five super-blocks per row (an odd count for the Q4_K tiles), experts
+    # of up to ~40 rows
+    "nsb5": dict(ne=5, hid=1280, nff=512, rows=70, k=2),
     # grouping fused with the gather-quantize over several 256-assignment
     # chunks (with skipped ids)
     "many_chunks": dict(ne=6, hid=256, nff=256, rows=700, k=2),
