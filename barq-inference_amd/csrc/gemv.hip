@@ -131,9 +131,9 @@ __device__ __forceinline__ void wait_vmcnt_upto8(uint32_t n) {
 // inline asm) issued after these it would wait for everything (vmcnt(0))
 // before its first use of an activation register; loaded by asm, nothing
 // waits until gemv_q4k_rows_finish's explicit waits, which can then let row
-// 0's arithmetic run while row 1's copies are still in flight.  No code
-// reads these registers before q4k_x_ready (checked in the built ISA: the
-// registers are read first after the wait).
+// 0's arithmetic run while row 1's copies are still in flight.  No code may
+// read or write these registers before that wait: the build checks the
+// device assembly for it (isa_check_asm_loads.py).
 typedef int i32x2v __attribute__((ext_vector_type(2)));
 struct Q4KXRaw {
     i32x4v v[4];
