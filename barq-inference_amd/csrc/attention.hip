@@ -358,7 +358,13 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
 constexpr int ATT_MAX_SPLIT = 1024;
 
 // One output head: out value of dim t (t < HD) from the n_split partial
-// states at pp; every thread of the 1024 calls it (it synchronises).
+// states at pp, by NT threads t = 0 .. NT - 1 (all of them call it: it
+// synchronises the workgroup).  The split maxima and weights are spread over
+// the threads; the output sums run over SUB = 1024 / HD subsets of the splits
+// (split s in subset s % SUB, in increasing order), then are added in LDS in
+// subset order.  With NT < 1024 each thread runs 1024 / NT subsets one after
+// another, so the sums and their order do not depend on NT: the Q8_K merge
+// (heads side by side) quantizes exactly the f32 merge's values.
 template <int HD>
 struct CombineLds {
     float w[ATT_MAX_SPLIT];
@@ -366,18 +372,22 @@ struct CombineLds {
     float wred[2][1024 / 64];
 };
 
-template <int HD>
-__device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp, int n_split, CombineLds<HD>& sm) {
-    constexpr int NT = 1024, NWV = NT / 64, SUB = NT / HD, PRE = 8;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int sub = t / HD, d = t % HD;
+template <int HD, int NT>
+__device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp, int n_split, CombineLds<HD>& sm,
+                                                   int t) {
+    constexpr int NWV = NT / 64, SUB = 1024 / HD, K = 1024 / NT, STEP = NT / HD, PRE = 8;
+    static_assert(NT % HD == 0 && 1024 % NT == 0, "threads per head");
+    const int lane = t & 63, wave = t >> 6;
+    const int sub = t / HD, d = t % HD;   // subsets sub + STEP j, j < K
     // every load of the first PRE rounds is issued before any reduction
-    float ov[PRE];
+    float ov[K][PRE];
     #pragma unroll
-    for (int u = 0; u < PRE; u++) {
-        const int s = sub + SUB * u;
-        ov[u] = s < n_split ? pp[(size_t)s * (HD + 2) + 2 + d] : 0.0f;
-    }
+    for (int j = 0; j < K; j++)
+        #pragma unroll
+        for (int u = 0; u < PRE; u++) {
+            const int s = sub + STEP * j + SUB * u;
+            ov[j][u] = s < n_split ? pp[(size_t)s * (HD + 2) + 2 + d] : 0.0f;
+        }
     float M = -INFINITY, Ls = 0.0f, Ms = -INFINITY;
     if (t < n_split) {
         Ms = pp[(size_t)t * (HD + 2)];
@@ -406,14 +416,18 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
     L = sm.wred[1][0];
     #pragma unroll
     for (int u = 1; u < NWV; u++) L += sm.wred[1][u];
-    float O = 0.0f;
     #pragma unroll
-    for (int u = 0; u < PRE; u++) {
-        const int s = sub + SUB * u;
-        if (s < n_split) O = __builtin_fmaf(ov[u], sm.w[s], O);
+    for (int j = 0; j < K; j++) {
+        const int sj = sub + STEP * j;
+        float O = 0.0f;
+        #pragma unroll
+        for (int u = 0; u < PRE; u++) {
+            const int s = sj + SUB * u;
+            if (s < n_split) O = __builtin_fmaf(ov[j][u], sm.w[s], O);
+        }
+        for (int s = sj + SUB * PRE; s < n_split; s += SUB) O = __builtin_fmaf(pp[(size_t)s * (HD + 2) + 2 + d], sm.w[s], O);
+        sm.red[sj][d] = O;
     }
-    for (int s = sub + SUB * PRE; s < n_split; s += SUB) O = __builtin_fmaf(pp[(size_t)s * (HD + 2) + 2 + d], sm.w[s], O);
-    sm.red[sub][d] = O;
     __syncthreads();
     float acc = 0.0f;
     if (t < HD) {
@@ -425,37 +439,33 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
     return acc;
 }
 
-// out[i, h, :] from the n_split partial states of (i, h): one workgroup per
-// (h, i).  The split maxima and weights are spread over the 1024 threads;
-// the output sums over 1024 / HD thread subsets of the splits, then added in
-// LDS.
+// out[i, h, :] from the n_split partial states of (i, h): one workgroup of
+// 1024 threads per (h, i).
 template <int HD>
 __global__ __launch_bounds__(1024)
 void attn_combine_kernel(const float* __restrict__ part, int n_split, int n_head, float* __restrict__ out) {
     __shared__ CombineLds<HD> sm;
     const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
-    const float v = attn_combine_head<HD>(part + ((size_t)i * n_head + h) * n_split * (HD + 2), n_split, sm);
+    const float v = attn_combine_head<HD, 1024>(part + ((size_t)i * n_head + h) * n_split * (HD + 2), n_split, sm, t);
     if (t < HD) out[((size_t)i * n_head + h) * HD + t] = v;
 }
 
 // The same merge with the output row written as Q8_K blocks (the o
 // projection's activation): workgroup (b, i) merges the 256 / HD heads of
-// block b of row i one after another, then one wave quantizes the block
-// (q8_k_block: the bytes quantize_q8_k_kernel writes for the same values).
+// block b of row i side by side (1024 / (256 / HD) threads each), then one
+// wave quantizes the block (q8_k_block: the bytes quantize_q8_k_kernel
+// writes for the same values).
 template <int HD>
 __global__ __launch_bounds__(1024)
 void attn_combine_q8k_kernel(const float* __restrict__ part, int n_split, int n_head, uint8_t* __restrict__ out) {
-    constexpr int NH = 256 / HD;
-    __shared__ CombineLds<HD> sm;
+    constexpr int NH = 256 / HD, NT = 1024 / NH;
+    __shared__ CombineLds<HD> sm[NH];
     __shared__ __align__(16) float vals[256];
     const int b = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
-    #pragma unroll 1
-    for (int hh = 0; hh < NH; hh++) {
-        const int h = b * NH + hh;
-        const float v = attn_combine_head<HD>(part + ((size_t)i * n_head + h) * n_split * (HD + 2), n_split, sm);
-        if (t < HD) vals[hh * HD + t] = v;
-        __syncthreads();   // the merge's LDS is reused by the next head
-    }
+    const int hh = t / NT, tg = t % NT, h = b * NH + hh;
+    const float v = attn_combine_head<HD, NT>(part + ((size_t)i * n_head + h) * n_split * (HD + 2), n_split, sm[hh], tg);
+    if (tg < HD) vals[hh * HD + tg] = v;
+    __syncthreads();
     if (t < 64) {
         const float4 v4 = reinterpret_cast<const float4*>(vals)[t];
         const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
