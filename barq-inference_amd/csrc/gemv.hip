@@ -105,7 +105,9 @@ void gemv_q8_kernel(const uint8_t* __restrict__ W, size_t row_bytes, const uint8
 // reduction: outputs are bit-identical to gemv_q8_rows<FmtQ4K, 2, true>.
 // Measured at C2 (14336 x 4096, one box, 11 rotating weight copies): 7.14
 // against 7.29 us; the bare staging reaches the streaming-read floor.
-// per wave: R rows of 2304 bytes (k = 4096) rounded up to whole 1 KB load instructions
+
+// LDS per wave: R rows of 2304 bytes (k = 4096) rounded up to whole 1 KB load
+// instructions
 template <int R>
 constexpr int q4k_lds_buf = (R * 16 * Q4_K_BYTES + 1023) / 1024 * 1024;
 constexpr int Q4K_LDS_BUF = q4k_lds_buf<2>;
