@@ -203,6 +203,24 @@ def test_gemv_q4k_lds_equals_register_gemv(be, orc):
         assert_close_1e3(got, ref.ravel())
 
 
+def test_gemv_q4_0_pairs_equal_dma_gemv(be, orc):
+    """The two-row LDS-staged Q4_0 GEMV (the default for k <= 4096) against
+    the LDS-streamed one-row-per-wave GEMV (BARQ_GEMV_LDS=0): bit-identical
+    outputs (same lane slicing, arithmetic and reduction), both within the
+    bar of the oracle; odd row counts leave the last wave one row, short k
+    leaves lanes idle."""
+    from conftest import assert_bits_equal
+    for n, k in [(1, 256), (7, 512), (300, 4096), (4096, 4096), (129, 1280), (64, 3840)]:
+        print("q4_0 pair gemv", n, k, flush=True)
+        w, xq, ref = matmul_case(orc, B.Q4_0, n, k, 1, 1900 + n + k)
+        wd, xd = dev(w), dev(xq)
+        got = be.matvec(B.Q4_0, wd, n, k, B.Q8_0, xd).cpu().numpy()
+        with env(BARQ_GEMV_LDS=0) as b:
+            base = b.matvec(B.Q4_0, wd, n, k, B.Q8_0, xd).cpu().numpy()
+        assert_bits_equal(got, base)
+        assert_close_1e3(got, ref.ravel())
+
+
 MOE_VARIANTS = [dict(BARQ_GEMM_BM=16), dict(BARQ_GEMM_BM=16, BARQ_GEMM_NS=4), dict(BARQ_GEMM_NS=3),
                 dict(BARQ_GEMM_NS=4), dict(BARQ_GEMM_KS=1), dict(BARQ_GEMM_KS=2), dict(BARQ_GEMM_KS=4)]
 
