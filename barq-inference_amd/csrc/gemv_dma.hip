@@ -415,6 +415,105 @@ void gemv_q40_pair_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const
     }
 }
 
+// ---- Q6_K, two rows per wave (k <= 4096) ------------------------------------------
+// The same scheme for Q6_K: each of the wave's two rows is copied as
+// gemv_dma_kernel's slice (eight 27-chunk windows, one per block pair, so
+// every block starts 0 or 2 bytes past a 16-byte boundary), the rows 3456
+// bytes apart in the wave's LDS buffer; the lane's Q8_K activation slice
+// (FmtQ6K's lane slicing) comes from inline-asm global loads issued before
+// the copies.  The outputs are gemv_dma_kernel<DQ6K, ...>'s, bit for bit.
+constexpr int Q6P_ROW = 8 * 432, Q6P_BUF = 7 * 1024;
+
+struct Q6XRaw {
+    i32x4v v[4];
+    i32x4v bs;
+    int dx;
+};
+
+__device__ __forceinline__ void q6_x_issue(Q6XRaw& r, const uint8_t* __restrict__ xq, int blk, const FmtQ6K::Lane& c) {
+    const uint8_t* b = xq + (size_t)blk * 292;
+    const uint8_t* bq = b + 128 * c.h + c.lr;   // quants of this lane at +4 + 128 h + lr + 32 qd
+    const uint8_t* bb = b + 16 * c.h;           // its bsums at +260 + 16 h
+    asm volatile("global_load_dword %0, %1, off" : "=v"(r.dx) : "v"(b));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:4" : "=v"(r.v[0]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:36" : "=v"(r.v[1]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:68" : "=v"(r.v[2]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:100" : "=v"(r.v[3]) : "v"(bq));
+    asm volatile("global_load_dwordx4 %0, %1, off offset:260" : "=v"(r.bs) : "v"(bb));
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q6k_pair_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
+                          float* __restrict__ y, int n_rows, int nblk) {
+    using F = FmtQ6K;
+    __shared__ __align__(16) uint8_t lds[WAVES][Q6P_BUF];
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * WAVES + wave) * 2;
+    if (row0 >= n_rows) return;
+    uint8_t* buf = lds[wave];
+    const F::Lane c = F::lane(l);
+    // every lane loads (lanes past the last block re-read it and ignore it)
+    Q6XRaw xr;
+    q6_x_issue(xr, xq, min(c.bl, nblk - 1), c);
+    const uint32_t rb = (uint32_t)nblk * Q6_K_BYTES, base = (uint32_t)row0 * rb;
+    const int npair = nblk / 2;
+    const i32x4v rs = make_rsrc4(W, w_bytes);
+    #pragma unroll
+    for (int q = 0; q < Q6P_BUF / 1024; q++) {
+        const int i = 64 * q + l, r = i / 216, j = i - 216 * r, p = j / 27, ch = j - 27 * p;
+        const uint32_t src = r < 2 && p < npair ? base + (uint32_t)r * rb + 420u * (uint32_t)p + 16u * (uint32_t)ch
+                                                : DMA_SKIP;
+        lds_load16_nt(rs, buf + 1024 * q, src, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const bool act = F::active(0, c, nblk);
+    // row 0's windows end at byte 3456: copies 0-3; copies 4-6 are row 1's
+    wait_vmcnt<3>();
+    asm volatile("" ::: "memory");
+    asm volatile("" : "+v"(xr.v[0]), "+v"(xr.v[1]), "+v"(xr.v[2]), "+v"(xr.v[3]), "+v"(xr.bs), "+v"(xr.dx));
+    F::X x;
+    #pragma unroll
+    for (int qd = 0; qd < 4; qd++)
+        x.v[qd] = make_uint4((uint32_t)xr.v[qd].x, (uint32_t)xr.v[qd].y, (uint32_t)xr.v[qd].z, (uint32_t)xr.v[qd].w);
+    x.dx = __builtin_bit_cast(float, xr.dx);
+    {
+        const uint32_t off = 16u * (uint32_t)c.s0;
+        x.bs32[0] = 32 * sext16((uint32_t)xr.bs.x, off);
+        x.bs32[1] = 32 * sext16((uint32_t)xr.bs.y, off);
+        x.bs32[2] = 32 * sext16((uint32_t)xr.bs.z, off);
+        x.bs32[3] = 32 * sext16((uint32_t)xr.bs.w, off);
+    }
+    float acc0 = 0.0f, acc1 = 0.0f;
+    if (act) {
+        F::Wt w;
+        DQ6K::load_w(w, buf, c);
+        acc0 = F::dot(w, x, c);
+    }
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    if (act) {
+        F::Wt w;
+        DQ6K::load_w(w, buf + Q6P_ROW, c);
+        acc1 = F::dot(w, x, c);
+    }
+    const float v = reduce4(acc0, acc1, 0.0f, 0.0f);
+    if ((l & 31) == 0) {
+        const int rr = l >> 5;
+        if (row0 + rr < n_rows) y[row0 + rr] = v;
+    }
+}
+
+// Whether the Q6_K two-row kernel takes a one-token GEMV (k <= 4096;
+// BARQ_GEMV_LDS=0 keeps gemv_dma_kernel).  Measured on one box, paired runs,
+// us per call: C3 (128256 x 4096) 62.9-63.5 against 64.4-64.6, 14336 x 4096
+// 9.9-10.0 against 11.3, 4096 x 4096 4.56-4.59 against 5.03.
+static bool q6k_pair_path(size_t n_rows, size_t k) {
+    return k > 0 && k <= 4096 && k % 512 == 0 && n_rows * (k / 256 * Q6_K_BYTES) < 0x80000000ull &&
+           tuning_env(TUNE_GEMV_LDS, 1) != 0;
+}
+
 // Whether the Q4_0 two-row kernel takes a one-token GEMV (k <= 4096, whole
 // 16-byte chunks per row; BARQ_GEMV_LDS=0 keeps gemv_dma_kernel).  Measured
 // at C1 (4096 x 4096, four paired runs on one box): 3.70-3.71 against
@@ -517,7 +616,16 @@ hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, c
                            hipStream_t s, size_t m) {
     if (n_rows == 0) return hipSuccess;
     switch (w_type) {
-    case TYPE_Q6_K: return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES, m);
+    case TYPE_Q6_K:
+        if (m == 1 && q6k_pair_path(n_rows, k)) {
+            constexpr int WAVES = 4;
+            hipLaunchKernelGGL((gemv_q6k_pair_kernel<WAVES>), dim3((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))),
+                               dim3(WAVES * 64), 0, s, static_cast<const uint8_t*>(W),
+                               (uint32_t)(n_rows * (k / 256 * Q6_K_BYTES)), static_cast<const uint8_t*>(xq), y,
+                               (int)n_rows, (int)(k / 256));
+            return hipGetLastError();
+        }
+        return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES, m);
     case TYPE_Q4_K: return dispatch_dma<DQ4K>(W, n_rows, k, xq, y, s, Q4_K_BYTES, Q8_K_BYTES, m);
     case TYPE_Q4_0:
         if (m == 1 && q40_pair_path(W, n_rows, k)) {

@@ -203,6 +203,23 @@ def test_gemv_q4k_lds_equals_register_gemv(be, orc):
         assert_close_1e3(got, ref.ravel())
 
 
+def test_gemv_q6_k_pairs_equal_dma_gemv(be, orc):
+    """The two-row LDS-staged Q6_K GEMV (the default for k <= 4096) against
+    the LDS-streamed GEMV (BARQ_GEMV_LDS=0): bit-identical outputs, both
+    within the bar of the oracle (both default launch shapes of the streamed
+    GEMV: one row per wave up to 8192 rows, four above)."""
+    from conftest import assert_bits_equal
+    for n, k in [(1, 512), (7, 1024), (300, 4096), (4096, 4096), (129, 3584), (8201, 4096)]:
+        print("q6_k pair gemv", n, k, flush=True)
+        w, xq, ref = matmul_case(orc, B.Q6_K, n, k, 1, 2100 + n + k)
+        wd, xd = dev(w), dev(xq)
+        got = be.matvec(B.Q6_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
+        with env(BARQ_GEMV_LDS=0) as b:
+            base = b.matvec(B.Q6_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
+        assert_bits_equal(got, base)
+        assert_close_1e3(got, ref.ravel())
+
+
 def test_gemv_q4_0_pairs_equal_dma_gemv(be, orc):
     """The two-row LDS-staged Q4_0 GEMV (the default for k <= 4096) against
     the LDS-streamed one-row-per-wave GEMV (BARQ_GEMV_LDS=0): bit-identical
