@@ -167,6 +167,7 @@ struct DQ40 {
         const int b = it * 128 + 2 * c.l;
         stage_x_q8_0(x, xs, b < nblk ? b : 0);
     }
+    static __device__ __forceinline__ void x_from_pair(F::X& x, const XQ80& r) { x = r; }
 };
 
 // Q8_0 weights (34-byte blocks): lane l's block pair is 68 bytes at 68 l
@@ -189,6 +190,7 @@ struct DQ80 {
         const int b = it * 128 + 2 * c.l;
         stage_x_q8_0(x, xs, b < nblk ? b : 0);
     }
+    static __device__ __forceinline__ void x_from_pair(F::X& x, const XQ80& r) { x = r; }
 };
 
 // Q4_0_BARQ (20-byte blocks): lane l's block pair is 40 bytes at 40 l
@@ -209,6 +211,10 @@ struct DQ40B {
         const int b = it * 128 + 2 * c.l;
         XQ80 r;
         stage_x_q8_0(r, xs, b < nblk ? b : 0);
+        x_from_pair(x, r);
+    }
+    // the even / odd activation bytes of the pair, for the split nibble layout
+    static __device__ __forceinline__ void x_from_pair(F::X& x, const XQ80& r) {
         #pragma unroll
         for (int j = 0; j < 2; j++) {
             const uint4 lo = r.v[2 * j], hi = r.v[2 * j + 1];
@@ -325,25 +331,27 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
     }
 }
 
-// ---- Q4_0, two rows per wave (k <= 4096) ------------------------------------------
-// The LDS-staged Q4_K rows' scheme (gemv.hip) for Q4_0: each wave copies its
-// two rows (2 * 18 * k / 32 contiguous bytes, 4608 at k = 4096) into its own
-// LDS buffer with whole-line non-temporal buffer->LDS loads; its lanes load
-// their Q8_0 activation block pair (68 bytes) into registers by inline-asm
-// global loads issued before the copies (the compiler does not count them,
-// so no wait of its own holds the copies back; nothing may touch these
-// registers before the explicit wait, which the build's assembly check
-// enforces), and row 0's arithmetic runs once its copies have landed.  No
-// workgroup barrier.  The lane slicing, arithmetic and reduction are
-// gemv_dma_kernel<DQ40, W, 1, 1>'s: the outputs are bit-identical.
-constexpr int Q40P_BUF = 5 * 1024;
+// ---- 32-element formats, two rows per wave (k <= 4096) ----------------------------
+// The LDS-staged Q4_K rows' scheme (gemv.hip) for Q4_0, Q8_0 and Q4_0_BARQ:
+// each wave copies its two rows (2 * rb contiguous bytes: 4608, 8704 and
+// 5120 at k = 4096) into its own LDS buffer with whole-line non-temporal
+// buffer->LDS loads; its lanes load their Q8_0 activation block pair (68
+// bytes) into registers by inline-asm global loads issued before the copies
+// (the compiler does not count them, so no wait of its own holds the copies
+// back; nothing may touch these registers before the explicit wait, which
+// the build's assembly check enforces), and row 0's arithmetic runs once its
+// copies have landed.  No workgroup barrier.  The lane slicing, arithmetic
+// and reduction are gemv_dma_kernel<P, W, 1, 1>'s: the outputs are
+// bit-identical.
+template <class P>
+constexpr int pair32_buf = (2 * 128 * P::F::ROW_BLOCK_BYTES + 1023) / 1024 * 1024;
 
-struct Q40XRaw {
+struct Q80XRaw {
     i32x4v v[4];
     int e;
 };
 
-__device__ __forceinline__ void q40_x_issue(Q40XRaw& r, const uint8_t* __restrict__ xq, int pair) {
+__device__ __forceinline__ void q80_x_issue(Q80XRaw& r, const uint8_t* __restrict__ xq, int pair) {
     const uint8_t* p = xq + (size_t)pair * 68;
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r.v[0]) : "v"(p));
     asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "=v"(r.v[1]) : "v"(p));
@@ -352,60 +360,71 @@ __device__ __forceinline__ void q40_x_issue(Q40XRaw& r, const uint8_t* __restric
     asm volatile("global_load_dword %0, %1, off offset:64" : "=v"(r.e) : "v"(p));
 }
 
-template <int WAVES>
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 4]
+__device__ __forceinline__ void wait_vmcnt_upto4(uint32_t n) {
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    default: wait_vmcnt<4>(); break;
+    }
+}
+
+template <class P, int WAVES>
 __global__ __launch_bounds__(WAVES * 64)
-void gemv_q40_pair_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
-                          float* __restrict__ y, int n_rows, int nblk) {
-    using F = FmtQ40;
-    __shared__ __align__(16) uint8_t lds[WAVES][Q40P_BUF];
+void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
+                        float* __restrict__ y, int n_rows, int nblk) {
+    using F = typename P::F;
+    constexpr int BUF = pair32_buf<P>;
+    __shared__ __align__(16) uint8_t lds[WAVES][BUF];
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * WAVES + wave) * 2;
     if (row0 >= n_rows) return;
     uint8_t* buf = lds[wave];
     // every lane loads (lanes past the last pair re-read it and ignore it)
-    Q40XRaw xr;
-    q40_x_issue(xr, xq, min(l, nblk / 2 - 1));
-    const uint32_t rb = (uint32_t)nblk * Q4_0_BYTES, span = 2 * rb;
+    Q80XRaw xr;
+    q80_x_issue(xr, xq, min(l, nblk / 2 - 1));
+    const uint32_t rb = (uint32_t)nblk * F::ROW_BLOCK_BYTES, span = 2 * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
     #pragma unroll
-    for (int q = 0; q < Q40P_BUF / 1024; q++) {
+    for (int q = 0; q < BUF / 1024; q++) {
         if (1024u * q < span) {
             const uint32_t off = 1024u * q + 16u * (uint32_t)l;
             lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : DMA_SKIP, 0);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    const F::Lane c = F::lane(l);
+    const typename F::Lane c = F::lane(l);
     const bool act = F::active(0, c, nblk);
-    // copies issued after the last one row 0 needs (0, 1 or 2)
-    const uint32_t later = (span + 1023) / 1024 - (rb + 1023) / 1024;
-    if (later >= 2) wait_vmcnt<2>();
-    else if (later == 1) wait_vmcnt<1>();
-    else wait_vmcnt<0>();
+    // copies issued after the last one row 0 needs (at most 4)
+    wait_vmcnt_upto4((span + 1023) / 1024 - (rb + 1023) / 1024);
     asm volatile("" ::: "memory");
     asm volatile("" : "+v"(xr.v[0]), "+v"(xr.v[1]), "+v"(xr.v[2]), "+v"(xr.v[3]), "+v"(xr.e));
-    F::X x;
+    typename F::X x;
     {
         const uint32_t w[17] = {(uint32_t)xr.v[0].x, (uint32_t)xr.v[0].y, (uint32_t)xr.v[0].z, (uint32_t)xr.v[0].w,
                                 (uint32_t)xr.v[1].x, (uint32_t)xr.v[1].y, (uint32_t)xr.v[1].z, (uint32_t)xr.v[1].w,
                                 (uint32_t)xr.v[2].x, (uint32_t)xr.v[2].y, (uint32_t)xr.v[2].z, (uint32_t)xr.v[2].w,
                                 (uint32_t)xr.v[3].x, (uint32_t)xr.v[3].y, (uint32_t)xr.v[3].z, (uint32_t)xr.v[3].w,
                                 (uint32_t)xr.e};
-        q8_0_pair_from_dwords(x, w);
+        XQ80 r;
+        q8_0_pair_from_dwords(r, w);
+        P::x_from_pair(x, r);
     }
     float acc0 = 0.0f, acc1 = 0.0f;
     if (act) {
-        F::Wt w;
-        DQ40::load_w(w, buf, c);
+        typename F::Wt w;
+        P::load_w(w, buf, c);
         acc0 = F::dot(w, x, c);
     }
     wait_vmcnt<0>();
     asm volatile("" ::: "memory");
     if (act) {
-        F::Wt w;
-        DQ40::load_w(w, buf + rb, c);
+        typename F::Wt w;
+        P::load_w(w, buf + rb, c);
         acc1 = F::dot(w, x, c);
     }
     const float v = reduce4(acc0, acc1, 0.0f, 0.0f);
@@ -514,13 +533,23 @@ static bool q6k_pair_path(size_t n_rows, size_t k) {
            tuning_env(TUNE_GEMV_LDS, 1) != 0;
 }
 
-// Whether the Q4_0 two-row kernel takes a one-token GEMV (k <= 4096, whole
-// 16-byte chunks per row; BARQ_GEMV_LDS=0 keeps gemv_dma_kernel).  Measured
-// at C1 (4096 x 4096, four paired runs on one box): 3.70-3.71 against
-// 3.89-3.91 us.
-static bool q40_pair_path(const void* W, size_t n_rows, size_t k) {
+// Whether a two-row kernel of the 32-element formats takes a one-token GEMV
+// (k <= 4096 and a multiple of 256, so rows are whole 16-byte chunks;
+// BARQ_GEMV_LDS=0 keeps gemv_dma_kernel).  Measured at C1 (Q4_0 4096 x 4096,
+// four paired runs on one box): 3.70-3.71 against 3.89-3.91 us.
+static bool pair32_path(const void* W, size_t n_rows, size_t k, int blk_bytes) {
     return k > 0 && k <= 4096 && k % 256 == 0 && ((uintptr_t)W & 15) == 0 &&
-           n_rows * (k / 32 * Q4_0_BYTES) < 0x80000000ull && tuning_env(TUNE_GEMV_LDS, 1) != 0;
+           n_rows * (k / 32 * (size_t)blk_bytes) < 0x80000000ull && tuning_env(TUNE_GEMV_LDS, 1) != 0;
+}
+
+template <class P>
+static hipError_t pair32_launch(const void* W, size_t n_rows, size_t k, const void* xq, float* y, hipStream_t s) {
+    constexpr int WAVES = 4;
+    hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES>), dim3((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))),
+                       dim3(WAVES * 64), 0, s, static_cast<const uint8_t*>(W),
+                       (uint32_t)(n_rows * (k / 32 * P::F::ROW_BLOCK_BYTES)), static_cast<const uint8_t*>(xq), y,
+                       (int)n_rows, (int)(k / 32));
+    return hipGetLastError();
 }
 
 // ---- launch ------------------------------------------------------------------
@@ -628,17 +657,14 @@ hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, c
         return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES, m);
     case TYPE_Q4_K: return dispatch_dma<DQ4K>(W, n_rows, k, xq, y, s, Q4_K_BYTES, Q8_K_BYTES, m);
     case TYPE_Q4_0:
-        if (m == 1 && q40_pair_path(W, n_rows, k)) {
-            constexpr int WAVES = 4;
-            hipLaunchKernelGGL((gemv_q40_pair_kernel<WAVES>), dim3((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))),
-                               dim3(WAVES * 64), 0, s, static_cast<const uint8_t*>(W),
-                               (uint32_t)(n_rows * (k / 32 * Q4_0_BYTES)), static_cast<const uint8_t*>(xq), y,
-                               (int)n_rows, (int)(k / 32));
-            return hipGetLastError();
-        }
+        if (m == 1 && pair32_path(W, n_rows, k, Q4_0_BYTES)) return pair32_launch<DQ40>(W, n_rows, k, xq, y, s);
         return dispatch_dma<DQ40>(W, n_rows, k, xq, y, s, Q4_0_BYTES, Q8_0_BYTES, m);
-    case TYPE_Q8_0: return dispatch_dma<DQ80>(W, n_rows, k, xq, y, s, Q8_0_BYTES, Q8_0_BYTES, m);
-    case TYPE_Q4_0_BARQ: return dispatch_dma<DQ40B>(W, n_rows, k, xq, y, s, Q4_0_BARQ_BYTES, Q8_0_BYTES, m);
+    case TYPE_Q8_0:
+        if (m == 1 && pair32_path(W, n_rows, k, Q8_0_BYTES)) return pair32_launch<DQ80>(W, n_rows, k, xq, y, s);
+        return dispatch_dma<DQ80>(W, n_rows, k, xq, y, s, Q8_0_BYTES, Q8_0_BYTES, m);
+    case TYPE_Q4_0_BARQ:
+        if (m == 1 && pair32_path(W, n_rows, k, Q4_0_BARQ_BYTES)) return pair32_launch<DQ40B>(W, n_rows, k, xq, y, s);
+        return dispatch_dma<DQ40B>(W, n_rows, k, xq, y, s, Q4_0_BARQ_BYTES, Q8_0_BYTES, m);
     default: return hipErrorInvalidValue;
     }
 }

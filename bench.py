@@ -122,18 +122,20 @@ def time_launches(launch, K, eager):
 ROTATE_BYTES = 1 << 30
 
 # dominant kernel of each config (config 5: every kernel of the MoE step)
-# (Q4_K, Q4_0 and Q6_K GEMVs with k <= 4096 run the LDS-staged two-row
-# kernels unless BARQ_GEMV_LDS=0)
+# (GEMVs with k <= 4096 run the LDS-staged two-row kernels unless
+# BARQ_GEMV_LDS=0)
 _LDS_OFF = os.environ.get("BARQ_GEMV_LDS") == "0"
 Q4K_GEMV = "gemv_q8_kernel<barq::FmtQ4K" if _LDS_OFF else "gemv_q4k_lds_kernel"
-Q40_GEMV = "gemv_dma_kernel<barq::DQ40," if _LDS_OFF else "gemv_q40_pair_kernel"
+Q40_GEMV = "gemv_dma_kernel<barq::DQ40," if _LDS_OFF else "gemv_pair32_kernel<barq::DQ40,"
 Q6K_GEMV = "gemv_dma_kernel<barq::DQ6K" if _LDS_OFF else "gemv_q6k_pair_kernel"
 KERNEL_OF_CONFIG = {1: Q40_GEMV, 2: Q4K_GEMV,
                     3: Q6K_GEMV, 4: "kq_kernel<barq::KQ4, 64", 5: "barq::"}
 # with --w-type: (GEMV, GEMM) kernel of each format
 KERNEL_OF_TYPE = {"Q4_0": (Q40_GEMV, "b32_gemm_kernel<barq::B40,"),
-                  "Q8_0": ("gemv_dma_kernel<barq::DQ80", "b32_gemm_kernel<barq::B80,"),
-                  "Q4_0_BARQ": ("gemv_dma_kernel<barq::DQ40B", "b32_gemm_kernel<barq::B40Barq"),
+                  "Q8_0": ("gemv_dma_kernel<barq::DQ80" if _LDS_OFF else "gemv_pair32_kernel<barq::DQ80",
+                           "b32_gemm_kernel<barq::B80,"),
+                  "Q4_0_BARQ": ("gemv_dma_kernel<barq::DQ40B" if _LDS_OFF else "gemv_pair32_kernel<barq::DQ40B",
+                                "b32_gemm_kernel<barq::B40Barq"),
                   "Q4_K": (Q4K_GEMV, "kq_kernel<barq::KQ4, 64"),
                   "Q6_K": (Q6K_GEMV, "kq_kernel<barq::KQ6")}
 

@@ -43,11 +43,8 @@ def env(**kv):
         b.close()
 
 
-GEN = {B.Q4_K: synth.gen_q4_k, B.Q6_K: synth.gen_q6_k, B.Q4_0: synth.gen_q4_0, B.Q8_0: synth.gen_q8_0}
-
-
 def matmul_case(orc, w_type, n, k, m, seed):
-    w = GEN[w_type](n, k, seed)
+    w = synth.gen_weights(w_type, n, k, seed)
     x = synth.gen_f32(m * k, seed + 1).reshape(m, k)
     xq = orc.quantize_act(B.Q8_PARTNER[w_type], x)
     return w, xq, orc.matmul(w_type, w, n, k, B.Q8_PARTNER[w_type], xq, m)
@@ -220,20 +217,22 @@ def test_gemv_q6_k_pairs_equal_dma_gemv(be, orc):
         assert_close_1e3(got, ref.ravel())
 
 
-def test_gemv_q4_0_pairs_equal_dma_gemv(be, orc):
-    """The two-row LDS-staged Q4_0 GEMV (the default for k <= 4096) against
-    the LDS-streamed one-row-per-wave GEMV (BARQ_GEMV_LDS=0): bit-identical
-    outputs (same lane slicing, arithmetic and reduction), both within the
-    bar of the oracle; odd row counts leave the last wave one row, short k
-    leaves lanes idle."""
+@pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_0_BARQ"])
+def test_gemv_32_element_pairs_equal_dma_gemv(be, orc, name):
+    """The two-row LDS-staged GEMV of the 32-element formats (the default for
+    k <= 4096) against the LDS-streamed one-row-per-wave GEMV
+    (BARQ_GEMV_LDS=0): bit-identical outputs (same lane slicing, arithmetic
+    and reduction), both within the bar of the oracle; odd row counts leave
+    the last wave one row, short k leaves lanes idle."""
     from conftest import assert_bits_equal
+    t = getattr(B, name)
     for n, k in [(1, 256), (7, 512), (300, 4096), (4096, 4096), (129, 1280), (64, 3840)]:
-        print("q4_0 pair gemv", n, k, flush=True)
-        w, xq, ref = matmul_case(orc, B.Q4_0, n, k, 1, 1900 + n + k)
+        print(f"{name} pair gemv", n, k, flush=True)
+        w, xq, ref = matmul_case(orc, t, n, k, 1, 1900 + n + k)
         wd, xd = dev(w), dev(xq)
-        got = be.matvec(B.Q4_0, wd, n, k, B.Q8_0, xd).cpu().numpy()
+        got = be.matvec(t, wd, n, k, B.Q8_PARTNER[t], xd).cpu().numpy()
         with env(BARQ_GEMV_LDS=0) as b:
-            base = b.matvec(B.Q4_0, wd, n, k, B.Q8_0, xd).cpu().numpy()
+            base = b.matvec(t, wd, n, k, B.Q8_PARTNER[t], xd).cpu().numpy()
         assert_bits_equal(got, base)
         assert_close_1e3(got, ref.ravel())
 
