@@ -118,7 +118,7 @@ def test_ffn_fused_gate_up_matches_separate_path(be, orc):
     assert np.array_equal(two[0], two[1])
     for glu in (14, 12, 18, 24, 22, 28):
         print(f"ffn glu shape {glu}", flush=True)
-        with tuned(BARQ_GEMV_GLU=glu) as b:
+        with tuned(BARQ_GEMV_GLU=glu, BARQ_GEMV_LDS=0) as b:
             got = host(b.ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, n_embd, n_ff, B.Q8_K, dev(xq), 1))
         assert_close_chained(got, ref)
     # odd n_ff: the last wave of the two-output shape has one output
@@ -126,9 +126,27 @@ def test_ffn_fused_gate_up_matches_separate_path(be, orc):
     gate2, up2, down2, x2 = ffn_case(1024, n_ff2, 1, 420, B.Q4_K, B.Q4_K, B.Q4_K)
     xq2 = orc.quantize_act(B.Q8_K, x2)
     ref2 = orc.ffn(B.Q4_K, gate2, B.Q4_K, up2, B.Q4_K, down2, 1024, n_ff2, orc.Q8_K, xq2, 1)
-    with tuned(BARQ_GEMV_GLU=24) as b:
+    with tuned(BARQ_GEMV_GLU=24, BARQ_GEMV_LDS=0) as b:
         got2 = host(b.ffn(B.Q4_K, dev(gate2), B.Q4_K, dev(up2), B.Q4_K, dev(down2), 1024, n_ff2, B.Q8_K, dev(xq2), 1))
     assert_close_chained(got2, ref2)
+
+
+def test_ffn_lds_gate_up_equals_register_gate_up(be, orc):
+    """The LDS-staged fused gate/up GEMV (the default for k <= 4096) gives
+    the register kernel's h (BARQ_GEMV_LDS=0) bit for bit, so the whole FFN
+    output matches; short k leaves lanes idle, and n_ff is not a multiple of
+    the rows per workgroup."""
+    for n_embd, n_ff in [(4096, 14336), (1024, 256 * 9), (768, 512)]:
+        print(f"ffn lds glu {n_embd} {n_ff}", flush=True)
+        gate, up, down, x = ffn_case(n_embd, n_ff, 1, 440 + n_embd, B.Q4_K, B.Q4_K, B.Q6_K)
+        xq = orc.quantize_act(B.Q8_K, x)
+        gd, ud, dd = dev(gate), dev(up), dev(down)
+        got = host(be.ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, n_embd, n_ff, B.Q8_K, dev(xq), 1))
+        with tuned(BARQ_GEMV_LDS=0) as b:
+            base = host(b.ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, n_embd, n_ff, B.Q8_K, dev(xq), 1))
+        assert np.array_equal(got, base)
+        ref = orc.ffn(B.Q4_K, gate, B.Q4_K, up, B.Q6_K, down, n_embd, n_ff, orc.Q8_K, xq, 1)
+        assert_close_chained(got, ref)
 
 
 @pytest.mark.parametrize("m", [1, 3])
