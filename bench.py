@@ -999,6 +999,32 @@ def main():
     q_ms, _ = time_launches(qlaunch, args.steps, args.eager)
 
     alg = algorithmic_bytes(w_type, n, k, m)
+    fixed = {}
+    if m == 1:
+        # What a launch costs apart from its bytes: a one-element fill kernel
+        # timed the same way on the same stream (the graph's per-launch floor),
+        # and the same GEMV over twice the rows, whose extra time gives the
+        # streaming rate once the launch is under way.
+        t1 = torch.zeros(1, device="cuda")
+
+        def flaunch(i):
+            t1.fill_(float(i))
+        floor_ms, _ = time_launches(flaunch, args.steps, args.eager)
+        w2 = torch.cat([w0, w0])
+        copies2 = max(2, -(-ROTATE_BYTES // (2 * wbytes)))
+        ws2 = [w2] + [w2.clone() for _ in range(copies2 - 1)]
+        y2 = torch.empty(2 * n, dtype=torch.float32, device="cuda")
+
+        def launch2(i):
+            be.matvec_raw(w_type, ws2[i % copies2], 2 * n, k, at, xq, y2, B.MEM_DEVICE)
+        for i in range(min(args.warmup, 500)):
+            launch2(i)
+        torch.cuda.synchronize()
+        ms2, _ = time_launches(launch2, args.steps, args.eager)
+        extra = algorithmic_bytes(w_type, 2 * n, k, 1) - alg
+        fixed = {"launch_floor_us": round(floor_ms * 1e3, 3), "us_per_call_2x_rows": round(ms2 * 1e3, 3),
+                 "marginal_gbs": round(extra / ((ms2 - ms) * 1e-3) / 1e9, 1) if ms2 > ms else None}
+        del ws2, w2
     us = ms * 1e3
     gbs = alg / (ms * 1e-3) / 1e9
     # correctness of the timed output against the oracle
@@ -1036,6 +1062,7 @@ def main():
         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "us_per_call_eager": round(ms_eager * 1e3, 3),
         "act_quant_us": round(q_ms * 1e3, 3),
+        **fixed,
         "parity_rel_err": ok,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
