@@ -147,6 +147,25 @@ def test_prompt_attention_graph_replays(be, q_len):
     c.close()
 
 
+def test_ffn_graph_replays(be):
+    """The one-token FFN (fused gate/up launch, h's quantizer, down GEMV):
+    every replay equals the eager call, with FFN calls of another shape
+    between the replays."""
+    import torch
+    n_embd, n_ff = 1024, 2304
+    w = [dev(synth.gen_q4_k(n_ff, n_embd, 41)), dev(synth.gen_q4_k(n_ff, n_embd, 42)),
+         dev(synth.gen_weights(B.Q6_K, n_embd, n_ff, 43))]
+    xq = be.quantize_act(B.Q8_K, dev(synth.gen_f32(n_embd, 44)))
+    y = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
+    w2 = [dev(synth.gen_q4_k(512, 768, 45)), dev(synth.gen_q4_k(512, 768, 46)), dev(synth.gen_weights(B.Q6_K, 768, 512, 47))]
+    x2 = be.quantize_act(B.Q8_K, dev(synth.gen_f32(768, 48)))
+
+    def noise():
+        be.ffn(B.Q4_K, w2[0], B.Q4_K, w2[1], B.Q6_K, w2[2], 768, 512, B.Q8_K, x2, 1, sync=False)
+    replays_match(be, lambda: be.ffn(B.Q4_K, w[0], B.Q4_K, w[1], B.Q6_K, w[2], n_embd, n_ff, B.Q8_K, xq, 1,
+                                     sync=False, out=y), y, noise)
+
+
 def test_graph_replay_after_workspace_growth(be):
     """A graph captured around a call that uses the workspace keeps working
     after a later, larger call grows the workspace: the old buffer is
