@@ -68,6 +68,9 @@ def parse():
                    help="one Llama-3-8B layer over a --m token prompt (GEMMs, MFMA attention): tokens/s")
     p.add_argument("--layer", action="store_true",
                    help="time one Llama-3-8B decode layer (norm, q/k/v, RoPE + KV append, attention, o, norm, FFN)")
+    p.add_argument("--no-fixed", action="store_true",
+                   help="one-token configs: skip timing the per-launch floor and the GEMV over twice the rows "
+                        "(kernel traces and counter runs then hold only the measured launches)")
     p.add_argument("--probe-copy", action="store_true",
                    help="also run 5 device copies of 256 MiB (reference for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -164,7 +167,7 @@ def measure_traffic(config, w_type_name=None):
         out = os.path.join(tmp, counter)
         cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "t", "--",
                sys.executable, os.path.abspath(__file__), "--config", str(config), "--steps", "10", "--warmup", "2",
-               "--no-cpu", "--no-traffic", "--probe-copy"] + extra
+               "--no-cpu", "--no-traffic", "--no-fixed", "--probe-copy"] + extra
         try:
             r = subprocess.run(cmd, cwd=tmp, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, timeout=180)
         except subprocess.TimeoutExpired:
@@ -1000,7 +1003,7 @@ def main():
 
     alg = algorithmic_bytes(w_type, n, k, m)
     fixed = {}
-    if m == 1:
+    if m == 1 and not args.no_fixed:
         # What a launch costs apart from its bytes: a one-element fill kernel
         # timed the same way on the same stream (the graph's per-launch floor),
         # and the same GEMV over twice the rows, whose extra time gives the
