@@ -266,6 +266,76 @@ void gemv_q4k_lds_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const 
     }
 }
 
+// Q4_K with k <= 4096 for NX = 2-4 activation rows (a small decode batch):
+// the LDS-staged rows above, each wave copying its R weight rows once and
+// loading its lanes' slice of every activation row by inline asm ahead of the
+// copies.  Each (token, row) product is FmtQ4K::dot on the one-token kernel's
+// lane slices, reduced by reduce4, so y[j][r] equals the one-token GEMV of
+// activation row j bit for bit.
+template <int WAVES, int R, int NX>
+__global__ __launch_bounds__(WAVES * 64)
+void gemv_q4k_lds_multi_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
+                               uint32_t x_row_bytes, float* __restrict__ y, int n_rows, int nblk) {
+    using F = FmtQ4K;
+    constexpr int NA = NX * R;   // token j, row r at j * R + r
+    __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][q4k_lds_buf<R>];
+    const int l = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (wg_rows_remap<R * WAVES>(blockIdx.x, gridDim.x) * WAVES + wave) * R;
+    if (row0 >= n_rows) return;
+    uint8_t* buf = lds[wave];
+    Q4KXRaw xr[NX];
+    #pragma unroll
+    for (int j = 0; j < NX; j++) q4k_x_issue(xr[j], xq + (size_t)j * x_row_bytes, min(l >> 2, nblk - 1), l & 3);
+    const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = R * rb;
+    const i32x4v rs = make_rsrc4(W, w_bytes);
+    const uint32_t base = (uint32_t)row0 * rb;
+    #pragma unroll
+    for (int q = 0; q < q4k_lds_buf<R> / 1024; q++) {
+        if (1024u * q < span) {
+            const uint32_t off = 1024u * q + 16u * (uint32_t)l;
+            lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const F::Lane c = F::lane(l);
+    const uint32_t n_all = (span + 1023) / 1024;
+    const bool act = F::active(0, c, nblk);
+    const uint8_t* b = buf + Q4_K_BYTES * c.sbl;
+    F::X xs[NX];
+    float acc[NA];
+    #pragma unroll
+    for (int i = 0; i < NA; i++) acc[i] = 0.0f;
+    #pragma unroll
+    for (int r = 0; r < R; r++) {
+        // the activation rows and row r's copies (loads complete in order)
+        wait_vmcnt_upto8(n_all - (rb * (r + 1) + 1023) / 1024);
+        asm volatile("" ::: "memory");
+        if (r == 0) {
+            #pragma unroll
+            for (int j = 0; j < NX; j++) q4k_x_ready(xr[j], xs[j]);
+        }
+        if (act) {
+            F::Wt w;
+            w.hdr = *reinterpret_cast<const uint4*>(b + r * rb);
+            w.q0 = *reinterpret_cast<const uint4*>(b + r * rb + 16 + 32 * c.p);
+            w.q1 = *reinterpret_cast<const uint4*>(b + r * rb + 32 + 32 * c.p);
+            #pragma unroll
+            for (int j = 0; j < NX; j++) acc[j * R + r] = F::dot(w, xs[j], c);
+        }
+    }
+    #pragma unroll
+    for (int g = 0; g < NA; g += 4) {
+        const float v = reduce4(acc[g], g + 1 < NA ? acc[g + 1] : 0.0f, g + 2 < NA ? acc[g + 2] : 0.0f,
+                                g + 3 < NA ? acc[g + 3] : 0.0f);
+        if ((l & 15) == 0) {
+            const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+            const int j = f / R, rr = f - j * R;
+            if (f < NA && row0 + rr < n_rows) y[(size_t)j * n_rows + row0 + rr] = v;
+        }
+    }
+}
+
 // One row of W by this wave with the single-chunk lane slicing (k <= 4096):
 // gemv_q8_rows<F, 1, true>'s arithmetic, the result in lane 0.
 template <class F>
@@ -785,6 +855,30 @@ hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t
     const uint8_t* x = static_cast<const uint8_t*>(xq);
     const size_t rb = k / 256 * 144, xrb = k / 256 * 292;
     const int n = (int)n_rows, kk = (int)k;
+    // measured at 14336 x 4096 (two paired runs on one box, us per call for
+    // 2 / 3 / 4 tokens): four rows per wave 8.40 / 10.05 / 11.58, two rows
+    // (BARQ_GEMV_LDS=2) 8.54 / 10.39 / 12.11, the register GEMV
+    // (BARQ_GEMV_LDS=0) 9.35 / 12.30 / 13.17
+    const int lds_mode = tuning_env(TUNE_GEMV_LDS, 1);
+    if (k <= 4096 && n_rows * rb < 0x80000000ull && lds_mode != 0) {
+        constexpr int WAVES = 4;
+        const int R = lds_mode == 2 ? 2 : 4;
+        const unsigned grid = (unsigned)((n_rows + (size_t)R * WAVES - 1) / ((size_t)R * WAVES));
+#define BARQ_LDS_MULTI(RR, NN)                                                                                    \
+    hipLaunchKernelGGL((gemv_q4k_lds_multi_kernel<WAVES, RR, NN>), dim3(grid), dim3(WAVES * 64), 0, s, w,          \
+                       (uint32_t)(n_rows * rb), x, (uint32_t)xrb, y, n, kk / 256);                                \
+    return hipGetLastError();
+        if (R == 2) {
+            if (m == 2) { BARQ_LDS_MULTI(2, 2) }
+            if (m == 3) { BARQ_LDS_MULTI(2, 3) }
+            BARQ_LDS_MULTI(2, 4)
+        } else {
+            if (m == 2) { BARQ_LDS_MULTI(4, 2) }
+            if (m == 3) { BARQ_LDS_MULTI(4, 3) }
+            BARQ_LDS_MULTI(4, 4)
+        }
+#undef BARQ_LDS_MULTI
+    }
     switch (m) {
     case 2: return launch_q8_multi<FmtQ4K, 2, 4, 2>(w, rb, x, xrb, y, n, kk, s);
     case 3: return launch_q8_multi<FmtQ4K, 2, 4, 3>(w, rb, x, xrb, y, n, kk, s);

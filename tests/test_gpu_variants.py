@@ -131,9 +131,10 @@ def test_gemm_k_slices(be, orc, w_type):
 
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_matmul_small_m(be, orc, name):
-    """A few activation rows: 2-4 rows run one GEMV over all of them (the
-    register GEMV for Q4_K, the LDS-streamed one for the other formats; k =
-    5120 adds a second, partial 4096-element chunk), 5 and more the MFMA
+    """A few activation rows: 2-4 rows run one GEMV over all of them (for
+    Q4_K the LDS-staged GEMV up to k = 4096 and the register GEMV above, the
+    LDS-streamed one for the other formats; k = 5120 adds a second, partial
+    4096-element chunk), 5 and more the MFMA
     GEMMs; each M also with the GEMM and the per-row GEMVs forced
     (BARQ_GEMM_MIN_M=2 or 16 with the multi-row GEMV off), device and host
     buffers."""
@@ -198,6 +199,31 @@ def test_gemv_q4k_lds_equals_register_gemv(be, orc):
         assert_bits_equal(got, reg)
         assert_bits_equal(quad, reg)
         assert_close_1e3(got, ref.ravel())
+
+
+def test_gemv_q4k_lds_multi_equals_one_token_gemv(be, orc):
+    """2-4 activation rows on the LDS-staged Q4_K GEMV (the default for k <=
+    4096; four or, with BARQ_GEMV_LDS=2, two weight rows per wave): row j of
+    the result equals the one-token GEMV of activation row j bit for bit, and
+    the oracle within its bar.  Ragged row counts, short k."""
+    from conftest import assert_bits_equal
+    for n, k in [(300, 4096), (14336, 4096), (37, 512), (1, 256), (8203, 1024)]:
+        for m in (2, 3, 4):
+            print("q4_k lds multi", n, k, m, flush=True)
+            w, xq, ref = matmul_case(orc, B.Q4_K, n, k, m, 2500 + n + k + m)
+            wd, xd = dev(w), dev(xq)
+            rb = B.row_bytes(B.Q8_K, k)
+            one = [be.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd[j * rb:(j + 1) * rb]).cpu().numpy() for j in range(m)]
+            got = be.matmul(B.Q4_K, wd, n, k, B.Q8_K, xd, m).cpu().numpy().reshape(m, n)
+            with env(BARQ_GEMV_LDS=2) as b:
+                pair = b.matmul(B.Q4_K, wd, n, k, B.Q8_K, xd, m).cpu().numpy().reshape(m, n)
+            with env(BARQ_GEMV_LDS=0) as b:   # the register multi-row GEMV
+                reg = b.matmul(B.Q4_K, wd, n, k, B.Q8_K, xd, m).cpu().numpy().reshape(m, n)
+            for j in range(m):
+                assert_bits_equal(got[j], one[j])
+                assert_bits_equal(pair[j], one[j])
+            assert_close_1e3(got, ref)
+            assert_close_1e3(reg, ref)
 
 
 def test_gemv_q6_k_pairs_equal_dma_gemv(be, orc):
