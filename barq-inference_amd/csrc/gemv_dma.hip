@@ -461,10 +461,30 @@ __device__ __forceinline__ void q6_x_issue(Q6XRaw& r, const uint8_t* __restrict_
     asm volatile("global_load_dwordx4 %0, %1, off offset:260" : "=v"(r.bs) : "v"(bb));
 }
 
-template <int WAVES>
+// FmtQ6K::X from the loaded registers, after the wait that covers them (the
+// empty asm keeps the compiler from reading them earlier)
+__device__ __forceinline__ void q6_x_ready(Q6XRaw& xr, FmtQ6K::X& x, const FmtQ6K::Lane& c) {
+    asm volatile("" : "+v"(xr.v[0]), "+v"(xr.v[1]), "+v"(xr.v[2]), "+v"(xr.v[3]), "+v"(xr.bs), "+v"(xr.dx));
+    #pragma unroll
+    for (int qd = 0; qd < 4; qd++)
+        x.v[qd] = make_uint4((uint32_t)xr.v[qd].x, (uint32_t)xr.v[qd].y, (uint32_t)xr.v[qd].z, (uint32_t)xr.v[qd].w);
+    x.dx = __builtin_bit_cast(float, xr.dx);
+    const uint32_t off = 16u * (uint32_t)c.s0;
+    x.bs32[0] = 32 * sext16((uint32_t)xr.bs.x, off);
+    x.bs32[1] = 32 * sext16((uint32_t)xr.bs.y, off);
+    x.bs32[2] = 32 * sext16((uint32_t)xr.bs.z, off);
+    x.bs32[3] = 32 * sext16((uint32_t)xr.bs.w, off);
+}
+
+//
+// NX = 2-4 activation rows (a small decode batch; x_row_bytes apart, y is
+// [NX x n_rows]): the wave loads its lanes' slice of every activation row
+// ahead of the copies and computes each (token, row) product the same way, so
+// y[j] equals the one-token GEMV of activation row j bit for bit.
+template <int WAVES, int NX = 1>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_q6k_pair_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
-                          float* __restrict__ y, int n_rows, int nblk) {
+                          float* __restrict__ y, int n_rows, int nblk, uint32_t x_row_bytes) {
     using F = FmtQ6K;
     __shared__ __align__(16) uint8_t lds[WAVES][Q6P_BUF];
     const int l = threadIdx.x & 63;
@@ -474,8 +494,9 @@ void gemv_q6k_pair_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const
     uint8_t* buf = lds[wave];
     const F::Lane c = F::lane(l);
     // every lane loads (lanes past the last block re-read it and ignore it)
-    Q6XRaw xr;
-    q6_x_issue(xr, xq, min(c.bl, nblk - 1), c);
+    Q6XRaw xr[NX];
+    #pragma unroll
+    for (int j = 0; j < NX; j++) q6_x_issue(xr[j], xq + (size_t)j * x_row_bytes, min(c.bl, nblk - 1), c);
     const uint32_t rb = (uint32_t)nblk * Q6_K_BYTES, base = (uint32_t)row0 * rb;
     const int npair = nblk / 2;
     const i32x4v rs = make_rsrc4(W, w_bytes);
@@ -491,36 +512,43 @@ void gemv_q6k_pair_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const
     // row 0's windows end at byte 3456: copies 0-3; copies 4-6 are row 1's
     wait_vmcnt<3>();
     asm volatile("" ::: "memory");
-    asm volatile("" : "+v"(xr.v[0]), "+v"(xr.v[1]), "+v"(xr.v[2]), "+v"(xr.v[3]), "+v"(xr.bs), "+v"(xr.dx));
-    F::X x;
+    F::X x[NX];
     #pragma unroll
-    for (int qd = 0; qd < 4; qd++)
-        x.v[qd] = make_uint4((uint32_t)xr.v[qd].x, (uint32_t)xr.v[qd].y, (uint32_t)xr.v[qd].z, (uint32_t)xr.v[qd].w);
-    x.dx = __builtin_bit_cast(float, xr.dx);
-    {
-        const uint32_t off = 16u * (uint32_t)c.s0;
-        x.bs32[0] = 32 * sext16((uint32_t)xr.bs.x, off);
-        x.bs32[1] = 32 * sext16((uint32_t)xr.bs.y, off);
-        x.bs32[2] = 32 * sext16((uint32_t)xr.bs.z, off);
-        x.bs32[3] = 32 * sext16((uint32_t)xr.bs.w, off);
-    }
-    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int j = 0; j < NX; j++) q6_x_ready(xr[j], x[j], c);
+    float acc[2 * NX];   // token j, row r at 2 j + r
+    #pragma unroll
+    for (int i = 0; i < 2 * NX; i++) acc[i] = 0.0f;
     if (act) {
         F::Wt w;
         DQ6K::load_w(w, buf, c);
-        acc0 = F::dot(w, x, c);
+        #pragma unroll
+        for (int j = 0; j < NX; j++) acc[2 * j] = F::dot(w, x[j], c);
     }
     wait_vmcnt<0>();
     asm volatile("" ::: "memory");
     if (act) {
         F::Wt w;
         DQ6K::load_w(w, buf + Q6P_ROW, c);
-        acc1 = F::dot(w, x, c);
+        #pragma unroll
+        for (int j = 0; j < NX; j++) acc[2 * j + 1] = F::dot(w, x[j], c);
     }
-    const float v = reduce4(acc0, acc1, 0.0f, 0.0f);
-    if ((l & 31) == 0) {
-        const int rr = l >> 5;
-        if (row0 + rr < n_rows) y[row0 + rr] = v;
+    if constexpr (NX == 1) {
+        const float v = reduce4(acc[0], acc[1], 0.0f, 0.0f);
+        if ((l & 31) == 0) {
+            const int rr = l >> 5;
+            if (row0 + rr < n_rows) y[row0 + rr] = v;
+        }
+    } else {
+        constexpr int NA = 2 * NX;
+        #pragma unroll
+        for (int g = 0; g < NA; g += 4) {
+            const float v = reduce4(acc[g], acc[g + 1], g + 2 < NA ? acc[g + 2] : 0.0f, g + 3 < NA ? acc[g + 3] : 0.0f);
+            if ((l & 15) == 0) {
+                const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+                const int j = f >> 1, rr = f & 1;
+                if (f < NA && row0 + rr < n_rows) y[(size_t)j * n_rows + row0 + rr] = v;
+            }
+        }
     }
 }
 
@@ -646,12 +674,19 @@ hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, c
     if (n_rows == 0) return hipSuccess;
     switch (w_type) {
     case TYPE_Q6_K:
-        if (m == 1 && q6k_pair_path(n_rows, k)) {
+        if (m <= 4 && q6k_pair_path(n_rows, k)) {
             constexpr int WAVES = 4;
-            hipLaunchKernelGGL((gemv_q6k_pair_kernel<WAVES>), dim3((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))),
-                               dim3(WAVES * 64), 0, s, static_cast<const uint8_t*>(W),
-                               (uint32_t)(n_rows * (k / 256 * Q6_K_BYTES)), static_cast<const uint8_t*>(xq), y,
-                               (int)n_rows, (int)(k / 256));
+            const dim3 grid((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))), block(WAVES * 64);
+            const uint32_t wb = (uint32_t)(n_rows * (k / 256 * Q6_K_BYTES)), xrb = (uint32_t)(k / 256 * Q8_K_BYTES);
+            const uint8_t* w8 = static_cast<const uint8_t*>(W);
+            const uint8_t* x8 = static_cast<const uint8_t*>(xq);
+            const int n = (int)n_rows, nb = (int)(k / 256);
+            switch (m) {
+            case 1: hipLaunchKernelGGL((gemv_q6k_pair_kernel<WAVES, 1>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+            case 2: hipLaunchKernelGGL((gemv_q6k_pair_kernel<WAVES, 2>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+            case 3: hipLaunchKernelGGL((gemv_q6k_pair_kernel<WAVES, 3>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+            default: hipLaunchKernelGGL((gemv_q6k_pair_kernel<WAVES, 4>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+            }
             return hipGetLastError();
         }
         return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES, m);

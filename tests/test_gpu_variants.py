@@ -243,6 +243,28 @@ def test_gemv_q6_k_pairs_equal_dma_gemv(be, orc):
         assert_close_1e3(got, ref.ravel())
 
 
+def test_gemv_q6_k_pairs_multi_equal_one_token_gemv(be, orc):
+    """2-4 activation rows on the two-row Q6_K GEMV (the default for k <=
+    4096): row j of the result equals the one-token GEMV of activation row j
+    bit for bit, the LDS-streamed multi-token GEMV (BARQ_GEMV_LDS=0) and the
+    oracle within the bar.  Odd row counts, short k, more than 8192 rows."""
+    from conftest import assert_bits_equal
+    for n, k in [(300, 4096), (129, 3584), (1, 512), (8201, 1024)]:
+        for m in (2, 3, 4):
+            print("q6_k pair multi", n, k, m, flush=True)
+            w, xq, ref = matmul_case(orc, B.Q6_K, n, k, m, 2700 + n + k + m)
+            wd, xd = dev(w), dev(xq)
+            rb = B.row_bytes(B.Q8_K, k)
+            one = [be.matvec(B.Q6_K, wd, n, k, B.Q8_K, xd[j * rb:(j + 1) * rb]).cpu().numpy() for j in range(m)]
+            got = be.matmul(B.Q6_K, wd, n, k, B.Q8_K, xd, m).cpu().numpy().reshape(m, n)
+            with env(BARQ_GEMV_LDS=0) as b:
+                base = b.matmul(B.Q6_K, wd, n, k, B.Q8_K, xd, m).cpu().numpy().reshape(m, n)
+            for j in range(m):
+                assert_bits_equal(got[j], one[j])
+            assert_close_1e3(got, ref)
+            assert_close_1e3(base, ref)
+
+
 @pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_gemv_32_element_pairs_equal_dma_gemv(be, orc, name):
     """The two-row LDS-staged GEMV of the 32-element formats (the default for
