@@ -371,10 +371,14 @@ __device__ __forceinline__ void wait_vmcnt_upto4(uint32_t n) {
     }
 }
 
-template <class P, int WAVES>
+// NX = 2-4 activation rows (x_row_bytes apart; y is [NX x n_rows]): every
+// row's block pair is loaded ahead of the copies and each (token, row)
+// product computed the same way, so y[j] equals the one-token GEMV of
+// activation row j bit for bit.
+template <class P, int WAVES, int NX = 1>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
-                        float* __restrict__ y, int n_rows, int nblk) {
+                        float* __restrict__ y, int n_rows, int nblk, uint32_t x_row_bytes) {
     using F = typename P::F;
     constexpr int BUF = pair32_buf<P>;
     __shared__ __align__(16) uint8_t lds[WAVES][BUF];
@@ -384,8 +388,9 @@ void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const u
     if (row0 >= n_rows) return;
     uint8_t* buf = lds[wave];
     // every lane loads (lanes past the last pair re-read it and ignore it)
-    Q80XRaw xr;
-    q80_x_issue(xr, xq, min(l, nblk / 2 - 1));
+    Q80XRaw xr[NX];
+    #pragma unroll
+    for (int j = 0; j < NX; j++) q80_x_issue(xr[j], xq + (size_t)j * x_row_bytes, min(l, nblk / 2 - 1));
     const uint32_t rb = (uint32_t)nblk * F::ROW_BLOCK_BYTES, span = 2 * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
@@ -402,35 +407,54 @@ void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const u
     // copies issued after the last one row 0 needs (at most 4)
     wait_vmcnt_upto4((span + 1023) / 1024 - (rb + 1023) / 1024);
     asm volatile("" ::: "memory");
-    asm volatile("" : "+v"(xr.v[0]), "+v"(xr.v[1]), "+v"(xr.v[2]), "+v"(xr.v[3]), "+v"(xr.e));
-    typename F::X x;
-    {
-        const uint32_t w[17] = {(uint32_t)xr.v[0].x, (uint32_t)xr.v[0].y, (uint32_t)xr.v[0].z, (uint32_t)xr.v[0].w,
-                                (uint32_t)xr.v[1].x, (uint32_t)xr.v[1].y, (uint32_t)xr.v[1].z, (uint32_t)xr.v[1].w,
-                                (uint32_t)xr.v[2].x, (uint32_t)xr.v[2].y, (uint32_t)xr.v[2].z, (uint32_t)xr.v[2].w,
-                                (uint32_t)xr.v[3].x, (uint32_t)xr.v[3].y, (uint32_t)xr.v[3].z, (uint32_t)xr.v[3].w,
-                                (uint32_t)xr.e};
+    typename F::X x[NX];
+    #pragma unroll
+    for (int j = 0; j < NX; j++) {
+        Q80XRaw& q = xr[j];
+        asm volatile("" : "+v"(q.v[0]), "+v"(q.v[1]), "+v"(q.v[2]), "+v"(q.v[3]), "+v"(q.e));
+        const uint32_t w[17] = {(uint32_t)q.v[0].x, (uint32_t)q.v[0].y, (uint32_t)q.v[0].z, (uint32_t)q.v[0].w,
+                                (uint32_t)q.v[1].x, (uint32_t)q.v[1].y, (uint32_t)q.v[1].z, (uint32_t)q.v[1].w,
+                                (uint32_t)q.v[2].x, (uint32_t)q.v[2].y, (uint32_t)q.v[2].z, (uint32_t)q.v[2].w,
+                                (uint32_t)q.v[3].x, (uint32_t)q.v[3].y, (uint32_t)q.v[3].z, (uint32_t)q.v[3].w,
+                                (uint32_t)q.e};
         XQ80 r;
         q8_0_pair_from_dwords(r, w);
-        P::x_from_pair(x, r);
+        P::x_from_pair(x[j], r);
     }
-    float acc0 = 0.0f, acc1 = 0.0f;
+    float acc[2 * NX];   // token j, row r at 2 j + r
+    #pragma unroll
+    for (int i = 0; i < 2 * NX; i++) acc[i] = 0.0f;
     if (act) {
         typename F::Wt w;
         P::load_w(w, buf, c);
-        acc0 = F::dot(w, x, c);
+        #pragma unroll
+        for (int j = 0; j < NX; j++) acc[2 * j] = F::dot(w, x[j], c);
     }
     wait_vmcnt<0>();
     asm volatile("" ::: "memory");
     if (act) {
         typename F::Wt w;
         P::load_w(w, buf + rb, c);
-        acc1 = F::dot(w, x, c);
+        #pragma unroll
+        for (int j = 0; j < NX; j++) acc[2 * j + 1] = F::dot(w, x[j], c);
     }
-    const float v = reduce4(acc0, acc1, 0.0f, 0.0f);
-    if ((l & 31) == 0) {
-        const int rr = l >> 5;
-        if (row0 + rr < n_rows) y[row0 + rr] = v;
+    if constexpr (NX == 1) {
+        const float v = reduce4(acc[0], acc[1], 0.0f, 0.0f);
+        if ((l & 31) == 0) {
+            const int rr = l >> 5;
+            if (row0 + rr < n_rows) y[row0 + rr] = v;
+        }
+    } else {
+        constexpr int NA = 2 * NX;
+        #pragma unroll
+        for (int g = 0; g < NA; g += 4) {
+            const float v = reduce4(acc[g], acc[g + 1], g + 2 < NA ? acc[g + 2] : 0.0f, g + 3 < NA ? acc[g + 3] : 0.0f);
+            if ((l & 15) == 0) {
+                const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
+                const int j = f >> 1, rr = f & 1;
+                if (f < NA && row0 + rr < n_rows) y[(size_t)j * n_rows + row0 + rr] = v;
+            }
+        }
     }
 }
 
@@ -571,12 +595,20 @@ static bool pair32_path(const void* W, size_t n_rows, size_t k, int blk_bytes) {
 }
 
 template <class P>
-static hipError_t pair32_launch(const void* W, size_t n_rows, size_t k, const void* xq, float* y, hipStream_t s) {
+static hipError_t pair32_launch(const void* W, size_t n_rows, size_t k, const void* xq, float* y, hipStream_t s,
+                                size_t m) {
     constexpr int WAVES = 4;
-    hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES>), dim3((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))),
-                       dim3(WAVES * 64), 0, s, static_cast<const uint8_t*>(W),
-                       (uint32_t)(n_rows * (k / 32 * P::F::ROW_BLOCK_BYTES)), static_cast<const uint8_t*>(xq), y,
-                       (int)n_rows, (int)(k / 32));
+    const dim3 grid((unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES))), block(WAVES * 64);
+    const uint8_t* w8 = static_cast<const uint8_t*>(W);
+    const uint8_t* x8 = static_cast<const uint8_t*>(xq);
+    const uint32_t wb = (uint32_t)(n_rows * (k / 32 * P::F::ROW_BLOCK_BYTES)), xrb = (uint32_t)(k / 32 * Q8_0_BYTES);
+    const int n = (int)n_rows, nb = (int)(k / 32);
+    switch (m) {
+    case 1: hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 1>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+    case 2: hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 2>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+    case 3: hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 3>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+    default: hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 4>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
+    }
     return hipGetLastError();
 }
 
@@ -692,13 +724,13 @@ hipError_t gemv_dma_launch(int w_type, const void* W, size_t n_rows, size_t k, c
         return dispatch_dma<DQ6K>(W, n_rows, k, xq, y, s, Q6_K_BYTES, Q8_K_BYTES, m);
     case TYPE_Q4_K: return dispatch_dma<DQ4K>(W, n_rows, k, xq, y, s, Q4_K_BYTES, Q8_K_BYTES, m);
     case TYPE_Q4_0:
-        if (m == 1 && pair32_path(W, n_rows, k, Q4_0_BYTES)) return pair32_launch<DQ40>(W, n_rows, k, xq, y, s);
+        if (m <= 4 && pair32_path(W, n_rows, k, Q4_0_BYTES)) return pair32_launch<DQ40>(W, n_rows, k, xq, y, s, m);
         return dispatch_dma<DQ40>(W, n_rows, k, xq, y, s, Q4_0_BYTES, Q8_0_BYTES, m);
     case TYPE_Q8_0:
-        if (m == 1 && pair32_path(W, n_rows, k, Q8_0_BYTES)) return pair32_launch<DQ80>(W, n_rows, k, xq, y, s);
+        if (m <= 4 && pair32_path(W, n_rows, k, Q8_0_BYTES)) return pair32_launch<DQ80>(W, n_rows, k, xq, y, s, m);
         return dispatch_dma<DQ80>(W, n_rows, k, xq, y, s, Q8_0_BYTES, Q8_0_BYTES, m);
     case TYPE_Q4_0_BARQ:
-        if (m == 1 && pair32_path(W, n_rows, k, Q4_0_BARQ_BYTES)) return pair32_launch<DQ40B>(W, n_rows, k, xq, y, s);
+        if (m <= 4 && pair32_path(W, n_rows, k, Q4_0_BARQ_BYTES)) return pair32_launch<DQ40B>(W, n_rows, k, xq, y, s, m);
         return dispatch_dma<DQ40B>(W, n_rows, k, xq, y, s, Q4_0_BARQ_BYTES, Q8_0_BYTES, m);
     default: return hipErrorInvalidValue;
     }

@@ -266,6 +266,31 @@ def test_gemv_q6_k_pairs_multi_equal_one_token_gemv(be, orc):
 
 
 @pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_0_BARQ"])
+def test_gemv_32_element_pairs_multi_equal_one_token_gemv(be, orc, name):
+    """2-4 activation rows on the two-row GEMV of the 32-element formats (the
+    default for k <= 4096): row j equals the one-token GEMV of activation
+    row j bit for bit; the LDS-streamed multi-token GEMV (BARQ_GEMV_LDS=0)
+    and the oracle within the bar."""
+    from conftest import assert_bits_equal
+    t = getattr(B, name)
+    at = B.Q8_PARTNER[t]
+    for n, k in [(300, 4096), (129, 2048), (1, 256), (8201, 1024)]:
+        for m in (2, 3, 4):
+            print(name, "pair multi", n, k, m, flush=True)
+            w, xq, ref = matmul_case(orc, t, n, k, m, 2900 + n + k + m)
+            wd, xd = dev(w), dev(xq)
+            rb = B.row_bytes(at, k)
+            one = [be.matvec(t, wd, n, k, at, xd[j * rb:(j + 1) * rb]).cpu().numpy() for j in range(m)]
+            got = be.matmul(t, wd, n, k, at, xd, m).cpu().numpy().reshape(m, n)
+            with env(BARQ_GEMV_LDS=0) as b:
+                base = b.matmul(t, wd, n, k, at, xd, m).cpu().numpy().reshape(m, n)
+            for j in range(m):
+                assert_bits_equal(got[j], one[j])
+            assert_close_1e3(got, ref)
+            assert_close_1e3(base, ref)
+
+
+@pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_gemv_32_element_pairs_equal_dma_gemv(be, orc, name):
     """The two-row LDS-staged GEMV of the 32-element formats (the default for
     k <= 4096) against the LDS-streamed one-row-per-wave GEMV
