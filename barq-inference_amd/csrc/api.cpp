@@ -609,6 +609,10 @@ int ffn_dev(barq_rocm_handle* h, int gt, const void* gate, int ut, const void* u
         // gate and up in one launch, SwiGLU in its epilogue
         BARQ_CHECK(launched(barq::gemv_glu_launch(gt, gate, up, n_ff, n_embd, xq, g, s), "gemv_glu"));
         BARQ_CHECK(launched(quantize_act_dev(pd, g, 1, n_ff, hq, s), "quantize_act"));
+    } else if (gt == ut && barq::gemv_glu_multi_supported(gt, gate, up, n_ff, n_embd, m)) {
+        // 2-4 tokens: the same launch over every row (weights read once)
+        BARQ_CHECK(launched(barq::gemv_glu_launch(gt, gate, up, n_ff, n_embd, xq, g, s, m), "gemv_glu"));
+        BARQ_CHECK(launched(quantize_act_dev(pd, g, m, n_ff, hq, s), "quantize_act"));
     } else {
         BARQ_CHECK(matmul_dev(h, gt, gate, n_ff, n_embd, pa, xq, m, g, mm));
         BARQ_CHECK(matmul_dev(h, ut, up, n_ff, n_embd, pa, xq, m, u, mm));

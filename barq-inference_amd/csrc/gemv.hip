@@ -547,10 +547,16 @@ void gemv_q8_glu_kernel(const uint8_t* __restrict__ G, const uint8_t* __restrict
 // gemv_q8_glu_kernel<FmtQ4K, 1, ...>'s, so h is bit-identical.
 constexpr int GLU_LDS_BUF = 6 * 1024;
 
-template <int WAVES>
+//
+// NX = 2-4 activation rows (x_row_bytes apart; h is [NX x n_rows]): the wave
+// loads its lanes' slice of every row ahead of the copies and computes each
+// token's g and u the same way, so h[j] equals the one-token launch's h for
+// activation row j bit for bit.
+template <int WAVES, int NX = 1>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restrict__ U, uint32_t m_bytes,
-                         const uint8_t* __restrict__ xq, float* __restrict__ h, int n_rows, int nblk) {
+                         const uint8_t* __restrict__ xq, float* __restrict__ h, int n_rows, int nblk,
+                         uint32_t x_row_bytes) {
     using F = FmtQ4K;
     __shared__ __attribute__((aligned(16))) uint8_t lds[WAVES][GLU_LDS_BUF];
     const int l = threadIdx.x & 63;
@@ -558,8 +564,9 @@ void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restric
     const int row = wg_rows_remap<WAVES>(blockIdx.x, gridDim.x) * WAVES + wave;
     if (row >= n_rows) return;
     uint8_t* buf = lds[wave];
-    Q4KXRaw xr;
-    q4k_x_issue(xr, xq, min(l >> 2, nblk - 1), l & 3);
+    Q4KXRaw xr[NX];
+    #pragma unroll
+    for (int j = 0; j < NX; j++) q4k_x_issue(xr[j], xq + (size_t)j * x_row_bytes, min(l >> 2, nblk - 1), l & 3);
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, base = (uint32_t)row * rb;
     const i32x4v gs = make_rsrc4(G, m_bytes), us = make_rsrc4(U, m_bytes);
     #pragma unroll
@@ -577,16 +584,20 @@ void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restric
     const bool act = F::active(0, c, nblk);
     wait_vmcnt<3>();   // the activation and the gate row's copies
     asm volatile("" ::: "memory");
-    F::X xs;
-    q4k_x_ready(xr, xs);
+    F::X xs[NX];
+    #pragma unroll
+    for (int j = 0; j < NX; j++) q4k_x_ready(xr[j], xs[j]);
     const uint8_t* b = buf + Q4_K_BYTES * c.sbl;
-    float acc_g = 0.0f, acc_u = 0.0f;
+    float acc[2 * NX];   // token j: g at 2 j, u at 2 j + 1
+    #pragma unroll
+    for (int i = 0; i < 2 * NX; i++) acc[i] = 0.0f;
     if (act) {
         F::Wt w;
         w.hdr = *reinterpret_cast<const uint4*>(b);
         w.q0 = *reinterpret_cast<const uint4*>(b + 16 + 32 * c.p);
         w.q1 = *reinterpret_cast<const uint4*>(b + 32 + 32 * c.p);
-        acc_g = F::dot(w, xs, c);
+        #pragma unroll
+        for (int j = 0; j < NX; j++) acc[2 * j] = F::dot(w, xs[j], c);
     }
     wait_vmcnt<0>();
     asm volatile("" ::: "memory");
@@ -595,12 +606,19 @@ void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restric
         w.hdr = *reinterpret_cast<const uint4*>(b + 3072);
         w.q0 = *reinterpret_cast<const uint4*>(b + 3072 + 16 + 32 * c.p);
         w.q1 = *reinterpret_cast<const uint4*>(b + 3072 + 32 + 32 * c.p);
-        acc_u = F::dot(w, xs, c);
+        #pragma unroll
+        for (int j = 0; j < NX; j++) acc[2 * j + 1] = F::dot(w, xs[j], c);
     }
-    // lane 0: g, lane 32: u
-    const float v = reduce4(acc_g, acc_u, 0.0f, 0.0f);
-    const float other = __shfl_xor(v, 32);
-    if (l == 0) h[row] = ffn_swiglu(v, other);
+    // per group of two tokens: lane 0 g and lane 32 u of the first, lanes 16
+    // and 48 those of the second
+    #pragma unroll
+    for (int t = 0; t < NX; t += 2) {
+        const float v = reduce4(acc[2 * t], acc[2 * t + 1], t + 1 < NX ? acc[2 * t + 2] : 0.0f,
+                                t + 1 < NX ? acc[2 * t + 3] : 0.0f);
+        const float other = __shfl_xor(v, 32);
+        if (l == 0) h[(size_t)t * n_rows + row] = ffn_swiglu(v, other);
+        if (t + 1 < NX && l == 16) h[(size_t)(t + 1) * n_rows + row] = ffn_swiglu(v, other);
+    }
 }
 
 // A few activation rows (2-4 tokens of a small decode batch): each wave's
@@ -1106,8 +1124,29 @@ static hipError_t launch_glu(const uint8_t* G, const uint8_t* U, size_t rb, cons
     return hipGetLastError();
 }
 
+bool gemv_glu_multi_supported(int w_type, const void* G, const void* U, size_t n_rows, size_t k, size_t m) {
+    return m >= 2 && m <= 4 && gemv_glu_supported(w_type, G, U, n_rows, k) && k <= 4096 &&
+           n_rows * (k / 256 * 144) < 0x80000000ull && tuning_env(TUNE_GEMV_LDS, 1) != 0;
+}
+
 hipError_t gemv_glu_launch(int w_type, const void* G, const void* U, size_t n_rows, size_t k, const void* xq, float* h,
-                           hipStream_t s) {
+                           hipStream_t s, size_t m) {
+    if (m > 1) {
+        if (!gemv_glu_multi_supported(w_type, G, U, n_rows, k, m)) return hipErrorInvalidValue;
+        constexpr int WAVES = 4;
+        const dim3 grid((unsigned)((n_rows + WAVES - 1) / WAVES)), block(WAVES * 64);
+        const uint8_t* g = static_cast<const uint8_t*>(G);
+        const uint8_t* u = static_cast<const uint8_t*>(U);
+        const uint8_t* x = static_cast<const uint8_t*>(xq);
+        const uint32_t mb = (uint32_t)(n_rows * (k / 256 * 144)), xrb = (uint32_t)(k / 256 * Q8_K_BYTES);
+        const int n = (int)n_rows, nb = (int)(k / 256);
+        switch (m) {
+        case 2: hipLaunchKernelGGL((gemv_glu_lds_kernel<WAVES, 2>), grid, block, 0, s, g, u, mb, x, h, n, nb, xrb); break;
+        case 3: hipLaunchKernelGGL((gemv_glu_lds_kernel<WAVES, 3>), grid, block, 0, s, g, u, mb, x, h, n, nb, xrb); break;
+        default: hipLaunchKernelGGL((gemv_glu_lds_kernel<WAVES, 4>), grid, block, 0, s, g, u, mb, x, h, n, nb, xrb); break;
+        }
+        return hipGetLastError();
+    }
     if (!gemv_glu_supported(w_type, G, U, n_rows, k)) return hipErrorInvalidValue;
     const uint8_t* g = static_cast<const uint8_t*>(G);
     const uint8_t* u = static_cast<const uint8_t*>(U);
@@ -1118,8 +1157,8 @@ hipError_t gemv_glu_launch(int w_type, const void* G, const void* U, size_t n_ro
     // box): the whole FFN 23.98-24.03 against 25.09-25.12 us
     if (k <= 4096 && n_rows * rb < 0x80000000ull && tuning_env(TUNE_GEMV_LDS, 1) != 0) {
         constexpr int WAVES = 4;
-        hipLaunchKernelGGL((gemv_glu_lds_kernel<WAVES>), dim3((unsigned)((n + WAVES - 1) / WAVES)), dim3(WAVES * 64), 0,
-                           s, g, u, (uint32_t)(n_rows * rb), x, h, n, kk / 256);
+        hipLaunchKernelGGL((gemv_glu_lds_kernel<WAVES, 1>), dim3((unsigned)((n + WAVES - 1) / WAVES)), dim3(WAVES * 64),
+                           0, s, g, u, (uint32_t)(n_rows * rb), x, h, n, kk / 256, 0u);
         return hipGetLastError();
     }
     // BARQ_GEMV_GLU = 10 * P + W: P outputs per wave (1 or 2), W waves (2, 4, 8)

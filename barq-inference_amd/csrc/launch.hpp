@@ -59,8 +59,11 @@ hipError_t moe_gemv_launch(int w_type, const void* const* W, size_t n_experts, s
 // Gate and up of one Q8_K row in one launch with the dense SwiGLU in the
 // epilogue: h[n_rows] (Q4_K weights, 16-byte aligned)
 bool gemv_glu_supported(int w_type, const void* G, const void* U, size_t n_rows, size_t k);
+// m = 2-4 activation rows (x_row_bytes apart, h [m x n_rows]): the
+// LDS-staged launch only (gemv_glu_multi_supported)
 hipError_t gemv_glu_launch(int w_type, const void* G, const void* U, size_t n_rows, size_t k, const void* xq, float* h,
-                           hipStream_t s);
+                           hipStream_t s, size_t m = 1);
+bool gemv_glu_multi_supported(int w_type, const void* G, const void* U, size_t n_rows, size_t k, size_t m);
 // 2-4 Q8 activation rows at once (y[m x n_rows]): the weights read once
 bool gemv_multi_supported(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m);
 hipError_t gemv_q8_multi_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq, size_t m,

@@ -149,6 +149,31 @@ def test_ffn_lds_gate_up_equals_register_gate_up(be, orc):
         assert_close_chained(got, ref)
 
 
+def test_ffn_small_batch_equals_one_token_ffn(be, orc):
+    """2-4 tokens (gate and up in one launch over every row, then h's
+    quantizer and the down GEMV over every row): each token's output equals
+    the one-token FFN of that row bit for bit, and the oracle within the
+    chained bar.  n_ff is a multiple of 512, so the Q6_K down projection of
+    2-4 tokens is a GEMV too (otherwise 3-4 tokens take the MFMA GEMM, whose
+    sums are ordered differently)."""
+    from conftest import assert_bits_equal
+    for n_embd, n_ff in [(4096, 14336), (1024, 2560), (768, 512)]:
+        gate, up, down, _ = ffn_case(n_embd, n_ff, 1, 520 + n_embd, B.Q4_K, B.Q4_K, B.Q6_K)
+        gd, ud, dd = dev(gate), dev(up), dev(down)
+        for m in (2, 3, 4):
+            print(f"ffn small batch {n_embd} {n_ff} m={m}", flush=True)
+            x = synth.gen_f32(m * n_embd, 530 + m).reshape(m, n_embd)
+            xq = orc.quantize_act(B.Q8_K, x)
+            got = host(be.ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, n_embd, n_ff, B.Q8_K, dev(xq), m))
+            rb = B.row_bytes(B.Q8_K, n_embd)
+            for j in range(m):
+                one = host(be.ffn(B.Q4_K, gd, B.Q4_K, ud, B.Q6_K, dd, n_embd, n_ff, B.Q8_K,
+                                  dev(xq[j * rb:(j + 1) * rb]), 1))
+                assert_bits_equal(got[j], one[0])
+            ref = orc.ffn(B.Q4_K, gate, B.Q4_K, up, B.Q6_K, down, n_embd, n_ff, orc.Q8_K, xq, m)
+            assert_close_chained(got, ref)
+
+
 @pytest.mark.parametrize("m", [1, 3])
 def test_ffn_literal_f32(be, orc, m):
     n_embd, n_ff = 1024, 2816
