@@ -61,7 +61,9 @@ def parse():
     p.add_argument("--q-len", type=int, default=1, help="--attn: new tokens per call (1 = decode; > 1 = a prompt chunk)")
     p.add_argument("--ffn", action="store_true",
                    help="time the dense FFN (feed_forward: gate/up Q4_K, SwiGLU, down Q6_K) at Llama-3-8B shapes")
-    p.add_argument("--m", type=int, default=1, help="--ffn: tokens per call; --prefill: prompt tokens (default 512)")
+    p.add_argument("--m", type=int, default=1,
+                   help="--ffn: tokens per call; --prefill: prompt tokens (default 512); "
+                        "configs 1-3: 2-4 activation rows on the same weights (a small decode batch)")
     p.add_argument("--decode", action="store_true",
                    help="a whole Llama-3-8B decode token (32 layers, output norm, LM head) over --kv-len cached positions")
     p.add_argument("--prefill", action="store_true",
@@ -959,8 +961,11 @@ def main():
     cfg = synth.CONFIGS[args.config]
     w_type, n, k, m = cfg["w_type"], cfg["n_rows"], cfg["k"], cfg["m"]
     workload = cfg["name"]
+    if args.m > 1 and args.config in (1, 2, 3):
+        m = args.m
+        workload = f"{cfg['name']}, {m} activation rows (small decode batch)"
     log(f"generating {cfg['name']}")
-    t, w, x = synth.linear_inputs(args.config)
+    t, w, x = synth.linear_inputs(args.config, m=m)
     if args.w_type:
         # the same shape and activation with weights of another format
         w_type = getattr(B, args.w_type)
@@ -1089,12 +1094,13 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log("copy probe: 5 x 256 MiB device copies")
-    if not args.no_traffic:
+    small_batch = args.config in (1, 2, 3) and m > 1   # the counter runs and the CPU sample are one-token
+    if not args.no_traffic and not small_batch:
         log("measuring HBM traffic per launch (rocprofv3 --pmc child runs)")
         traffic, detail = measure_traffic(args.config, args.w_type)
         result["roofline"]["traffic"] = round(traffic) if traffic else None
         result["roofline"]["traffic_detail"] = detail
-    if not args.no_cpu:
+    if not args.no_cpu and not small_batch:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(w_type, w, x[0], n, k, args.cpu_seconds, alg)
     be.close()
