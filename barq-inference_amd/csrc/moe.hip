@@ -90,8 +90,11 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
 hipError_t moe_route_launch(const float* logits, size_t rows, size_t n_experts, size_t top_k,
                             int32_t* ids, float* weights, hipStream_t s, size_t max_active, float min_weight) {
     if (rows == 0) return hipSuccess;
+    // keep_max in [1, top_k] when reducing (a "no cap" max_active such as
+    // usize::MAX keeps every slot), 0 = route only
+    const int keep = max_active == 0 ? 0 : (int)(max_active < top_k ? max_active : top_k);
     hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, logits,
-                       (int)rows, (int)n_experts, (int)top_k, (int)max_active, min_weight, ids, weights);
+                       (int)rows, (int)n_experts, (int)top_k, keep, min_weight, ids, weights);
     return hipGetLastError();
 }
 
@@ -117,8 +120,10 @@ __global__ __launch_bounds__(64) void moe_reduce_kernel(const int32_t* ids, cons
 hipError_t moe_reduce_launch(const int32_t* ids, const float* weights, size_t rows, size_t k, size_t max_active,
                              float min_weight, int32_t* out_ids, float* out_weights, hipStream_t s) {
     if (rows == 0) return hipSuccess;
+    // keep_max = clamp(max_active, 1, k): a "no cap" value keeps every slot
+    const int keep = max_active == 0 ? 1 : (int)(max_active < k ? max_active : k);
     hipLaunchKernelGGL(moe_reduce_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(64), 0, s, ids, weights,
-                       (int)rows, (int)k, (int)(max_active > 0 ? max_active : 1), min_weight, out_ids, out_weights);
+                       (int)rows, (int)k, keep, min_weight, out_ids, out_weights);
     return hipGetLastError();
 }
 

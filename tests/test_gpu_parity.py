@@ -322,6 +322,17 @@ def test_moe_route_reduce_and_reduce(be, orc):
                            mem=B.MEM_HOST)
     assert gi.tolist() == [[0, 1, -1], [2, 1, -1]]
     assert np.all(np.abs(gw.sum(1) - 1.0) < 1e-6)
+    # "no cap" (usize::MAX, or anything >= 2^31): every slot above the
+    # threshold is kept and renormalised, as in the oracle
+    for cap in (2**64 - 1, 2**31, k + 1):
+        ref_i, ref_w = orc.moe_reduce_experts(rid, rw, cap, 0.05)
+        assert (ref_i[:, 2] >= 0).sum() > 10
+        gi, gw = be.moe_reduce(dev(rid), dev(rw), cap, 0.05)
+        assert np.array_equal(host(gi), ref_i)
+        assert_bits_equal(host(gw), ref_w)
+        fi, fw = be.moe_route_reduce(dev(logits), rows, ne, k, cap, 0.05)
+        assert np.array_equal(host(fi), ref_i)
+        assert np.allclose(host(fw), ref_w, rtol=1e-6, atol=1e-7)
 
 
 def test_moe_ffn_after_reduction(be, orc):
