@@ -52,8 +52,8 @@ EXPORTS = (
     "barq_rocm_create", "barq_rocm_destroy", "barq_rocm_last_error", "barq_rocm_set_stream",
     "barq_rocm_get_stream", "barq_rocm_synchronize", "barq_rocm_abi_version",
     "barq_rocm_block_elems", "barq_rocm_block_bytes", "barq_rocm_row_bytes",
-    "barq_rocm_dequantize", "barq_rocm_quantize_act", "barq_rocm_rms_norm", "barq_rocm_rms_norm_quantize",
-    "barq_rocm_add_rms_norm_quantize",
+    "barq_rocm_dequantize", "barq_rocm_get_rows", "barq_rocm_quantize_act", "barq_rocm_rms_norm",
+    "barq_rocm_rms_norm_quantize", "barq_rocm_add_rms_norm_quantize", "barq_rocm_add_bias",
     "barq_rocm_matvec", "barq_rocm_matmul", "barq_rocm_swiglu", "barq_rocm_ffn",
     "barq_rocm_gemm_f32", "barq_rocm_gemv_f32", "barq_rocm_dequantize_split",
     "barq_rocm_quantized_matmul_split", "barq_rocm_quantize_q4_0_barq", "barq_rocm_quantize_q4_k_barq",
@@ -104,6 +104,8 @@ def _declare(lib):
         "barq_rocm_block_bytes": (_sz, [_i]),
         "barq_rocm_row_bytes": (_sz, [_i, _sz]),
         "barq_rocm_dequantize": (_i, [_vp, _i, _vp, _sz, _vp, _i]),
+        "barq_rocm_get_rows": (_i, [_vp, _i, _vp, _sz, _sz, _vp, _sz, _vp, _i]),
+        "barq_rocm_add_bias": (_i, [_vp, _vp, _vp, _sz, _sz, _i]),
         "barq_rocm_quantize_act": (_i, [_vp, _i, _vp, _sz, _sz, _vp, _i]),
         "barq_rocm_rms_norm": (_i, [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i]),
         "barq_rocm_rms_norm_quantize": (_i, [_vp, _i, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i]),

@@ -94,6 +94,28 @@ class Backend:
             self.sync()
         return out
 
+    def get_rows(self, type_, table, n_rows, k, tokens, mem=L.MEM_DEVICE, sync=True, out=None):
+        """get_embeddings (transformer.rs:96-119): the decoded rows `tokens` of
+        an n_rows x k table; out-of-range ids give zero rows."""
+        n = len(tokens)
+        if out is None:
+            if mem == L.MEM_HOST:
+                out = np.empty((n, k), np.float32)
+            else:
+                import torch
+                out = torch.empty((n, k), dtype=torch.float32, device=tokens.device)
+        L.check(self._lib.barq_rocm_get_rows(self.h, type_, _ptr(table), n_rows, k, _ptr(tokens), n, _ptr(out), mem))
+        if sync and mem == L.MEM_DEVICE:
+            self.sync()
+        return out
+
+    def add_bias(self, y, bias, rows, dim, mem=L.MEM_DEVICE, sync=True):
+        """add_bias (transformer.rs:444-465): y[r, j] += bias[j] in place."""
+        L.check(self._lib.barq_rocm_add_bias(self.h, _ptr(y), _ptr(bias), rows, dim, mem))
+        if sync and mem == L.MEM_DEVICE:
+            self.sync()
+        return y
+
     def quantize_act(self, act_type, x, sync=True):
         import torch
         rows, k = (1, x.numel()) if x.dim() == 1 else tuple(x.shape)

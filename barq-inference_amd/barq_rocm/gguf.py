@@ -99,6 +99,15 @@ class WeightCache:
                                               ctypes.byref(k), ctypes.byref(p)))
         return t.value, n.value, k.value, p.value
 
+    def find(self, name: str):
+        """get(name), or None when the file has no such tensor."""
+        t, n, k, p = ctypes.c_int(), ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_void_p()
+        rc = self._lib.barq_rocm_cache_get(self.c, name.encode(), ctypes.byref(t), ctypes.byref(n),
+                                           ctypes.byref(k), ctypes.byref(p))
+        if rc != L.OK:
+            return None
+        return t.value, n.value, k.value, p.value
+
     def nbytes(self) -> int:
         return self._lib.barq_rocm_cache_bytes(self.c)
 

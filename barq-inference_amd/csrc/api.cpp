@@ -216,6 +216,69 @@ int barq_rocm_dequantize(barq_rocm_handle* h, int type, const void* blocks, size
     return ok();
 }
 
+int barq_rocm_get_rows(barq_rocm_handle* h, int type, const void* table, size_t n_rows, size_t k,
+                       const int32_t* tokens, size_t n_tokens, float* out, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (type == BARQ_TYPE_Q4_K_BARQ || (type != BARQ_TYPE_F32 && !blk_elems(type)))
+        return fail(BARQ_E_UNSUPPORTED, "get_rows: unsupported type %d", type);
+    const size_t rb = type == BARQ_TYPE_F32 ? k * 4 : row_bytes_of(type, k);
+    if (k % 4 || (k && !rb))
+        return fail(BARQ_E_QUANT, "get_rows: k=%zu is not a whole number of blocks (and of 4 elements)", k);
+    if (n_tokens == 0 || k == 0) return ok();
+    if (!table || !tokens || !out) return fail(BARQ_E_INVALID, "get_rows: null buffer");
+    if (n_rows > UINT32_MAX || k / 4 > UINT32_MAX) return fail(BARQ_E_DIM, "get_rows: table of %zu x %zu is too large", n_rows, k);
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    if (mem == BARQ_MEM_DEVICE) {
+        const size_t ta = type == BARQ_TYPE_F32 ? 16 : type == BARQ_TYPE_F16 ? 8 : weight_align(type);
+        if (!aligned(table, ta) || !aligned(tokens, 4) || !aligned(out, 16))
+            return fail(BARQ_E_INVALID, "get_rows: misaligned buffer (table %zu-byte, tokens 4-byte, out 16-byte)", ta);
+        return launched(barq::get_rows_launch(type, table, rb, n_rows, k, tokens, n_tokens, out, h->stream), "get_rows");
+    }
+    // host buffers: only the rows the tokens name travel (slot j holds the
+    // j-th in-range token's row; the others map to -1 and stay zero)
+    std::vector<int32_t> ids(n_tokens);
+    size_t used = 0;
+    for (size_t t = 0; t < n_tokens; t++)
+        ids[t] = tokens[t] >= 0 && (size_t)tokens[t] < n_rows ? (int32_t)used++ : -1;
+    Arena a;
+    const size_t orows = a.add(used * rb), oid = a.add(n_tokens * 4), oo = a.add(n_tokens * k * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    const uint8_t* tb = static_cast<const uint8_t*>(table);
+    for (size_t t = 0; t < n_tokens; t++)
+        if (ids[t] >= 0)
+            BARQ_HIP(hipMemcpyAsync(at<uint8_t>(h, orows) + (size_t)ids[t] * rb, tb + (size_t)tokens[t] * rb, rb,
+                                    hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<int32_t>(h, oid), ids.data(), n_tokens * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::get_rows_launch(type, at<uint8_t>(h, orows), rb, used, k, at<int32_t>(h, oid), n_tokens,
+                                              at<float>(h, oo), h->stream), "get_rows"));
+    BARQ_HIP(hipMemcpyAsync(out, at<float>(h, oo), n_tokens * k * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
+int barq_rocm_add_bias(barq_rocm_handle* h, float* y, const float* bias, size_t rows, size_t dim, int mem) {
+    BARQ_CHECK(check_mem(mem));
+    if (rows == 0 || dim == 0) return ok();
+    if (!y || !bias) return fail(BARQ_E_INVALID, "add_bias: null buffer");
+    if (dim > UINT32_MAX) return fail(BARQ_E_DIM, "add_bias: dim %zu exceeds 2^32", dim);
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    if (mem == BARQ_MEM_DEVICE) {
+        if (!aligned(y, 4) || !aligned(bias, 4)) return fail(BARQ_E_INVALID, "add_bias: misaligned buffer");
+        return launched(barq::add_bias_launch(y, bias, rows, dim, h->stream), "add_bias");
+    }
+    Arena a;
+    const size_t oy = a.add(rows * dim * 4), ob = a.add(dim * 4);
+    BARQ_CHECK(ensure_ws(h, a.used));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, oy), y, rows * dim * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_HIP(hipMemcpyAsync(at<float>(h, ob), bias, dim * 4, hipMemcpyHostToDevice, h->stream));
+    BARQ_CHECK(launched(barq::add_bias_launch(at<float>(h, oy), at<float>(h, ob), rows, dim, h->stream), "add_bias"));
+    BARQ_HIP(hipMemcpyAsync(y, at<float>(h, oy), rows * dim * 4, hipMemcpyDeviceToHost, h->stream));
+    BARQ_HIP(hipStreamSynchronize(h->stream));
+    return ok();
+}
+
 static hipError_t quantize_act_dev(int act_type, const float* x, size_t n_rows, size_t k, void* out, hipStream_t s) {
     return act_type == BARQ_TYPE_Q8_0 ? barq::quantize_q8_0_launch(x, n_rows, k, out, s)
                                       : barq::quantize_q8_k_launch(x, n_rows, k, out, s);

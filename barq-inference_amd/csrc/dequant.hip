@@ -156,6 +156,62 @@ hipError_t dequant_launch(int type, const void* blocks, size_t n_elems, float* o
     return hipGetLastError();
 }
 
+// ---- get_embeddings (models/src/transformer.rs:96-119) ---------------------
+// Output row t is row tokens[t] of the table decoded as dequant_kernel
+// decodes it (the same deq4_at, so bit-identical to decoding the whole
+// table and copying the row); ids outside [0, n_rows) give a zero row, as
+// the reference leaves those rows of its zero-initialised output.  One
+// workgroup column per token (grid.y), k4 = k / 4 float4 outputs per row.
+template <int TYPE>
+__global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t* __restrict__ table, size_t row_bytes,
+                                                       uint32_t n_rows, const int32_t* __restrict__ tokens,
+                                                       float4* __restrict__ out, uint32_t k4) {
+    const int32_t id = tokens[blockIdx.y];
+    const bool in = id >= 0 && (uint32_t)id < n_rows;
+    const uint8_t* row = table + (size_t)(in ? id : 0) * row_bytes;
+    float4* o = out + (size_t)blockIdx.y * k4;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < k4; i += gridDim.x * 256) {
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (in) {
+            if constexpr (TYPE == TYPE_F32) {
+                const float4 f = reinterpret_cast<const float4*>(row)[i];
+                v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            } else {
+                deq4_at<TYPE>(row, (size_t)i * 4, v);
+            }
+        }
+        o[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+hipError_t get_rows_launch(int type, const void* table, size_t row_bytes, size_t n_rows, size_t k,
+                           const int32_t* tokens, size_t n_tokens, float* out, hipStream_t s) {
+    const uint8_t* src = static_cast<const uint8_t*>(table);
+    const uint32_t k4 = (uint32_t)(k / 4);
+    if (n_tokens == 0 || k4 == 0) return hipSuccess;
+    const unsigned gx = (unsigned)((k4 + 255) / 256 < 64 ? (k4 + 255) / 256 : 64);
+    for (size_t t0 = 0; t0 < n_tokens; t0 += 65535) {
+        const dim3 g(gx, (unsigned)(n_tokens - t0 < 65535 ? n_tokens - t0 : 65535)), b(256);
+        float4* o = reinterpret_cast<float4*>(out + t0 * k);
+        const int32_t* tk = tokens + t0;
+        const uint32_t nr = (uint32_t)n_rows;
+        switch (type) {
+        case TYPE_F32: hipLaunchKernelGGL(get_rows_kernel<TYPE_F32>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_F16: hipLaunchKernelGGL(get_rows_kernel<TYPE_F16>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_Q4_0: hipLaunchKernelGGL(get_rows_kernel<TYPE_Q4_0>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_Q4_0_BARQ: hipLaunchKernelGGL(get_rows_kernel<TYPE_Q4_0_BARQ>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_Q8_0: hipLaunchKernelGGL(get_rows_kernel<TYPE_Q8_0>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_Q4_K: hipLaunchKernelGGL(get_rows_kernel<TYPE_Q4_K>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_Q6_K: hipLaunchKernelGGL(get_rows_kernel<TYPE_Q6_K>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        case TYPE_Q8_K: hipLaunchKernelGGL(get_rows_kernel<TYPE_Q8_K>, g, b, 0, s, src, row_bytes, nr, tk, o, k4); break;
+        default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 // ---- split-scale decoders of the reference's QuantizedCudaOps --------------
 // backend/src/cuda_quant.rs:44-75 (packed sign-extended nibbles, block b uses
 // scales[b] and quants[b*ceil(bs/2) ..]) and :77-102 (signed bytes,

@@ -9,6 +9,10 @@ namespace barq {
 
 // dequant.hip
 hipError_t dequant_launch(int type, const void* blocks, size_t n_elems, float* out, hipStream_t s);
+// get_embeddings: rows tokens[t] of a table of n_rows rows (k elements,
+// row_bytes each) decoded to f32 rows of out; out-of-range ids give zeros
+hipError_t get_rows_launch(int type, const void* table, size_t row_bytes, size_t n_rows, size_t k,
+                           const int32_t* tokens, size_t n_tokens, float* out, hipStream_t s);
 hipError_t dequant_split_launch(int kind_q8_0, const uint8_t* quants, size_t n_quants,
                                 const float* scales, size_t n_scales, size_t block_size,
                                 float* out, size_t n_out, hipStream_t s);
@@ -41,6 +45,8 @@ hipError_t rms_norm_quantize_launch(int act_type, const float* x, const float* w
 // out_type TYPE_F32 (f32 rows), TYPE_Q8_K or TYPE_Q8_0 (n % 256 == 0)
 hipError_t add_rms_norm_launch(int out_type, const float* x, const float* d, const float* w, size_t rows, size_t n,
                                float eps, float* sum, void* out, hipStream_t s);
+// y[r, j] += bias[j] (rows x dim, in place)
+hipError_t add_bias_launch(float* y, const float* bias, size_t rows, size_t dim, hipStream_t s);
 
 // gemv.hip
 hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, const void* xq,

@@ -203,4 +203,21 @@ hipError_t add_rms_norm_launch(int out_type, const float* x, const float* d, con
                                  : launch_norm<2>(x, d, w, rows, n, eps, sum, out, s);
 }
 
+// add_bias (transformer.rs:444-465) and final_output's output.bias
+// (:487-495): y[r, j] += bias[j], one f32 addition per element.
+__global__ __launch_bounds__(256) void add_bias_kernel(float* __restrict__ y, const float* __restrict__ bias,
+                                                       size_t n, uint32_t dim) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = y[i] + bias[i % dim];
+}
+
+hipError_t add_bias_launch(float* y, const float* bias, size_t rows, size_t dim, hipStream_t s) {
+    const size_t n = rows * dim;
+    if (n == 0) return hipSuccess;
+    const size_t g = (n + 255) / 256;
+    hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)(g < 4096 ? g : 4096)), dim3(256), 0, s, y, bias, n,
+                       (uint32_t)dim);
+    return hipGetLastError();
+}
+
 }  // namespace barq

@@ -519,13 +519,14 @@ def bench_ffn(args):
 
 def bench_decode(args):
     """One decode token of a Llama-3-8B-shaped model (LlamaTransformer::forward
-    for one token: 32 x forward_layer, transformer.rs:123-144, then the output
-    norm and final_output :468-498) on the integer path, all 290 launches of
-    a token captured in one HIP graph.  Each layer runs the decode-layer
-    chain of --layer (9 launches) over its own KV cache of --kv-len cached
-    positions and its own copy of a Q4_K_M layer's weights (32 copies of the
-    same synthetic contents at distinct addresses, 4.4 GB: no cache holds
-    them across layers); the LM head is Q6_K 128256 x 4096.  Synthetic
+    for one token, transformer.rs:81-94: get_embeddings, 32 x forward_layer
+    :123-144, final_output :468-498) on the integer path through
+    barq_rocm.llama.DeviceLlama (the chain tests/test_gpu_token.py checks
+    against the oracle), every launch of a token captured in one HIP graph.
+    Each layer has its own KV cache of --kv-len cached positions and its own
+    copy of a Q4_K_M layer's weights (32 copies of the same synthetic contents
+    at distinct addresses, 4.4 GB: no cache holds them across layers);
+    token_embd Q4_K and the LM head Q6_K are 128256 x 4096.  Synthetic
     weights and activations."""
     import numpy as np
     import torch
@@ -533,85 +534,74 @@ def bench_decode(args):
     import barq_rocm as B
     from barq_rocm import attention as A
     from barq_rocm import synth
+    from barq_rocm.llama import DeviceLlama, LlamaConfig
 
-    n_embd, n_head, n_kv, hd, n_ff, n_layer, n_vocab = 4096, 32, 8, 128, 14336, 32, 128256
+    cfg = LlamaConfig(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336)
+    n_vocab = 128256
     kv_len = args.kv_len
     tokens = args.steps if args.steps <= 16 else 4
-    mats = [("q", B.Q4_K, n_head * hd, n_embd), ("k", B.Q4_K, n_kv * hd, n_embd), ("v", B.Q6_K, n_kv * hd, n_embd),
-            ("o", B.Q4_K, n_embd, n_head * hd), ("gate", B.Q4_K, n_ff, n_embd), ("up", B.Q4_K, n_ff, n_embd),
-            ("down", B.Q6_K, n_embd, n_ff)]
-    log("generating the synthetic layer and LM-head weights")
+    mats = [("attn_q", B.Q4_K, cfg.n_head * cfg.head_dim, cfg.n_embd), ("attn_k", B.Q4_K, cfg.n_head_kv * cfg.head_dim, cfg.n_embd),
+            ("attn_v", B.Q6_K, cfg.n_head_kv * cfg.head_dim, cfg.n_embd), ("attn_output", B.Q4_K, cfg.n_embd, cfg.n_head * cfg.head_dim),
+            ("ffn_gate", B.Q4_K, cfg.n_ff, cfg.n_embd), ("ffn_up", B.Q4_K, cfg.n_ff, cfg.n_embd),
+            ("ffn_down", B.Q6_K, cfg.n_embd, cfg.n_ff)]
+    log("generating the synthetic layer, embedding and LM-head weights")
     host = {nm: synth.gen_weights(t, n, k, 800 + i) for i, (nm, t, n, k) in enumerate(mats)}
-    head_h = synth.gen_weights(B.Q6_K, n_vocab, n_embd, 880)
+    types = {nm: (t, n, k) for nm, t, n, k in mats}
+    head_h = synth.gen_weights(B.Q6_K, n_vocab, cfg.n_embd, 880)
+    emb_h = synth.gen_weights(B.Q4_K, n_vocab, cfg.n_embd, 881)
     wbytes = sum(a.nbytes for a in host.values())
-    copies = n_layer
     be = B.Backend(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     be.set_stream(stream.cuda_stream)
-    layers = [{nm: torch.from_numpy(a).cuda() for nm, a in host.items()} for _ in range(copies)]
-    head = torch.from_numpy(head_h).cuda()
-    del host, head_h
-    norm_w = torch.from_numpy((0.01 * (1.0 + 0.1 * synth.gen_f32(n_embd, 820))).astype(np.float32)).cuda()
-    f = torch.from_numpy(np.array([np.float32(500000.0) ** np.float32(-2.0 * i / hd) for i in range(hd // 2)],
-                                  dtype=np.float32)).cuda()
-    kv = A.KVCache(be, kv_len + 3 * tokens + 8, n_layer, n_kv, hd)
+    tensors, keep = {}, []
+    norm_w = torch.from_numpy((0.01 * (1.0 + 0.1 * synth.gen_f32(cfg.n_embd, 820))).astype(np.float32)).cuda()
+    keep.append(norm_w)
+    for il in range(cfg.n_layer):
+        for nm, a in host.items():
+            d = torch.from_numpy(a).cuda()
+            keep.append(d)
+            tensors[f"blk.{il}.{nm}.weight"] = (*types[nm], d.data_ptr())
+        for nm in ("attn_norm", "ffn_norm"):
+            tensors[f"blk.{il}.{nm}.weight"] = (0, 1, cfg.n_embd, norm_w.data_ptr())
+    for nm, t, a in (("output.weight", B.Q6_K, head_h), ("token_embd.weight", B.Q4_K, emb_h)):
+        d = torch.from_numpy(a).cuda()
+        keep.append(d)
+        tensors[nm] = (t, n_vocab, cfg.n_embd, d.data_ptr())
+    tensors["output_norm.weight"] = (0, 1, cfg.n_embd, norm_w.data_ptr())
+    head_bytes = head_h.nbytes
+    del host, head_h, emb_h
+    kv = A.KVCache(be, kv_len + 3 * tokens + 8, cfg.n_layer, cfg.n_head_kv, cfg.head_dim)
     rng = np.random.default_rng(5)
-    kk = rng.standard_normal((n_kv, kv_len - 1, hd)).astype(np.float32)
+    kk = rng.standard_normal((cfg.n_head_kv, kv_len - 1, cfg.head_dim)).astype(np.float32)
     kkd = torch.from_numpy(kk).cuda()
-    for layer in range(n_layer):   # kv_len - 1 cached positions per layer
-        kv.append(layer, kkd, kkd * 0.5, kv_len - 1, hd)
+    for layer in range(cfg.n_layer):   # kv_len - 1 cached positions per layer
+        kv.append(layer, kkd, kkd * 0.5, kv_len - 1, cfg.head_dim)
     del kkd
-    x0 = torch.from_numpy(synth.gen_f32(n_embd, 821)).cuda().reshape(1, n_embd)
-    zero = torch.zeros((1, n_embd), dtype=torch.float32, device="cuda")
-    bufA, bufB = torch.empty_like(x0), torch.empty_like(x0)
-    nbq = (n_embd // 256) * 292
-    xq, xq2, aq = (torch.empty((1, nbq), dtype=torch.uint8, device="cuda") for _ in range(3))
-    q = torch.empty((1, n_head * hd), dtype=torch.float32, device="cuda")
-    k = torch.empty((1, n_kv * hd), dtype=torch.float32, device="cuda")
-    v = torch.empty((1, n_kv * hd), dtype=torch.float32, device="cuda")
-    qr = torch.empty((n_head, 1, hd), dtype=torch.float32, device="cuda")
-    o = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
-    ff = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
-    logits = torch.empty((1, n_vocab), dtype=torch.float32, device="cuda")
+    llama = DeviceLlama(be, cfg, tensors.get, kv)
+    tok = torch.tensor([1234], dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
     pos = [kv_len - 1]
-    qkv_types = [B.Q4_K, B.Q4_K, B.Q6_K]
 
     def token(i):
-        p0 = pos[0]
-        h, prev = x0, zero
-        for layer in range(n_layer):
-            L = layers[layer % copies]
-            # residual stream: bufB = h + previous FFN output, bufA = bufB + attention output
-            be.add_rms_norm_quantize(B.Q8_K, h, prev, norm_w, 1e-5, sum_out=bufB, out=xq, sync=False)
-            kv.qkv_append_rope(layer, qkv_types, [L["q"], L["k"], L["v"]], n_head, n_embd, B.Q8_K, xq, p0, 1.0, f,
-                               A.ROPE_INTERLEAVED, q_out=qr)
-            A.compute_attention_q8k(be, qr, kv, layer, n_head, n_kv, hd, 1, p0 + 1, p0, sync=False, out=aq)
-            be.matmul_raw(B.Q4_K, L["o"], n_embd, n_head * hd, B.Q8_K, aq, 1, o, B.MEM_DEVICE)
-            be.add_rms_norm_quantize(B.Q8_K, bufB, o, norm_w, 1e-5, sum_out=bufA, out=xq2, sync=False)
-            be.ffn(B.Q4_K, L["gate"], B.Q4_K, L["up"], B.Q6_K, L["down"], n_embd, n_ff, B.Q8_K, xq2, 1, sync=False,
-                   out=ff)
-            h, prev = bufA, ff
-        # output norm of the last residual + FFN output, then the LM head
-        be.add_rms_norm_quantize(B.Q8_K, h, prev, norm_w, 1e-5, sum_out=bufB, out=xq, sync=False)
-        be.matmul_raw(B.Q6_K, head, n_vocab, n_embd, B.Q8_K, xq, 1, logits, B.MEM_DEVICE)
+        llama.forward(tok, pos[0])
         pos[0] += 1
 
-    token(0)   # warm-up outside the graph (workspace, kernel attributes)
+    token(0)   # warm-up outside the graph (workspace, kernel attributes, activation buffers)
     torch.cuda.synchronize()
-    log(f"timing {tokens} decode tokens ({n_layer} layers, kv_len {kv_len})")
+    log(f"timing {tokens} decode tokens ({cfg.n_layer} layers, kv_len {kv_len})")
     ms, method = time_launches(token, tokens, args.eager)
-    kv_bytes = 2 * n_kv * kv_len * hd * 4
-    alg = n_layer * (wbytes + kv_bytes) + head.numel()
+    kv_bytes = 2 * cfg.n_head_kv * kv_len * cfg.head_dim * 4
+    alg = cfg.n_layer * (wbytes + kv_bytes) + head_bytes
     gbs = alg / (ms * 1e-3) / 1e9
     result = {
         "metric": f"Llama-3-8B-shaped decode (batch 1, kv_len {kv_len}) tokens/s, 1 GPU",
         "value": round(1e3 / ms, 2), "unit": "tokens/s", "n_gpus": 1, "steps": tokens, "warmup": 1,
         "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
-        "config": {"workload": f"LlamaTransformer forward, 1 token, {n_layer} layers (Q4_K_M mix, one weight copy per layer), "
-                               f"kv_len {kv_len}, LM head Q6_K {n_vocab} x {n_embd}", "timing": method},
+        "config": {"workload": f"LlamaTransformer forward, 1 token, {cfg.n_layer} layers (Q4_K_M mix, one weight copy "
+                               f"per layer), kv_len {kv_len}, token_embd Q4_K + LM head Q6_K {n_vocab} x {cfg.n_embd}",
+                   "timing": method},
         "ms_per_token": round(ms, 4),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "alg_bytes_per_launch": alg,

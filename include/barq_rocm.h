@@ -116,6 +116,17 @@ size_t barq_rocm_row_bytes(int type, size_t k);
 int barq_rocm_dequantize(barq_rocm_handle* h, int type, const void* blocks,
                          size_t n_elems, float* out, int mem);
 
+/* get_embeddings (models/src/transformer.rs:96-119): out row t (k f32) is
+ * row tokens[t] of the n_rows x k table (any type barq_rocm_dequantize
+ * takes, or BARQ_TYPE_F32; token_embd.weight as the weight cache holds it),
+ * decoded bit-identically to dequantizing the whole table; an id outside
+ * [0, n_rows) gives a zero row (the reference skips it and leaves its
+ * zero-initialised row).  k a multiple of 4 and of the block size; device
+ * table aligned as the type's weights (F32 16-byte), out 16-byte.  With
+ * host buffers only the named rows are copied to the device. */
+int barq_rocm_get_rows(barq_rocm_handle* h, int type, const void* table, size_t n_rows, size_t k,
+                       const int32_t* tokens, size_t n_tokens, float* out, int mem);
+
 /* ---- activation quantize -----------------------------------------------
  * No reference counterpart: Q8_K is only an id (gguf.rs:132, quant.rs:29).
  * Implements llama.cpp's block_q8_0 (d = amax/127 stored f16,
@@ -155,6 +166,13 @@ int barq_rocm_rms_norm_quantize(barq_rocm_handle* h, int act_type, const float* 
 int barq_rocm_add_rms_norm_quantize(barq_rocm_handle* h, int out_type, const float* x,
                                     const float* d, const float* weight, size_t rows, size_t n,
                                     float eps, float* sum, void* out, int mem);
+
+/* LlamaTransformer::add_bias (transformer.rs:444-465; the q/k/v biases at
+ * :206-220) and final_output's output.bias (:487-495): y[r, j] += bias[j]
+ * for rows x dim, in place, one f32 addition per element (bit-identical).
+ * The reference applies a bias only when its length equals dim; the caller
+ * makes that check. */
+int barq_rocm_add_bias(barq_rocm_handle* h, float* y, const float* bias, size_t rows, size_t dim, int mem);
 
 /* ---- matvec / matmul ---------------------------------------------------
  * Replace blas::gemv_f32 (blas.rs:229-304; the output head,
