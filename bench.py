@@ -296,6 +296,84 @@ def cpu_baseline(w_type, w, x, n, k, budget_s, alg_bytes):
     }
 
 
+def cpu_baseline_gemm(w_type, w, x, n, k, m, budget_s):
+    """C4: the reference's per-call CPU path at M = m, blas::gemm_f32
+    (blas.rs:193-212) over f32 W^T dequantized and transposed at load (not
+    timed): output rows split over every host core (rayon par_chunks_mut),
+    each element a sequential sum over the column-strided W^T.  A bounded
+    sample of rows (each thread one row per round) is timed and scaled to the
+    m-row call."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    wf = orc.dequantize(w_type, w, n * k)
+    w_t = np.ascontiguousarray(wf.reshape(n, k).T)
+    del wf
+    threads = max(1, len(os.sched_getaffinity(0)))
+    c = np.empty((threads, n), np.float32)
+    rows, t_used, used = 0, 0.0, 0
+    while t_used < budget_s and rows < m:
+        i0 = rows % m
+        xs = np.ascontiguousarray(x[i0:i0 + threads], dtype=np.float32)
+        t0 = time.perf_counter()
+        used = orc.cpub_gemm_rows_threaded(xs, w_t, k, n, 0, xs.shape[0], c, threads)
+        t_used += time.perf_counter() - t0
+        rows += xs.shape[0]
+    per_call = t_used * m / rows
+    ops = 2.0 * m * n * k
+    cpu_model = host_cpu()
+    return {
+        "value": round(ops / per_call / 1e12, 6), "unit": "TOP/s (2 M N K / CPU time)", "cores": used,
+        "kind": "port",
+        "sample": (f"reference per-call path (blas.rs:193-212 gemm_f32 at M={m} over f32 W^T dequantized at load, "
+                   f"not timed), rows over {used} threads; {rows} of {m} rows timed in {t_used:.2f} s and scaled "
+                   f"to the call; {cpu_model}; nproc {os.cpu_count()}"),
+        "host_cpu": cpu_model, "nproc": os.cpu_count(), "us_per_call": round(per_call * 1e6, 1),
+    }
+
+
+def cpu_baseline_moe(gates, ups, downs, x, ids, hidden, n_ff, budget_s, alg_bytes):
+    """C5: the reference's MoE step on the CPU, MoEFusedOps::dispatch_experts
+    (moe_fused.rs:226-308): for each expert its batch of token rows through
+    fused_ffn (:84-92) = ops::MatMul (ops.rs:68-128, one thread) with G and U,
+    ops::Silu times x U, MatMul with D, over f32 weights transposed at load
+    (not timed), then the weighted scatter.  Every assignment costs the same
+    three products, so a bounded sample of rows of one expert is timed and
+    scaled to the step's assignments (the scatter and routing are <0.01 %)."""
+    import numpy as np
+
+    import barq_rocm as B
+    from oracle import oracle as orc
+
+    ids = np.asarray(ids)
+    n_assign = int((ids >= 0).sum())
+    e0 = int(ids.reshape(-1)[0])
+    toks = [t for t in range(ids.shape[0]) if e0 in ids[t].tolist()]
+    gt = np.ascontiguousarray(orc.dequantize(B.Q4_K, gates[e0], n_ff * hidden).reshape(n_ff, hidden).T)
+    ut = np.ascontiguousarray(orc.dequantize(B.Q4_K, ups[e0], n_ff * hidden).reshape(n_ff, hidden).T)
+    dt = np.ascontiguousarray(orc.dequantize(B.Q6_K, downs[e0], hidden * n_ff).reshape(hidden, n_ff).T)
+    g = np.empty((1, n_ff), np.float32)
+    u = np.empty_like(g)
+    out = np.empty((1, hidden), np.float32)
+    rows, t_used = 0, 0.0
+    while t_used < budget_s and rows < len(toks):
+        xr = np.ascontiguousarray(x[toks[rows]:toks[rows] + 1], dtype=np.float32)
+        t0 = time.perf_counter()
+        orc.cpub_moe_expert_ffn(xr, 1, hidden, n_ff, gt, ut, dt, g, u, out)
+        t_used += time.perf_counter() - t0
+        rows += 1
+    per_step = t_used / rows * n_assign
+    cpu_model = host_cpu()
+    return {
+        "value": round(alg_bytes / per_step / 1e9, 6), "unit": "GB/s (algorithmic step bytes / CPU time)",
+        "cores": 1, "kind": "port",
+        "sample": (f"reference MoE step (moe_fused.rs:226-308 dispatch_experts, fused_ffn over ops::MatMul, one "
+                   f"thread, f32 weights transposed at load, not timed); {rows} token rows of expert {e0} timed in "
+                   f"{t_used:.2f} s and scaled to the step's {n_assign} assignments; {cpu_model}"),
+        "host_cpu": cpu_model, "nproc": os.cpu_count(), "us_per_step": round(per_step * 1e6, 1),
+    }
+
+
 def bench_moe(args):
     """Config 5: the Mixtral-shaped MoE FFN step (barq_rocm_moe_ffn, integer path)
     on 64 tokens routed top-2 over 8 experts by the device router.  A step is
@@ -374,6 +452,9 @@ def bench_moe(args):
         traffic, detail = measure_traffic(5)
         result["roofline"]["traffic"] = round(traffic) if traffic else None
         result["roofline"]["traffic_detail"] = detail
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline_moe(gates, ups, downs, x, ids_h, hidden, n_ff, args.cpu_seconds, alg)
     be.close()
     print(json.dumps(result), flush=True)
     return 0
@@ -1092,7 +1173,10 @@ def main():
         result["roofline"]["traffic_detail"] = detail
     if not args.no_cpu and not small_batch:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(w_type, w, x[0], n, k, args.cpu_seconds, alg)
+        if m == 1:
+            result["cpu_baseline"] = cpu_baseline(w_type, w, x[0], n, k, args.cpu_seconds, alg)
+        else:
+            result["cpu_baseline"] = cpu_baseline_gemm(w_type, w, x, n, k, m, args.cpu_seconds)
     be.close()
     print(json.dumps(result), flush=True)
     return 0

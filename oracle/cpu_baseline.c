@@ -13,8 +13,18 @@
  *         simd.rs:142-168 where AVX-512 is absent) per output row over the
  *         row-major dequantized weight, one thread;
  *   (iii) SIMD, all host threads: (ii) row-partitioned over pthreads.
+ * For the batched configs:
+ *   C4:   blas::gemm_f32 at M = 512 (blas.rs:193-212): output rows split over
+ *         the host cores (rayon par_chunks_mut over rows of C), each row's
+ *         columns in order, kk sequential over the column-strided W^T;
+ *   C5:   MoEFusedOps::dispatch_experts (moe_fused.rs:226-308) with each
+ *         expert's fused_ffn (:84-92): ops::MatMul (ops.rs:68-128, one
+ *         thread, the same sequential sum) for x G and x U, ops::Silu
+ *         x / (1 + exp(-x)) (:191-211) times x U, MatMul with D, over f32
+ *         weights transposed at load.
  */
 #include <immintrin.h>
+#include <math.h>
 #include <pthread.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -111,4 +121,61 @@ int cpub_gemv_simd_threaded(const float* a, const float* x, size_t n, size_t r0,
     for (int t = 0; t < used; t++)
         if (created[t]) pthread_join(tid[t], NULL);
     return used;
+}
+
+/* blas.rs:202-210 / ops.rs:95-106: rows [i0, i1) of C[m x n] = A[m x k] B[k x n],
+   each element a sequential unfused sum over kk */
+void cpub_gemm_rows(const float* a, const float* b, size_t k, size_t n, size_t i0, size_t i1, float* c) {
+    for (size_t i = i0; i < i1; i++)
+        for (size_t j = 0; j < n; j++) {
+            float sum = 0.0f;
+            for (size_t kk = 0; kk < k; kk++) sum += a[i * k + kk] * b[kk * n + j];
+            c[i * n + j] = sum;
+        }
+}
+
+struct gjob { const float* a; const float* b; size_t k, n, i0, i1; float* c; };
+
+static void* run_gjob(void* p) {
+    struct gjob* j = (struct gjob*)p;
+    cpub_gemm_rows(j->a, j->b, j->k, j->n, j->i0, j->i1, j->c);
+    return NULL;
+}
+
+/* gemm_f32's rayon form: rows [i0, i1) split over `threads` pthreads
+   (returns the number of row ranges run) */
+int cpub_gemm_rows_threaded(const float* a, const float* b, size_t k, size_t n, size_t i0, size_t i1, float* c,
+                            int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > CPUB_MAX_THREADS) threads = CPUB_MAX_THREADS;
+    pthread_t tid[CPUB_MAX_THREADS];
+    char created[CPUB_MAX_THREADS];
+    struct gjob jobs[CPUB_MAX_THREADS];
+    size_t rows = i1 - i0, per = (rows + (size_t)threads - 1) / (size_t)threads;
+    int used = 0;
+    for (int t = 0; t < threads; t++) {
+        size_t s = i0 + (size_t)t * per, e = s + per < i1 ? s + per : i1;
+        if (s >= e) break;
+        jobs[t] = (struct gjob){a, b, k, n, s, e, c};
+        created[t] = pthread_create(&tid[t], NULL, run_gjob, &jobs[t]) == 0;
+        if (!created[t]) run_gjob(&jobs[t]);
+        used = t + 1;
+    }
+    for (int t = 0; t < used; t++)
+        if (created[t]) pthread_join(tid[t], NULL);
+    return used;
+}
+
+/* fused_ffn of one expert on t rows (moe_fused.rs:84-92): g = x Gt, u = x Ut
+   (Gt, Ut [hidden x n_ff]), h = (g / (1 + exp(-g))) * u, out = h Dt
+   (Dt [n_ff x hidden]); g and u are t x n_ff scratch */
+void cpub_moe_expert_ffn(const float* x, size_t t, size_t hidden, size_t n_ff, const float* gt, const float* ut,
+                         const float* dt, float* g, float* u, float* out) {
+    cpub_gemm_rows(x, gt, hidden, n_ff, 0, t, g);
+    cpub_gemm_rows(x, ut, hidden, n_ff, 0, t, u);
+    for (size_t i = 0; i < t * n_ff; i++) {
+        const float a = g[i] / (1.0f + expf(-g[i]));
+        g[i] = a * u[i];
+    }
+    cpub_gemm_rows(g, dt, n_ff, hidden, 0, t, out);
 }

@@ -63,6 +63,9 @@ def lib():
             "cpub_gemv_simd": (None, [_vp, _vp, _sz, _sz, _sz, _vp]),
             "cpub_gemv_simd_threaded": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _i]),
             "cpub_simd_level": (_i, []),
+            "cpub_gemm_rows": (None, [_vp, _vp, _sz, _sz, _sz, _sz, _vp]),
+            "cpub_gemm_rows_threaded": (_i, [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _i]),
+            "cpub_moe_expert_ffn": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(l, name)
@@ -377,6 +380,21 @@ def cpub_gemv_simd(a, x, n, r0, r1, y):
 
 def cpub_gemv_simd_threaded(a, x, n, r0, r1, y, threads) -> int:
     return lib().cpub_gemv_simd_threaded(_p(a), _p(x), n, r0, r1, _p(y), threads)
+
+
+def cpub_gemm_rows(a, b, k, n, i0, i1, c):
+    """gemm_f32's per-row loop (blas.rs:202-210) for rows [i0, i1), one thread."""
+    lib().cpub_gemm_rows(_p(a), _p(b), k, n, i0, i1, _p(c))
+
+
+def cpub_gemm_rows_threaded(a, b, k, n, i0, i1, c, threads) -> int:
+    """The same rows split over threads (rayon over rows of C)."""
+    return lib().cpub_gemm_rows_threaded(_p(a), _p(b), k, n, i0, i1, _p(c), threads)
+
+
+def cpub_moe_expert_ffn(x, t, hidden, n_ff, gt, ut, dt, g, u, out):
+    """fused_ffn of one expert on t rows over f32 transposed weights."""
+    lib().cpub_moe_expert_ffn(_p(x), t, hidden, n_ff, _p(gt), _p(ut), _p(dt), _p(g), _p(u), _p(out))
 
 
 def cpub_simd_level() -> int:

@@ -407,3 +407,45 @@ def test_cpu_baseline_simd_dot_matches_gemv_f32(orc, threads):
     used = orc.cpub_gemv_simd_threaded(a, x, n, 0, m, y2, threads)
     assert used == threads
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_cpu_baseline_gemm_rows_equals_gemm_f32(orc, threads):
+    # the C4 leg: gemm_f32 at M > 1 (blas.rs:193-212), rows split over
+    # threads, bit-exact with the oracle's gemm_f32 whatever the split
+    rng = np.random.default_rng(6)
+    m, k, n = 11, 300, 257
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    ref = orc.gemm_f32(a, b, m, k, n)
+    c = np.zeros((m, n), np.float32)
+    used = orc.cpub_gemm_rows_threaded(a, b, k, n, 0, m, c, threads)
+    per = -(-m // threads)                 # rows per range, as the split makes them
+    assert used == -(-m // per)
+    assert np.array_equal(c.view(np.uint32), ref.view(np.uint32))
+    c1 = np.zeros((m, n), np.float32)
+    orc.cpub_gemm_rows(a, b, k, n, 3, 7, c1)
+    assert np.array_equal(c1[3:7].view(np.uint32), ref[3:7].view(np.uint32))
+
+
+def test_cpu_baseline_moe_expert_equals_oracle_moe(orc):
+    import barq_rocm as B
+    from barq_rocm import synth
+    # the C5 leg: one expert's fused_ffn over f32 weights transposed at load
+    # equals the oracle's F32 MoE (moe_fused.rs:84-92, 226-308) for tokens
+    # routed to that expert alone with weight 1 (out = 0 + 1 * y), bit for bit
+    hid, nff, rows = 256, 512, 3
+    gate = synth.gen_weights(B.Q4_K, nff, hid, 31)
+    up = synth.gen_weights(B.Q4_K, nff, hid, 32)
+    down = synth.gen_weights(B.Q6_K, hid, nff, 33)
+    x = synth.gen_f32(rows * hid, 34).reshape(rows, hid)
+    ref = orc.moe_ffn(B.Q4_K, [gate], B.Q4_K, [up], B.Q6_K, [down], hid, nff, x, np.zeros((rows, 1), np.int32),
+                      np.ones((rows, 1), np.float32), orc.F32)
+    gt = np.ascontiguousarray(orc.dequantize(B.Q4_K, gate, nff * hid).reshape(nff, hid).T)
+    ut = np.ascontiguousarray(orc.dequantize(B.Q4_K, up, nff * hid).reshape(nff, hid).T)
+    dt = np.ascontiguousarray(orc.dequantize(B.Q6_K, down, hid * nff).reshape(hid, nff).T)
+    g = np.empty((rows, nff), np.float32)
+    u = np.empty_like(g)
+    out = np.empty((rows, hid), np.float32)
+    orc.cpub_moe_expert_ffn(x, rows, hid, nff, gt, ut, dt, g, u, out)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
