@@ -66,7 +66,7 @@ EXPORTS = (
     "barq_rocm_kv_cache_append_rope", "barq_rocm_kv_cache_size", "barq_rocm_kv_cache_layer_len",
     "barq_rocm_kv_cache_head", "barq_rocm_kv_cache_clear", "barq_rocm_kv_cache_destroy", "barq_rocm_attention",
     "barq_rocm_kv_cache_append_rope_q", "barq_rocm_attention_q8k", "barq_rocm_matvec_group",
-    "barq_rocm_qkv_append_rope", "barq_rocm_matmul_noalloc",
+    "barq_rocm_qkv_append_rope", "barq_rocm_matmul_noalloc", "barq_rocm_stream_read",
 )
 
 # bytes of the fixed per-GPU scratch behind barq_rocm_matmul_noalloc
@@ -106,6 +106,7 @@ def _declare(lib):
         "barq_rocm_dequantize": (_i, [_vp, _i, _vp, _sz, _vp, _i]),
         "barq_rocm_get_rows": (_i, [_vp, _i, _vp, _sz, _sz, _vp, _sz, _vp, _i]),
         "barq_rocm_add_bias": (_i, [_vp, _vp, _vp, _sz, _sz, _i]),
+        "barq_rocm_stream_read": (_i, [_vp, _vp, _sz, _vp]),
         "barq_rocm_quantize_act": (_i, [_vp, _i, _vp, _sz, _sz, _vp, _i]),
         "barq_rocm_rms_norm": (_i, [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i]),
         "barq_rocm_rms_norm_quantize": (_i, [_vp, _i, _vp, _vp, _sz, _sz, ctypes.c_float, _vp, _i]),

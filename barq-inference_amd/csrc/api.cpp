@@ -257,6 +257,15 @@ int barq_rocm_get_rows(barq_rocm_handle* h, int type, const void* table, size_t 
     return ok();
 }
 
+int barq_rocm_stream_read(barq_rocm_handle* h, const void* p, size_t bytes, uint32_t* sink) {
+    if (bytes < 16) return ok();
+    if (!p || !sink) return fail(BARQ_E_INVALID, "stream_read: null buffer");
+    if (!aligned(p, 16) || !aligned(sink, 4)) return fail(BARQ_E_INVALID, "stream_read: p must be 16-byte aligned");
+    BARQ_CHECK(check_handle(h));
+    DeviceGuard g(h);
+    return launched(barq::stream_read_launch(p, bytes, sink, h->stream), "stream_read");
+}
+
 int barq_rocm_add_bias(barq_rocm_handle* h, float* y, const float* bias, size_t rows, size_t dim, int mem) {
     BARQ_CHECK(check_mem(mem));
     if (rows == 0 || dim == 0) return ok();

@@ -194,6 +194,9 @@ hipError_t rope_qkv_launch(int layout, const float* qx, const float* kx, const f
                            float* v_out, size_t seq, size_t n_q, size_t n_kv, size_t hd, size_t start_pos,
                            float freq_scale, const float* inv_freq, size_t cache_head_stride, hipStream_t s);
 bool attention_supported(size_t head_dim);
+// probe.hip: read `bytes` (rounded down to 16) once with non-temporal loads
+hipError_t stream_read_launch(const void* p, size_t bytes, uint32_t* sink, hipStream_t s);
+
 void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len, int* n_split, int* chunk);
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv);
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s);

@@ -1104,6 +1104,18 @@ def main():
         fixed = {"launch_floor_us": round(floor_ms * 1e3, 3), "us_per_call_2x_rows": round(ms2 * 1e3, 3),
                  "marginal_gbs": round(extra / ((ms2 - ms) * 1e-3) / 1e9, 1) if ms2 > ms else None}
         del ws2, w2
+        # the streaming-read floor of the same weight bytes, same copies, graph and stream
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+        def slaunch(i):
+            B._lib.check(be._lib.barq_rocm_stream_read(be.h, ws[i % copies].data_ptr(), wbytes, sink.data_ptr()))
+        for i in range(min(args.warmup, 500)):
+            slaunch(i)
+        torch.cuda.synchronize()
+        st_ms, _ = time_launches(slaunch, args.steps, args.eager)
+        fixed.update({"stream_floor_us": round(st_ms * 1e3, 3),
+                      "stream_floor_gbs": round(wbytes / (st_ms * 1e-3) / 1e9, 1),
+                      "us_over_stream_floor": round((ms - st_ms) * 1e3, 3)})
     us = ms * 1e3
     gbs = alg / (ms * 1e-3) / 1e9
     # correctness of the timed output against the oracle

@@ -473,6 +473,15 @@ int barq_rocm_attention_q8k(barq_rocm_handle* h, const float* q, const barq_rocm
                             size_t n_head, size_t n_head_kv, size_t head_dim, size_t q_len, size_t kv_len,
                             size_t start_pos, void* out_q8k, int mem);
 
+/* ---- measurement ------------------------------------------------------------
+ * No counterpart in the reference.  Reads bytes (rounded down to 16) at the
+ * device pointer p once, with coalesced non-temporal loads and nothing else:
+ * the HBM streaming floor a GEMV over the same bytes is measured against
+ * (bench.py times it in the same graph, on the same stream, as the GEMV).
+ * sink: a device word written only when the XOR of all the data equals a
+ * fixed constant.  p 16-byte aligned. */
+int barq_rocm_stream_read(barq_rocm_handle* h, const void* p, size_t bytes, uint32_t* sink);
+
 /* ---- matmul without allocation -------------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory: code under HIP graph capture, serving loops, harnesses that forbid
