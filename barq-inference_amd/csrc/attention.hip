@@ -401,21 +401,34 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
     M = sm.wred[0][0];
     #pragma unroll
     for (int u = 1; u < NWV; u++) M = fmaxf(M, sm.wred[0][u]);
-    float L = 0.0f;
-    for (int s = t; s < n_split; s += NT) {
-        const float ms = s == t ? Ms : pp[(size_t)s * (HD + 2)];
-        const float ls = s == t ? Ls : pp[(size_t)s * (HD + 2) + 1];
-        const float ws = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
-        sm.w[s] = ws;
-        L = __builtin_fmaf(ls, ws, L);
+    // The denominator in the 1024-thread merge's order whatever NT is: thread
+    // t plays the 1024 lanes t + NT j (j < K), each summing its splits
+    // s = t + NT j + 1024 u in u order; a butterfly per 64 of those lanes
+    // (a real wave holds 64 consecutive ones); then the 16 wave partials in
+    // lane order.  So the Q8_K merge's rows are the f32 merge's to the bit.
+    float Lj[K];
+    #pragma unroll
+    for (int j = 0; j < K; j++) {
+        float L = 0.0f;
+        for (int s = t + NT * j; s < n_split; s += 1024) {
+            const float ms = s == t ? Ms : pp[(size_t)s * (HD + 2)];
+            const float ls = s == t ? Ls : pp[(size_t)s * (HD + 2) + 1];
+            const float ws = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
+            sm.w[s] = ws;
+            L = __builtin_fmaf(ls, ws, L);
+        }
+        #pragma unroll
+        for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+        Lj[j] = L;
     }
-    #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
-    if (lane == 0) sm.wred[1][wave] = L;
+    if (lane == 0) {
+        #pragma unroll
+        for (int j = 0; j < K; j++) sm.wred[1][NWV * j + wave] = Lj[j];
+    }
     __syncthreads();
-    L = sm.wred[1][0];
+    float L = sm.wred[1][0];
     #pragma unroll
-    for (int u = 1; u < NWV; u++) L += sm.wred[1][u];
+    for (int u = 1; u < 1024 / 64; u++) L += sm.wred[1][u];
     #pragma unroll
     for (int j = 0; j < K; j++) {
         const int sj = sub + STEP * j;

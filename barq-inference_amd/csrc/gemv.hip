@@ -186,12 +186,12 @@ __device__ __forceinline__ void gemv_q4k_rows_issue(const uint8_t* __restrict__ 
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = R * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
+    // every copy instruction is issued, so their number is a constant: the
+    // lanes past the span read out of range (zeros, no memory traffic)
     #pragma unroll
     for (int q = 0; q < q4k_lds_buf<R> / 1024; q++) {
-        if (1024u * q < span) {
-            const uint32_t off = 1024u * q + 16u * (uint32_t)l;
-            lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
-        }
+        const uint32_t off = 1024u * q + 16u * (uint32_t)l;
+        lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
     }
 }
 
@@ -205,7 +205,7 @@ __device__ __forceinline__ float gemv_q4k_rows_finish(int nblk, int l, const uin
     using F = FmtQ4K;
     const F::Lane c = F::lane(l);
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES;
-    const uint32_t n_all = (R * rb + 1023) / 1024;   // copies issued
+    constexpr uint32_t n_all = q4k_lds_buf<R> / 1024;   // copies issued
     const bool act = F::active(0, c, nblk);
     const uint8_t* b = buf + Q4_K_BYTES * c.sbl;
     F::X xs;
@@ -214,6 +214,12 @@ __device__ __forceinline__ float gemv_q4k_rows_finish(int nblk, int l, const uin
     for (int r = 0; r < R; r++) {
         // copies issued after the last one row r needs
         wait_vmcnt_upto8(n_all - (rb * (r + 1) + 1023) / 1024);
+        if (r == 0) {
+            // the activation loads precede all n_all copies: a constant wait
+            // that the runtime one above already implies, and that the
+            // build's assembly check can verify on every path
+            wait_vmcnt<n_all>();
+        }
         asm volatile("" ::: "memory");
         if (r == 0) q4k_x_ready(xr, xs);
         if (act) {
@@ -290,16 +296,16 @@ void gemv_q4k_lds_multi_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, 
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, span = R * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
+    // every copy instruction is issued (a constant count; lanes past the span
+    // read out of range)
     #pragma unroll
     for (int q = 0; q < q4k_lds_buf<R> / 1024; q++) {
-        if (1024u * q < span) {
-            const uint32_t off = 1024u * q + 16u * (uint32_t)l;
-            lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
-        }
+        const uint32_t off = 1024u * q + 16u * (uint32_t)l;
+        lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : 0x80000000u, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     const F::Lane c = F::lane(l);
-    const uint32_t n_all = (span + 1023) / 1024;
+    constexpr uint32_t n_all = q4k_lds_buf<R> / 1024;
     const bool act = F::active(0, c, nblk);
     const uint8_t* b = buf + Q4_K_BYTES * c.sbl;
     F::X xs[NX];
@@ -310,6 +316,7 @@ void gemv_q4k_lds_multi_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, 
     for (int r = 0; r < R; r++) {
         // the activation rows and row r's copies (loads complete in order)
         wait_vmcnt_upto8(n_all - (rb * (r + 1) + 1023) / 1024);
+        if (r == 0) wait_vmcnt<n_all>();   // the activation loads precede every copy
         asm volatile("" ::: "memory");
         if (r == 0) {
             #pragma unroll

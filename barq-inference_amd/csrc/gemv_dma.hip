@@ -394,18 +394,21 @@ void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const u
     const uint32_t rb = (uint32_t)nblk * F::ROW_BLOCK_BYTES, span = 2 * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
+    // every copy instruction is issued (a constant count; lanes past the
+    // span read out of range)
     #pragma unroll
     for (int q = 0; q < BUF / 1024; q++) {
-        if (1024u * q < span) {
-            const uint32_t off = 1024u * q + 16u * (uint32_t)l;
-            lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : DMA_SKIP, 0);
-        }
+        const uint32_t off = 1024u * q + 16u * (uint32_t)l;
+        lds_load16_nt(rs, buf + 1024 * q, off < span ? base + off : DMA_SKIP, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     const typename F::Lane c = F::lane(l);
     const bool act = F::active(0, c, nblk);
     // copies issued after the last one row 0 needs (at most 4)
-    wait_vmcnt_upto4((span + 1023) / 1024 - (rb + 1023) / 1024);
+    wait_vmcnt_upto4(BUF / 1024 - (rb + 1023) / 1024);
+    // the activation loads precede every copy (a constant wait the one above
+    // implies, which the build's assembly check can verify on every path)
+    wait_vmcnt<BUF / 1024>();
     asm volatile("" ::: "memory");
     typename F::X x[NX];
     #pragma unroll

@@ -228,6 +228,7 @@ def test_append_rope_q_equals_separate_steps(be, layout, n_head, n_kv, hd, n):
     (32, 8, 128, 40, 100, 60, 100),       # a prompt chunk on the MFMA kernel
     (8, 2, 64, 1, 1000, 999, 1000),       # head_dim 64: four heads per block
     (4, 2, 256, 1, 517, 516, 517),        # head_dim 256: one head per block
+    (8, 1, 64, 1, 20000, 19999, 20000),   # 313 splits: more than the 256 threads a head gets in the Q8_K merge
 ])
 def test_attention_q8k_equals_quantized_attention(be, n_head, n_kv, hd, q_len, kv_len, start, pos):
     """attention_q8k writes the bytes quantize_act(Q8_K) writes for the f32
@@ -283,4 +284,31 @@ def test_attention_mfma_kernel_small_chunks(be, orc, n_head, n_kv, q_len, kv_len
     ref = orc.attention(q, k, v, n_head, q_len, kv_len, start)
     assert np.max(np.abs(got - ref)) <= 2e-5 * np.max(np.abs(v))
     assert np.array_equal(got_q8.reshape(-1), ref_q8.reshape(-1))
+    c.close()
+
+
+def test_attention_q8k_many_splits_head_dim_128(be):
+    """More splits than the Q8_K merge's 512 threads per head at head_dim 128
+    (625 splits with BARQ_ATTN_WG=2048, read at handle creation): the merge
+    still writes the bytes the f32 merge's rows quantize to."""
+    import os
+    n_head, n_kv, hd, kv_len = 8, 1, 128, 40000
+    c, k, v = fill_cache(be, n_kv, hd, kv_len, 77)
+    q = rng_f32(78, n_head, 1, hd)
+    old = os.environ.get("BARQ_ATTN_WG")
+    os.environ["BARQ_ATTN_WG"] = "2048"
+    try:
+        b2 = B.Backend(0)
+    finally:
+        if old is None:
+            os.environ.pop("BARQ_ATTN_WG", None)
+        else:
+            os.environ["BARQ_ATTN_WG"] = old
+    try:
+        y = A.compute_attention(b2, dev(q), c, 1, n_head, n_kv, hd, 1, kv_len, kv_len - 1)
+        ref = b2.quantize_act(B.Q8_K, y.reshape(1, n_head * hd)).cpu().numpy().reshape(-1)
+        got = A.compute_attention_q8k(b2, dev(q), c, 1, n_head, n_kv, hd, 1, kv_len, kv_len - 1).cpu().numpy()
+    finally:
+        b2.close()
+    assert np.array_equal(got.reshape(-1), ref)
     c.close()
