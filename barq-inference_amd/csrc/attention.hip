@@ -236,15 +236,13 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     auto load = [&](Rows& b, int blk) {
         #pragma unroll
         for (int p = 0; p < P; p++) {
-            const int j = blk + p * R + r;
-            if (j < j1) {
-                const f32x4n* kp = reinterpret_cast<const f32x4n*>(kh + (size_t)j * HD);
-                const f32x4n* vp = reinterpret_cast<const f32x4n*>(vh + (size_t)j * HD);
-                b.k[p][0] = ntf4(kp + c); b.k[p][1] = ntf4(kp + c + LPR);
-                b.v[p][0] = ntf4(vp + c); b.v[p][1] = ntf4(vp + c + LPR);
-            } else {
-                b.k[p][0] = b.k[p][1] = b.v[p][0] = b.v[p][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            // a row past the range loads the range's last row instead (finite
+            // values, no zero fill): its score is masked and its weight is 0
+            const int j = min(blk + p * R + r, j1 - 1);
+            const f32x4n* kp = reinterpret_cast<const f32x4n*>(kh + (size_t)j * HD);
+            const f32x4n* vp = reinterpret_cast<const f32x4n*>(vh + (size_t)j * HD);
+            b.k[p][0] = ntf4(kp + c); b.k[p][1] = ntf4(kp + c + LPR);
+            b.v[p][0] = ntf4(vp + c); b.v[p][1] = ntf4(vp + c + LPR);
         }
     };
     auto block = [&](const Rows& b, int blk) {
@@ -292,14 +290,16 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
         }
     };
     if (j0 < j1) {
-        Rows cur;
-        load(cur, j0);
-        for (int blk = j0; blk < j1; blk += R * P) {
-            Rows nxt;
-            const bool more = blk + R * P < j1;
-            if (more) load(nxt, blk + R * P);
-            block(cur, blk);
-            if (more) cur = nxt;
+        // two row buffers used in turn (no register copies between blocks)
+        Rows ra, rb;
+        load(ra, j0);
+        for (int blk = j0; blk < j1; blk += 2 * R * P) {
+            const int b1 = blk + R * P;
+            if (b1 < j1) load(rb, b1);
+            block(ra, blk);
+            if (b1 >= j1) break;
+            if (b1 + R * P < j1) load(ra, b1 + R * P);
+            block(rb, b1);
         }
     }
 
