@@ -167,6 +167,18 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Maximum over aligned groups of N lanes, the same exchanges as group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    if constexpr (N >= 16)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+    return v;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // K/V rows are streamed once per call: loaded with the non-temporal hint
@@ -318,19 +330,21 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     }
     __syncthreads();
     // each row state's weight exp2(m_rr - M) once per (row, head), in place
-    // of its max (then the same sums in the same order for every dim)
-    if (t < G) {
-        const int g = t;
-        float M = -INFINITY;
-        for (int rr = 0; rr < R; rr++) M = fmaxf(M, red_ml[rr][g][0]);
-        float L = 0.0f;
-        for (int rr = 0; rr < R; rr++) {
-            const float w = M == -INFINITY ? 0.0f : fast_exp2(red_ml[rr][g][0] - M);
-            L = __builtin_fmaf(red_ml[rr][g][1], w, L);
-            red_ml[rr][g][0] = w;
+    // of its max (then the same sums in the same order for every dim): one
+    // thread per (head, row state), each head's R states an aligned group of
+    // lanes (G * R <= ATT_THREADS)
+    static_assert(G * R <= ATT_THREADS && R <= 32, "one thread per row state");
+    if (t < G * R) {
+        const int g = t / R, rr = t % R;
+        const float mr = red_ml[rr][g][0];
+        const float M = group_max<R>(mr);
+        const float w = M == -INFINITY ? 0.0f : fast_exp2(mr - M);
+        const float L = group_sum<R>(red_ml[rr][g][1] * w);
+        red_ml[rr][g][0] = w;
+        if (rr == 0) {
+            red_ms[g][0] = M;
+            red_ms[g][1] = L;
         }
-        red_ms[g][0] = M;
-        red_ms[g][1] = L;
     }
     __syncthreads();
     for (int e = t; e < G * HD; e += ATT_THREADS) {
