@@ -181,6 +181,23 @@ __device__ __forceinline__ float group_max(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Maximum and sum over the 64 lanes of a wave, every lane getting the
+// result: 16-lane DPP rounds, then the gfx950 row and half-wave swaps (no
+// LDS round trips).
+__device__ __forceinline__ float wave_max64(float v) {
+    v = group_max<16>(v);
+    auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    v = fmaxf(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
+}
+
+__device__ __forceinline__ float wave_sum64(float v) {
+    v = group_sum<16>(v);
+    v = swap16_add(v, v);
+    return swap32_add(v, v);
+}
+
 // K/V rows are streamed once per call: loaded with the non-temporal hint
 // (measured in one run: 55.1 -> 49.5 us at 32K positions, 14.1 -> 13.5 us at 4K)
 typedef float f32x4n __attribute__((ext_vector_type(4)));
@@ -408,8 +425,7 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
         Ls = pp[(size_t)t * (HD + 2) + 1];
     }
     for (int s = t; s < n_split; s += NT) M = fmaxf(M, pp[(size_t)s * (HD + 2)]);
-    #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    M = wave_max64(M);
     if (lane == 0) sm.wred[0][wave] = M;
     __syncthreads();
     M = sm.wred[0][0];
@@ -431,8 +447,7 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
             sm.w[s] = ws;
             L = __builtin_fmaf(ls, ws, L);
         }
-        #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+        L = wave_sum64(L);
         Lj[j] = L;
     }
     if (lane == 0) {
