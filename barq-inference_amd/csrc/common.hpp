@@ -193,6 +193,40 @@ __device__ __forceinline__ float reduce4(float a, float b, float c, float d) {
     return row16_sum(v);
 }
 
+// Maximum over a row of 16 lanes with DPP (the exchanges of row16_sum).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true)));
+    return v;
+}
+
+// Maximum over the whole wave, in every lane: row16_max, then the row and
+// half-wave swaps (no LDS round trips).  Every lane must be active.
+__device__ __forceinline__ float wave_max_all(float v) {
+    v = row16_max(v);
+    auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    v = fmaxf(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
+}
+
+// Sum over the whole wave, in every lane, in a fixed order: row16_sum, then
+// the row pairs, then the halves.  Every lane must be active.
+__device__ __forceinline__ float wave_sum_all(float v) {
+    v = row16_sum(v);
+    v = swap16_add(v, v);
+    return swap32_add(v, v);
+}
+
+// Integer sum over each aligned group of four lanes (quad permutes).
+__device__ __forceinline__ int quad_isum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;

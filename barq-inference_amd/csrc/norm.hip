@@ -8,57 +8,21 @@
 //
 // One workgroup (a wave per 256 elements, up to 16) per row; the row is held in registers, so the
 // fused variant reads x once and writes only Q8_K / Q8_0 blocks.  The sum of
-// squares runs in a fixed tree order (per lane, then a butterfly across the
-// wave, then the wave partials in order); the reference sums
+// squares runs in a fixed tree order (per lane, then DPP rows and lane swaps
+// across the wave, then the wave partials in order); the reference sums
 // sequentially, so the two agree to float rounding, not bit for bit.  Every
 // later step (the products and the quantizer) is the reference's own
 // sequence of single IEEE operations.
 #include "common.hpp"
 #include "launch.hpp"
+#include "q8k_block.hpp"
 
 namespace barq {
 
 constexpr int NORM_MAX_WAVES = 16;
 
-// q8_k_block / q8_0 quantizers of quantize.hip, restated for values already
-// in registers: 4 elements per lane, a Q8_K block per wave, a Q8_0 block per
-// 8 lanes.
-__device__ __forceinline__ void norm_q8_k_block(const float (&vv)[4], int lane, uint8_t* __restrict__ blk) {
-    float ba = 0.0f, bv = 0.0f;
-    int bi = 0x7fffffff;
-    #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float ax = fabsf(vv[j]);
-        if (ax > ba) { ba = ax; bv = vv[j]; bi = 4 * lane + j; }
-    }
-    #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(ba, off);
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
-    }
-    if (ba == 0.0f) {
-        reinterpret_cast<uint32_t*>(blk + 4)[lane] = 0u;
-        if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = 0;
-        if (lane == 0) *reinterpret_cast<float*>(blk) = 0.0f;
-        return;
-    }
-    const float iscale = -127.0f / bv;
-    int q[4];
-    #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int t = (int)rintf(iscale * vv[j]);
-        q[j] = t < 127 ? t : 127;
-    }
-    reinterpret_cast<uint32_t*>(blk + 4)[lane] = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                                                 ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *reinterpret_cast<float*>(blk) = 1.0f / iscale;
-}
+// The Q8_K blocks come from q8_k_block (q8k_block.hpp): a wave per block, four
+// elements per lane, the bytes quantize_q8_k_kernel writes for the same values.
 
 // Q8_0 block of 32 = lanes 8g .. 8g + 7 (4 elements each): d = amax / 127
 // (stored f16), q = roundf(x * (1 / d)).
@@ -124,8 +88,7 @@ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ d, c
         ss = ss + v[i].z * v[i].z;
         ss = ss + v[i].w * v[i].w;
     }
-    #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
+    ss = wave_sum_all(ss);
     if (lane == 0) part[wave] = ss;
     __syncthreads();
     float sum_sq = part[0];
@@ -144,7 +107,7 @@ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ d, c
                 make_float4(y[0], y[1], y[2], y[3]);
         } else if constexpr (OUT == 1) {
             uint8_t* o = static_cast<uint8_t*>(out) + (row * (size_t)(n / 256) + blk) * Q8_K_BYTES;
-            norm_q8_k_block(y, lane, o);
+            q8_k_block(y, lane, o);
         } else {
             uint8_t* o = static_cast<uint8_t*>(out) + (row * (size_t)(n / 32) + 8 * blk + (lane >> 3)) * Q8_0_BYTES;
             norm_q8_0_block(y, lane, o);

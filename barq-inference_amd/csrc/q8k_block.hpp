@@ -10,20 +10,17 @@ namespace barq {
 // iscale = -127/max; q = min(127, rint(iscale*x)); d = 1/iscale;
 // bsums[g] = sum of q[16g .. 16g+16).  An all-zero block stores zeros.
 __device__ __forceinline__ void q8_k_block(const float (&vv)[4], int lane, uint8_t* __restrict__ blk) {
-    float ba = 0.0f, bv = 0.0f;
-    int bi = 0x7fffffff;
-    #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float ax = fabsf(vv[j]);
-        if (ax > ba) { ba = ax; bv = vv[j]; bi = 4 * lane + j; }
-    }
-    #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(ba, off);
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
-    }
+    // the largest |x| of the block (DPP rows and lane swaps; NaN never wins:
+    // fmaxf returns the other operand), then the first element holding it:
+    // the lowest lane with such an element, and in that lane the lowest j
+    float a = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
+    const float ba = wave_max_all(fmaxf(a, 0.0f));
+    const bool hit = fabsf(vv[0]) == ba || fabsf(vv[1]) == ba || fabsf(vv[2]) == ba || fabsf(vv[3]) == ba;
+    const uint64_t lanes = __ballot(hit && ba != 0.0f);
+    const float mine = fabsf(vv[0]) == ba ? vv[0] : fabsf(vv[1]) == ba ? vv[1] : fabsf(vv[2]) == ba ? vv[2] : vv[3];
+    const float bv = lanes ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine),
+                                                                                 (int)__builtin_ctzll(lanes)))
+                           : 0.0f;
     if (ba == 0.0f) {
         reinterpret_cast<uint32_t*>(blk + 4)[lane] = 0u;
         if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = 0;
@@ -40,9 +37,7 @@ __device__ __forceinline__ void q8_k_block(const float (&vv)[4], int lane, uint8
     const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                             ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
     reinterpret_cast<uint32_t*>(blk + 4)[lane] = packed;
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    const int s = quad_isum(q[0] + q[1] + q[2] + q[3]);
     if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blk + 260 + 2 * (lane >> 2)) = (int16_t)s;
     if (lane == 0) *reinterpret_cast<float*>(blk) = 1.0f / iscale;
 }
