@@ -76,7 +76,8 @@ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ d, c
             if (f < n4) {
                 const float4 dv = dr[f];
                 v[i] = make_float4(v[i].x + dv.x, v[i].y + dv.y, v[i].z + dv.z, v[i].w + dv.w);
-                if (sum) reinterpret_cast<float4*>(sum + row * (size_t)n)[f] = v[i];
+                // f32 rows: the sum is stored before them (a caller's out == sum ends with the norm)
+                if (OUT == 0 && sum) reinterpret_cast<float4*>(sum + row * (size_t)n)[f] = v[i];
             }
         }
     }
@@ -111,6 +112,15 @@ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ d, c
         } else {
             uint8_t* o = static_cast<uint8_t*>(out) + (row * (size_t)(n / 32) + 8 * blk + (lane >> 3)) * Q8_0_BYTES;
             norm_q8_0_block(y, lane, o);
+        }
+    }
+    // quantized rows: the sum x + d is stored last, since a store issued before
+    // the reduction made the compiler wait for it (vmcnt counts stores too)
+    if (OUT != 0 && dr && sum) {
+        #pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int f = 64 * (wave + W * i) + lane;
+            if (f < n4) reinterpret_cast<float4*>(sum + row * (size_t)n)[f] = v[i];
         }
     }
 }
