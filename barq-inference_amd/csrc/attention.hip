@@ -153,50 +153,8 @@ hipError_t transpose_heads_launch(const float* x, float* out, size_t seq, size_t
 constexpr int ATT_THREADS = 256;
 constexpr float LOG2E = 1.44269504088896340736f;
 
-// Sum over aligned groups of N lanes (N = 8, 16 or 32); every lane of the
-// group gets the sum.  Within a row of 16 lanes: quad swaps, then the
-// half-row and row mirrors; across two rows: a 16-lane xor.
-template <int N>
-__device__ __forceinline__ float group_sum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    if constexpr (N >= 16)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-    if constexpr (N >= 32) v += __shfl_xor(v, 16);
-    return v;
-}
-
-// Maximum over aligned groups of N lanes, the same exchanges as group_sum.
-template <int N>
-__device__ __forceinline__ float group_max(float v) {
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
-    if constexpr (N >= 16)
-        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
-    if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-    return v;
-}
-
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Maximum and sum over the 64 lanes of a wave, every lane getting the
-// result: 16-lane DPP rounds, then the gfx950 row and half-wave swaps (no
-// LDS round trips).
-__device__ __forceinline__ float wave_max64(float v) {
-    v = group_max<16>(v);
-    auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-    v = fmaxf(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
-    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-    return fmaxf(__builtin_bit_cast(float, (int)b[0]), __builtin_bit_cast(float, (int)b[1]));
-}
-
-__device__ __forceinline__ float wave_sum64(float v) {
-    v = group_sum<16>(v);
-    v = swap16_add(v, v);
-    return swap32_add(v, v);
-}
 
 // K/V rows are streamed once per call: loaded with the non-temporal hint
 // (measured in one run: 55.1 -> 49.5 us at 32K positions, 14.1 -> 13.5 us at 4K)
@@ -425,7 +383,7 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
         Ls = pp[(size_t)t * (HD + 2) + 1];
     }
     for (int s = t; s < n_split; s += NT) M = fmaxf(M, pp[(size_t)s * (HD + 2)]);
-    M = wave_max64(M);
+    M = wave_max_all(M);
     if (lane == 0) sm.wred[0][wave] = M;
     __syncthreads();
     M = sm.wred[0][0];
@@ -447,7 +405,7 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
             sm.w[s] = ws;
             L = __builtin_fmaf(ls, ws, L);
         }
-        L = wave_sum64(L);
+        L = wave_sum_all(L);
         Lj[j] = L;
     }
     if (lane == 0) {
@@ -661,7 +619,10 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
             sc[r] = vis ? (sa[r] + sb[r]) * score_scale : -INFINITY;
             bm = fmaxf(bm, sc[r]);
         }
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        {   // with the other half-wave (one gfx950 half-wave swap, no LDS round trip)
+            auto hb = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, bm), __builtin_bit_cast(int, bm), false, false);
+            bm = fmaxf(__builtin_bit_cast(float, (int)hb[0]), __builtin_bit_cast(float, (int)hb[1]));
+        }
         // Position 0 is visible to every query, so without a split mn is
         // finite from the first block on; a split that starts later can hold
         // blocks a query sees none of (mn = -inf): exponents then use 0 as
@@ -678,7 +639,7 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
             p[r] = fast_exp2(sc[r] - mref);   // 0 for masked positions
             rs += p[r];
         }
-        rs += __shfl_xor(rs, 32);
+        rs = swap32_add(rs, rs);   // + the other half-wave's, as v + v[lane ^ 32]
         lsum = lsum * corr + rs;
         o0 *= corr; o1 *= corr; o2 *= corr; o3 *= corr;
         #pragma unroll

@@ -193,6 +193,37 @@ __device__ __forceinline__ float reduce4(float a, float b, float c, float d) {
     return row16_sum(v);
 }
 
+// Sum over aligned groups of N lanes (N = 8, 16 or 32); every lane of the
+// group gets the sum.  Within a row of 16 lanes: quad swaps, then the
+// half-row and row mirrors; across two rows: the gfx950 row swap.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16 || N == 32, "groups of 8, 16 or 32 lanes");
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    if constexpr (N >= 16)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    if constexpr (N >= 32) v = swap16_add(v, v);
+    return v;
+}
+
+// Maximum over aligned groups of N lanes, the same exchanges as group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(N == 8 || N == 16 || N == 32, "groups of 8, 16 or 32 lanes");
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    if constexpr (N >= 16)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    if constexpr (N >= 32) {
+        auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+        v = fmaxf(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
+    }
+    return v;
+}
+
 // Maximum over a row of 16 lanes with DPP (the exchanges of row16_sum).
 __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)));
@@ -218,6 +249,13 @@ __device__ __forceinline__ float wave_sum_all(float v) {
     v = row16_sum(v);
     v = swap16_add(v, v);
     return swap32_add(v, v);
+}
+
+// Lanes l < 32 get the value of lane l + 32 (one gfx950 half-wave swap, no
+// LDS round trip); lanes l >= 32 keep their own.
+__device__ __forceinline__ float upper_half(float v) {
+    auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return __builtin_bit_cast(float, (int)s[1]);
 }
 
 // Integer sum over each aligned group of four lanes (quad permutes).

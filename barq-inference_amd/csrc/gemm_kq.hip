@@ -897,20 +897,20 @@ struct KQExperts {
             const int v = __shfl_up(inc, o);
             if (l >= o) inc += v;
         }
-        total = __builtin_amdgcn_readfirstlane(__shfl(inc, 63)) * nmat * ks * tiles_n;
+        total = __builtin_amdgcn_readlane(inc, 63) * nmat * ks * tiles_n;
     }
 
     __device__ __forceinline__ KQTile operator()(int t) const {
         const int ntile = t % tiles_n, rk = t / tiles_n, ksl = rk % ks, r = rk / ks, mat = r % nmat, s = r / nmat;
         // expert of m-slot s: the number of experts whose tiles all lie before it
         const int e = __builtin_amdgcn_readfirstlane(__popcll(__ballot(inc <= s)));
-        const int mt = s - __builtin_amdgcn_readfirstlane(__shfl(inc - nt, e));
-        const int row0 = __builtin_amdgcn_readfirstlane(__shfl(r0, e));
+        const int mt = s - __builtin_amdgcn_readlane(inc - nt, e);
+        const int row0 = __builtin_amdgcn_readlane(r0, e);
         KQTile T;
         T.W = wt.w[mat * ne + e];
         T.X = X + (size_t)row0 * xrb;
         T.Y = Y + (size_t)mat * ymat + (size_t)ksl * ykstride + (size_t)row0 * N;
-        T.count = __builtin_amdgcn_readfirstlane(__shfl(cnt, e));
+        T.count = __builtin_amdgcn_readlane(cnt, e);
         T.m0 = mt * BM;
         T.n0 = ntile * KQ_BN;
         T.kb0 = ksl * nsb_k;

@@ -540,7 +540,7 @@ void gemv_q8_glu_kernel(const uint8_t* __restrict__ G, const uint8_t* __restrict
 
     // lane 0: g0, lane 32: u0, lane 16: g1, lane 48: u1
     const float v = reduce4(acc[0], acc[1], P > 1 ? acc[2] : 0.0f, P > 1 ? acc[3] : 0.0f);
-    const float other = __shfl_xor(v, 32);
+    const float other = upper_half(v);
     if (l == 0) h[row0] = ffn_swiglu(v, other);
     if (P > 1 && l == 16 && last >= 1) h[row0 + 1] = ffn_swiglu(v, other);
 }
@@ -622,7 +622,7 @@ void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restric
     for (int t = 0; t < NX; t += 2) {
         const float v = reduce4(acc[2 * t], acc[2 * t + 1], t + 1 < NX ? acc[2 * t + 2] : 0.0f,
                                 t + 1 < NX ? acc[2 * t + 3] : 0.0f);
-        const float other = __shfl_xor(v, 32);
+        const float other = upper_half(v);
         if (l == 0) h[(size_t)t * n_rows + row] = ffn_swiglu(v, other);
         if (t + 1 < NX && l == 16) h[(size_t)(t + 1) * n_rows + row] = ffn_swiglu(v, other);
     }

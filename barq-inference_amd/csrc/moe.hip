@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void moe_group_gather_q8k_kernel(
         uint64_t todo = __ballot(e >= 0);
         while (todo) {   // wave-uniform: one round per distinct expert in the wave
             const int leader = __ffsll((unsigned long long)todo) - 1;
-            const int el = __shfl(e, leader);
+            const int el = __builtin_amdgcn_readlane(e, leader);   // leader is wave-uniform
             const uint64_t m = __ballot(e == el);
             if (e == el) rank = __popcll(m & ((1ull << lane) - 1ull));
             if (lane == leader) wcnt[wave][el] = __popcll(m);

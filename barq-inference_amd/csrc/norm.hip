@@ -28,9 +28,7 @@ constexpr int NORM_MAX_WAVES = 16;
 // (stored f16), q = roundf(x * (1 / d)).
 __device__ __forceinline__ void norm_q8_0_block(const float (&vv)[4], int lane, uint8_t* __restrict__ blk) {
     float a = fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3])));
-    a = fmaxf(a, __shfl_xor(a, 1));
-    a = fmaxf(a, __shfl_xor(a, 2));
-    a = fmaxf(a, __shfl_xor(a, 4));
+    a = group_max<8>(a);
     const float d = a / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int l8 = lane & 7;

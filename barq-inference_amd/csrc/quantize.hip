@@ -20,8 +20,7 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
     const int l = (int)(e % 32);
     const float v = x[e];
     float a = fabsf(v);
-    #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    a = group_max<32>(a);
     const float d = a / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q = (int)roundf(v * id);
@@ -94,8 +93,7 @@ __global__ __launch_bounds__(256) void swiglu_q8_0_kernel(const float* __restric
     const int l = (int)(e % 32);
     const float v = swiglu_form<true>(g[e], u[e]);
     float a = fabsf(v);
-    #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    a = group_max<32>(a);
     const float d = a / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q = (int)roundf(v * id);
@@ -123,8 +121,7 @@ __global__ __launch_bounds__(256) void quantize_q4_0_barq_kernel(const float* __
     const int l = (int)(e % 32);
     const float v = x[e];
     float a = fabsf(v);
-    #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    a = group_max<32>(a);
     const float scale = a == 0.0f ? 0.0f : a / 8.0f;
     int q = 0;
     if (scale != 0.0f) {
