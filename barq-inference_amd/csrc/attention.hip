@@ -377,12 +377,20 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
             const int s = sub + STEP * j + SUB * u;
             ov[j][u] = s < n_split ? pp[(size_t)s * (HD + 2) + 2 + d] : 0.0f;
         }
-    float M = -INFINITY, Ls = 0.0f, Ms = -INFINITY;
-    if (t < n_split) {
-        Ms = pp[(size_t)t * (HD + 2)];
-        Ls = pp[(size_t)t * (HD + 2) + 1];
+    // the maximum and sum of the splits t + NT j (j < K), loaded with the
+    // output sums above (n_split <= ATT_MAX_SPLIT = 1024, so these are all of
+    // this thread's splits): no load waits once the reductions start
+    static_assert(ATT_MAX_SPLIT <= 1024, "one split per virtual lane");
+    float Msj[K], Lsj[K];
+    #pragma unroll
+    for (int j = 0; j < K; j++) {
+        const int s = t + NT * j;
+        Msj[j] = s < n_split ? pp[(size_t)s * (HD + 2)] : -INFINITY;
+        Lsj[j] = s < n_split ? pp[(size_t)s * (HD + 2) + 1] : 0.0f;
     }
-    for (int s = t; s < n_split; s += NT) M = fmaxf(M, pp[(size_t)s * (HD + 2)]);
+    float M = Msj[0];
+    #pragma unroll
+    for (int j = 1; j < K; j++) M = fmaxf(M, Msj[j]);
     M = wave_max_all(M);
     if (lane == 0) sm.wred[0][wave] = M;
     __syncthreads();
@@ -390,20 +398,19 @@ __device__ __forceinline__ float attn_combine_head(const float* __restrict__ pp,
     #pragma unroll
     for (int u = 1; u < NWV; u++) M = fmaxf(M, sm.wred[0][u]);
     // The denominator in the 1024-thread merge's order whatever NT is: thread
-    // t plays the 1024 lanes t + NT j (j < K), each summing its splits
-    // s = t + NT j + 1024 u in u order; a butterfly per 64 of those lanes
-    // (a real wave holds 64 consecutive ones); then the 16 wave partials in
-    // lane order.  So the Q8_K merge's rows are the f32 merge's to the bit.
+    // t plays the 1024 lanes t + NT j (j < K), each holding its one split; a
+    // reduction per 64 of those lanes (a real wave holds 64 consecutive ones);
+    // then the 16 wave partials in lane order.  So the Q8_K merge's rows are
+    // the f32 merge's to the bit.
     float Lj[K];
     #pragma unroll
     for (int j = 0; j < K; j++) {
+        const int s = t + NT * j;
         float L = 0.0f;
-        for (int s = t + NT * j; s < n_split; s += 1024) {
-            const float ms = s == t ? Ms : pp[(size_t)s * (HD + 2)];
-            const float ls = s == t ? Ls : pp[(size_t)s * (HD + 2) + 1];
-            const float ws = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
+        if (s < n_split) {
+            const float ws = Msj[j] == -INFINITY ? 0.0f : fast_exp2(Msj[j] - M);
             sm.w[s] = ws;
-            L = __builtin_fmaf(ls, ws, L);
+            L = Lsj[j] * ws;
         }
         L = wave_sum_all(L);
         Lj[j] = L;
