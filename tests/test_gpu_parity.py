@@ -128,6 +128,37 @@ def test_quantize_act_bit_exact(be, orc, act):
         assert np.array_equal(got, ref)
 
 
+def test_quantize_q8_k_first_largest_magnitude(be, orc):
+    """Q8_K's scale comes from the signed value of the FIRST element with the
+    largest |x|; the device finds it by a wave maximum and a ballot (lane l
+    holds elements 4l .. 4l + 3), so place ties inside one lane, across
+    lanes with the later lane's element first in its lane, at the block's
+    last element, and over a whole block."""
+    k = 256
+    rows = []
+    b = synth.gen_f32(k, 31) * np.float32(0.5)
+    b[8], b[11] = -5.0, 5.0            # one lane (2): element 0 of it wins
+    rows.append(b)
+    b = synth.gen_f32(k, 32) * np.float32(0.5)
+    b[11], b[12] = 7.0, -7.0           # lanes 2 (last element) and 3 (first): index 11 wins
+    rows.append(b)
+    b = synth.gen_f32(k, 33) * np.float32(0.5)
+    b[255] = -6.0                      # the very last element
+    rows.append(b)
+    b = np.where(np.arange(k) % 3 == 0, 1.0, -1.0).astype(np.float32)   # every |x| equal
+    rows.append(b)
+    b = synth.gen_f32(k, 34) * np.float32(0.5)
+    b[200], b[17] = 3.0, -3.0          # the earlier index is in the lower lane
+    rows.append(b)
+    x = np.stack(rows).astype(np.float32)
+    got = host(be.quantize_act(B.Q8_K, dev(x)))
+    ref = np.concatenate([orc.quantize_act(B.Q8_K, r) for r in x])
+    assert np.array_equal(got, ref)
+    # the scale's sign follows the chosen element: d = 1 / (-127 / max)
+    d = got.reshape(len(rows), 292)[:, :4].copy().view(np.float32)[:, 0]
+    assert np.all(np.sign(d) == -np.sign(np.float32([-5.0, 7.0, -6.0, 1.0, -3.0])))
+
+
 def test_quantize_q4_0_barq_bit_exact(be, orc):
     x = act_rows(4096, 6, 31).reshape(-1)
     got = host(be.quantize_q4_0_barq(dev(x)))
