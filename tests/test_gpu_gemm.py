@@ -59,6 +59,16 @@ def test_gemm_mfma_q6k_full_scale_range(be, orc):
     run(be, orc, B.Q6_K, q6k_full_range(n, k, 5), n, k, m, 6)
 
 
+def test_gemm_q6k_128_row_tiles(be, orc):
+    """Q6_K prompts of 256+ rows against long K take 128 x 128 tiles (four
+    waves of 128 x 32, K slices): ragged M and N, and scales over the whole
+    int8 range (w' = sc*(q - 32) up to +4096 and down to -4064)."""
+    for n, k, m, full in [(520, 8192, 260, False), (136, 8192, 300, True)]:
+        print(f"gemm Q6_K 128-row tiles n={n} k={k} m={m} full-range={full}", flush=True)
+        w = q6k_full_range(n, k, 11) if full else synth.gen_weights(B.Q6_K, n, k, 10)
+        run(be, orc, B.Q6_K, w, n, k, m, 12 + m)
+
+
 def test_gemm_mfma_q4k_extreme_blocks(be, orc):
     # all-0xFF scale bytes (sc = m = 63), all-0xFF quants, f16 extremes for d / dmin
     n, k, m = 80, 512, 33

@@ -60,7 +60,7 @@ GEMM_VARIANTS = [
     dict(BARQ_GEMM_KS=2, BARQ_GEMM_BM=16), dict(BARQ_GEMM_KS=2, BARQ_GEMM_BM=65), dict(BARQ_GEMM_KS=4, BARQ_GEMM_BM=32),
     dict(BARQ_GEMM_DEFER=1), dict(BARQ_GEMM_DEFER=0), dict(BARQ_GEMM_DEFER=1, BARQ_GEMM_KS=2),
     dict(BARQ_GEMM_DEFER=2), dict(BARQ_GEMM_DEFER=3), dict(BARQ_GEMM_DEFER=3, BARQ_GEMM_KS=2), dict(BARQ_GEMM_DEFER=2, BARQ_GEMM_KS=4),
-    dict(BARQ_GEMM_BM=66), dict(BARQ_GEMM_BM=66, BARQ_GEMM_KS=2),
+    dict(BARQ_GEMM_BM=66), dict(BARQ_GEMM_BM=66, BARQ_GEMM_KS=2), dict(BARQ_GEMM_BM=67), dict(BARQ_GEMM_BM=67, BARQ_GEMM_KS=2),
 ]
 
 
