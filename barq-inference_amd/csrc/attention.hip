@@ -155,7 +155,6 @@ constexpr float LOG2E = 1.44269504088896340736f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-
 // K/V rows are streamed once per call: loaded with the non-temporal hint
 // (measured in one run: 55.1 -> 49.5 us at 32K positions, 14.1 -> 13.5 us at 4K)
 typedef float f32x4n __attribute__((ext_vector_type(4)));

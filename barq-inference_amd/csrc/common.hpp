@@ -156,16 +156,6 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Full wave sum; the result is wave-uniform.
-__device__ __forceinline__ float wave_sum(float v) {
-    v = row16_sum(v);
-    float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return (a + b) + (c + d);
-}
-
 // Sum R per-lane partials (one per row) over the 64 lanes with the gfx950
 // lane-swap instructions: two rows fold into one register per swap, so R rows
 // cost ~R/2 swaps + one 16-lane DPP reduction instead of R full reductions.
@@ -262,16 +252,6 @@ __device__ __forceinline__ float upper_half(float v) {
 __device__ __forceinline__ int quad_isum(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
     v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-
-__device__ __forceinline__ int wave_isum(int v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
     return v;
 }
 
