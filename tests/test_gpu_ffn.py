@@ -6,7 +6,9 @@ expf, both within an ulp of exp); h's Q8 blocks byte-identical to
 quantizing the device's own f32 h; FFN outputs with Q8 activations within
 1e-3 relative L2 error, the north star's bar, and max-abs within 5e-3 of
 max |y| (conftest.assert_close_chained: h is quantized a second time, so an
-ulp of exp can move one element of h by one Q8 quantum); the literal f32
+ulp of exp can move one element of h by one Q8 quantum); the down
+projection, and the FFN output, within 1e-3 on both measures of the
+oracle's down projection fed the device's own h blocks; the literal f32
 FFN within 1e-5 on both measures."""
 import contextlib
 import os
@@ -101,6 +103,18 @@ def test_ffn_q8(be, orc, name):
     # already-quantized input rows give the same result bit for bit
     got_q = host(be.ffn(gt, gd, ut, ud, dt, dd, n_embd, n_ff, pa, dev(xq), m))
     assert np.array_equal(got_q, got)
+    # the down projection at the north star's 1e-3 bar: the oracle's down
+    # projection fed the device's own h blocks (swiglu of the device's gate
+    # and up products), so h's second quantization is out of the comparison;
+    # the FFN's output is held to the same bar against it (its h comes from
+    # the same products, up to the f32 summation order of a fused launch)
+    pd = B.Q8_PARTNER[dt]
+    g_dev = be.matmul(gt, gd, n_ff, n_embd, pa, dev(xq), m)
+    u_dev = be.matmul(ut, ud, n_ff, n_embd, pa, dev(xq), m)
+    hq = be.swiglu(pd, g_dev, u_dev)
+    down_ref = orc.matmul(dt, down, n_embd, n_ff, pd, host(hq), m)
+    assert_close_1e3(host(be.matmul(dt, dd, n_embd, n_ff, pd, hq, m)), down_ref)
+    assert_close_1e3(got, down_ref)
 
 
 def test_ffn_fused_gate_up_matches_separate_path(be, orc):
