@@ -156,10 +156,16 @@ constexpr float LOG2E = 1.44269504088896340736f;
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // K/V rows are streamed once per call: loaded with the non-temporal hint
-// (measured in one run: 55.1 -> 49.5 us at 32K positions, 14.1 -> 13.5 us at 4K)
+// (measured in one run: 55.1 -> 49.5 us at 32K positions, 14.1 -> 13.5 us at 4K),
+// through a buffer descriptor over `bytes` bytes from `base`: reads at or past
+// the limit return zeros and touch no memory.  Cache policy 2 is the
+// non-temporal bit.
 typedef float f32x4n __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float4 ntf4(const f32x4n* p) {
-    const f32x4n v = __builtin_nontemporal_load(p);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rows(const float* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 kv_ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const f32x4n v = __builtin_bit_cast(f32x4n, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
@@ -219,16 +225,17 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
     struct Rows {
         float4 k[P][2], v[P][2];
     };
+    // Rows are read through buffer descriptors limited to [j0, j1): a row
+    // past the range reads as zeros without a memory access (its score is
+    // masked and its weight is 0), so a block's loads need no condition.
+    const __amdgpu_buffer_rsrc_t kr = kv_rows(kh + (size_t)j0 * HD, (uint32_t)(j1 - j0) * (HD * 4));
+    const __amdgpu_buffer_rsrc_t vr = kv_rows(vh + (size_t)j0 * HD, (uint32_t)(j1 - j0) * (HD * 4));
     auto load = [&](Rows& b, int blk) {
         #pragma unroll
         for (int p = 0; p < P; p++) {
-            // a row past the range loads the range's last row instead (finite
-            // values, no zero fill): its score is masked and its weight is 0
-            const int j = min(blk + p * R + r, j1 - 1);
-            const f32x4n* kp = reinterpret_cast<const f32x4n*>(kh + (size_t)j * HD);
-            const f32x4n* vp = reinterpret_cast<const f32x4n*>(vh + (size_t)j * HD);
-            b.k[p][0] = ntf4(kp + c); b.k[p][1] = ntf4(kp + c + LPR);
-            b.v[p][0] = ntf4(vp + c); b.v[p][1] = ntf4(vp + c + LPR);
+            const uint32_t off = (uint32_t)(blk - j0 + p * R + r) * (HD * 4) + (uint32_t)c * 16;
+            b.k[p][0] = kv_ld(kr, off); b.k[p][1] = kv_ld(kr, off + LPR * 16);
+            b.v[p][0] = kv_ld(vr, off); b.v[p][1] = kv_ld(vr, off + LPR * 16);
         }
     };
     auto block = [&](const Rows& b, int blk) {
@@ -252,16 +259,23 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
                 sc[p] = blk + p * R + r < j1 ? dot * score_scale : -INFINITY;
                 bm = fmaxf(bm, sc[p]);
             }
-            if (bm == -INFINITY) continue;             // no live row of this lane's in the block
+            // No branch on a block without live rows: a branch around the
+            // V products lets the compiler's wait insertion assume the V
+            // loads may still be in flight at the next block's loads into
+            // the same registers, and it waits for every load there.  With
+            // no live row so far (mn = -inf) the reference point 0 gives
+            // corr = e = 0; with no live row in the block but some before,
+            // corr = exp2(0) = 1 and e = 0, leaving the state as it was.
             const float mn = fmaxf(m[g], bm);
-            const float corr = fast_exp2(m[g] - mn);  // 0 while m is -inf
+            const float ref = mn == -INFINITY ? 0.0f : mn;
+            const float corr = fast_exp2(m[g] - ref);  // 0 while m is -inf
             m[g] = mn;
             l[g] *= corr;
             #pragma unroll
             for (int d = 0; d < 8; d++) o[g][d] *= corr;
             #pragma unroll
             for (int p = 0; p < P; p++) {
-                const float e = fast_exp2(sc[p] - mn);  // 0 for rows past the range
+                const float e = fast_exp2(sc[p] - ref);  // 0 for rows past the range
                 const float4 v0 = b.v[p][0], v1 = b.v[p][1];
                 l[g] += e;
                 o[g][0] = __builtin_fmaf(e, v0.x, o[g][0]);
@@ -276,16 +290,27 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
         }
     };
     if (j0 < j1) {
-        // two row buffers used in turn (no register copies between blocks)
+        // two row buffers used in turn (no register copies between blocks),
+        // each refilled two blocks ahead as soon as it has been scored.  The
+        // loads carry no condition (past the range they read zeros), so
+        // every block waits for its own loads only: with a conditional
+        // issue the compiler's wait counts cover both paths, and each block
+        // would also wait for the loads issued after it.
+        // Scheduling barriers keep the loads where they are written (the
+        // scheduler otherwise gathers all loads after both blocks).
         Rows ra, rb;
         load(ra, j0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(rb, j0 + R * P);
         for (int blk = j0; blk < j1; blk += 2 * R * P) {
-            const int b1 = blk + R * P;
-            if (b1 < j1) load(rb, b1);
+            __builtin_amdgcn_sched_barrier(0);
             block(ra, blk);
-            if (b1 >= j1) break;
-            if (b1 + R * P < j1) load(ra, b1 + R * P);
-            block(rb, b1);
+            __builtin_amdgcn_sched_barrier(0);
+            load(ra, blk + 2 * R * P);
+            __builtin_amdgcn_sched_barrier(0);
+            block(rb, blk + R * P);
+            __builtin_amdgcn_sched_barrier(0);
+            load(rb, blk + 3 * R * P);
         }
     }
 
