@@ -290,27 +290,29 @@ void attn_kernel(const float* __restrict__ q, const float* __restrict__ kc, cons
         }
     };
     if (j0 < j1) {
-        // two row buffers used in turn (no register copies between blocks),
-        // each refilled two blocks ahead as soon as it has been scored.  The
+        // NB row buffers used in turn (no register copies between blocks),
+        // each refilled NB blocks ahead as soon as it has been scored.  The
         // loads carry no condition (past the range they read zeros), so
         // every block waits for its own loads only: with a conditional
         // issue the compiler's wait counts cover both paths, and each block
         // would also wait for the loads issued after it.
         // Scheduling barriers keep the loads where they are written (the
-        // scheduler otherwise gathers all loads after both blocks).
-        Rows ra, rb;
-        load(ra, j0);
-        __builtin_amdgcn_sched_barrier(0);
-        load(rb, j0 + R * P);
-        for (int blk = j0; blk < j1; blk += 2 * R * P) {
+        // scheduler otherwise gathers all loads after the blocks).
+        constexpr int NB = 2;
+        Rows rows[NB];
+        #pragma unroll
+        for (int q = 0; q < NB; q++) {
+            load(rows[q], j0 + q * R * P);
             __builtin_amdgcn_sched_barrier(0);
-            block(ra, blk);
-            __builtin_amdgcn_sched_barrier(0);
-            load(ra, blk + 2 * R * P);
-            __builtin_amdgcn_sched_barrier(0);
-            block(rb, blk + R * P);
-            __builtin_amdgcn_sched_barrier(0);
-            load(rb, blk + 3 * R * P);
+        }
+        for (int blk = j0; blk < j1; blk += NB * R * P) {
+            #pragma unroll
+            for (int q = 0; q < NB; q++) {
+                __builtin_amdgcn_sched_barrier(0);
+                block(rows[q], blk + q * R * P);
+                __builtin_amdgcn_sched_barrier(0);
+                load(rows[q], blk + (q + NB) * R * P);
+            }
         }
     }
 
@@ -793,14 +795,21 @@ size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t 
 }
 
 
-// Splits: about 512 workgroups in all (two per CU; measured best on MI355X
-// for 4K-32K positions), at least 64 positions each.
+// Splits: at most about three workgroups per four CUs in all, whole
+// multiples of 64 positions each.  A CU that runs two workgroups while
+// others run one finishes last, so the launch keeps to one per CU; fewer,
+// longer workgroups keep more loads in flight each.  Measured on MI355X
+// (Llama-3-8B heads, us per call, targets 192 / 256 / 320 / 512 workgroups):
+// 4096 positions 10.96 / 11.09 / 11.08 / 11.73, 4097 11.03 / 11.00 / 13.30 /
+// 13.27, 8192 15.62 / 15.88 / 15.92 / 16.04, 16384 25.13 / 25.39 / 31.01 /
+// 25.68; the decode layer about 51.5 / 51.6 / 53.9 / 53.9.
 void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len, int* n_split, int* chunk) {
     const size_t g = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
     const size_t groups = (g == 1 || g > 8 || (g & (g - 1))) ? n_head : n_head_kv;
     const size_t wg = groups * (q_len ? q_len : 1);
     const int wg_override = tuning_env(TUNE_ATTN_WG);   // workgroup-count target (tuning)
-    const size_t target = wg_override > 0 ? (size_t)wg_override : 512;
+    const size_t cus = (size_t)cu_count_attn();
+    const size_t target = wg_override > 0 ? (size_t)wg_override : (cus * 3 / 4 > 0 ? cus * 3 / 4 : 1);
     size_t ns = (target + wg - 1) / wg;
     size_t max_ns = (kv_len + 63) / 64;
     if (max_ns > (size_t)ATT_MAX_SPLIT) max_ns = ATT_MAX_SPLIT;

@@ -124,6 +124,8 @@ ATTN_CASES = [
     (32, 8, 128, 1, 63, 62, 63),
     (32, 8, 128, 1, 65, 64, 80),
     (32, 8, 128, 1, 1000, 999, 1000),
+    (32, 8, 128, 1, 4097, 4096, 4100),    # one position past 4096: a short last split
+    (32, 8, 128, 1, 20000, 19999, 20000),
     (8, 8, 64, 1, 300, 299, 300),         # no grouping
     (16, 2, 128, 1, 700, 699, 700),       # 8 query heads per kv head
     (12, 6, 128, 1, 500, 499, 512),       # 2 per kv head
