@@ -814,6 +814,10 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
     size_t max_ns = (kv_len + 63) / 64;
     if (max_ns > (size_t)ATT_MAX_SPLIT) max_ns = ATT_MAX_SPLIT;
     if (ns > max_ns) ns = max_ns;
+    // at most 2^20 positions per split: the split kernel addresses its rows
+    // with 32-bit byte offsets (under 1 GiB at head_dim 256)
+    const size_t min_ns = (kv_len + ((size_t)1 << 20) - 1) >> 20;
+    if (ns < min_ns) ns = min_ns;
     if (ns < 1) ns = 1;
     size_t ch = (kv_len + ns - 1) / ns;
     ch = (ch + 63) / 64 * 64;
