@@ -28,8 +28,13 @@
 #include "mfma_common.hpp"
 #include "q8k_block.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <functional>
+#include <queue>
+#include <utility>
+#include <vector>
 
 namespace barq {
 
@@ -506,17 +511,27 @@ void attn_combine_q8k_kernel(const float* __restrict__ part, int n_split, int n_
     }
 }
 
+// Position blocks of 32 that query block qb sees (am_qblock's range).
+__host__ __device__ __forceinline__ int am_qblock_blocks(int qb, int q_len, int kv_len, long long start_pos) {
+    const int i_last = qb * 32 + 31 < q_len - 1 ? qb * 32 + 31 : q_len - 1;
+    const long long vis_last = start_pos + i_last + 1;
+    const int j_end = (int)(vis_last < kv_len ? vis_last : kv_len);
+    return (j_end + 31) / 32;
+}
+
 // The merge for a few splits (the prompt kernel's): one thread per output
 // value, 256 per workgroup (the 256 / HD heads of one Q8_K block of row i);
 // Q8 writes the block's Q8_K bytes (q8_k_block) instead of the f32 values.
 template <int HD, bool Q8>
 __global__ __launch_bounds__(256)
-void attn_combine_few_kernel(const float* __restrict__ part, int n_split, int n_head, float* __restrict__ out,
-                             uint8_t* __restrict__ out_q8) {
+void attn_combine_few_kernel(const float* __restrict__ part, int stride, int chunk, int n_head, int q_len, int kv_len,
+                             long long start_pos, float* __restrict__ out, uint8_t* __restrict__ out_q8) {
     __shared__ __align__(16) float vals[256];
     const int b = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
     const int h = b * (256 / HD) + t / HD, d = t % HD;
-    const float* pp = part + ((size_t)i * n_head + h) * n_split * (HD + 2);
+    // the pieces of row i's query block (attn_mfma_kernel's list)
+    const int n_split = (am_qblock_blocks(i / 32, q_len, kv_len, start_pos) + chunk - 1) / chunk;
+    const float* pp = part + ((size_t)i * n_head + h) * stride * (HD + 2);
     float M = -INFINITY;
     for (int sp = 0; sp < n_split; sp++) M = fmaxf(M, pp[(size_t)sp * (HD + 2)]);
     float L = 0.0f, O = 0.0f;
@@ -592,11 +607,12 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
                                           const float* __restrict__ kc, const float* __restrict__ vc, size_t layer_off,
                                           size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
                                           long long start_pos, float score_scale, float* __restrict__ out, int qb,
-                                          int n_split = 1, int split = 0, float* __restrict__ part = nullptr) {
+                                          int chunk = 0, int split = 0, int stride = 1,
+                                          float* __restrict__ part = nullptr, int grp = -1) {
     constexpr int HD = 128;
     const int l = threadIdx.x & 63, c = l & 31, g = l >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h = (int)blockIdx.y * W + wave;
+    const int h = (grp < 0 ? (int)blockIdx.y : grp) * W + wave;
     const int hk = (int)((long long)h * n_head_kv / n_head);   // the same for the W heads
     const int i0 = qb * 32, qi = i0 + c;
     const bool q_ok = qi < q_len;
@@ -605,12 +621,11 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
     const float* vh = vc + layer_off + (size_t)hk * head_stride;
     const i32x4v kr = make_rsrc4(kh, (uint32_t)kv_len * 512u);
     const i32x4v vr = make_rsrc4(vh, (uint32_t)kv_len * 512u);
-    const int i_last = min(i0 + 31, q_len - 1);
-    const long long vis_last = start_pos + i_last + 1;
-    const int j_end = (int)(vis_last < kv_len ? vis_last : kv_len);
-    const int nblk_all = (j_end + 31) / 32;
-    const int per = (nblk_all + n_split - 1) / n_split;
-    const int b_lo = min(split * per, nblk_all), nblk = min(b_lo + per, nblk_all);
+    const int nblk_all = am_qblock_blocks(qb, q_len, kv_len, start_pos);
+    // chunk > 0: this workgroup takes blocks [split, split + 1) * chunk of
+    // the query block's range and writes a partial state
+    const int b_lo = chunk > 0 ? min(split * chunk, nblk_all) : 0;
+    const int nblk = chunk > 0 ? min(b_lo + chunk, nblk_all) : nblk_all;
     if (b_lo < nblk) am_issue<W>(lds[0], kr, vr, (uint32_t)b_lo * 32u * 512u, wave, l);
 
     float qv[64];
@@ -685,9 +700,9 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
             o3 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[st], o3, 0, 0, 0);
         }
     }
-    if (n_split > 1) {
+    if (chunk > 0) {
         if (q_ok) {
-            float* pp = part + (((size_t)qi * n_head + h) * n_split + split) * (HD + 2);
+            float* pp = part + (((size_t)qi * n_head + h) * stride + split) * (HD + 2);
             if (g == 0) {
                 pp[0] = m;
                 pp[1] = lsum;
@@ -715,17 +730,39 @@ __device__ __forceinline__ void am_qblock(uint8_t (&lds)[2][2 * AM_BLK], const f
 // Causal prompts leave query block qb with qb + 1 position blocks (plus the
 // cached prefix).  PAIR: workgroup x takes the long block nqb - 1 - x and
 // then the short block x, so every workgroup has about the same work (used
-// when the pairs alone fill the CUs); otherwise the longest blocks start first.
+// when the pairs alone fill the CUs).  Otherwise, with chunk > 0, each query
+// block's range is cut into pieces of chunk blocks, and workgroup x takes
+// piece x of the list that runs from the longest query block down (so no
+// workgroup has more than chunk blocks, whatever the query block); with
+// chunk == 0 workgroup x takes query block nqb - 1 - x whole.
 template <int W, bool PAIR>
 __global__ __launch_bounds__(64 * W)
 void attn_mfma_kernel(const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
                       size_t layer_off, size_t head_stride, int n_head, int n_head_kv, int q_len, int kv_len,
-                      long long start_pos, float score_scale, float* __restrict__ out, float* __restrict__ part) {
+                      long long start_pos, float score_scale, float* __restrict__ out, float* __restrict__ part,
+                      int chunk, int stride) {
     __shared__ __align__(16) uint8_t lds[2][2 * AM_BLK];
     const int nqb = (q_len + 31) / 32, x = blockIdx.x;
+    if (!PAIR && chunk > 0) {
+        // the list is ordered by length across the head groups: workgroup x
+        // takes piece x / G of head group x % G (G = n_head / W groups; the
+        // grid is one-dimensional here)
+        const int groups = n_head / W;
+        const int grp = x % groups;
+        int qb = nqb - 1, rem = x / groups;
+        for (; qb >= 0; qb--) {
+            const int pieces = (am_qblock_blocks(qb, q_len, kv_len, start_pos) + chunk - 1) / chunk;
+            if (rem < pieces) break;
+            rem -= pieces;
+        }
+        if (qb < 0) return;   // past the list (the grid is its length)
+        am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale,
+                     out, qb, chunk, rem, stride, part, grp);
+        return;
+    }
     const int qb_long = nqb - 1 - x;
     am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale, out,
-                 qb_long, (int)gridDim.z, (int)blockIdx.z, part);
+                 qb_long);
     if (PAIR && x < qb_long) {
         __syncthreads();   // every wave is done with the stages
         am_qblock<W>(lds, q, kc, vc, layer_off, head_stride, n_head, n_head_kv, q_len, kv_len, start_pos, score_scale,
@@ -745,30 +782,112 @@ static int cu_count_attn();
 
 // Launch plan of the prompt kernel: W query heads per workgroup (W divides
 // the GQA group), query-block pairing when the pairs alone fill the CUs, and
-// otherwise a split of the positions (partial states merged by
-// attn_combine_few_kernel) until about one workgroup per CU runs.
+// otherwise pieces of `chunk` position blocks (partial states merged by
+// attn_combine_few_kernel): chunk is the work per CU if the blocks of all
+// query blocks were shared evenly, so no workgroup runs much longer than the
+// average.  The plan assumes the chunk's queries are the last q_len of the
+// kv_len positions (a prompt); at launch only the piece counts follow the
+// actual start position, within `stride` pieces per query block (the
+// workspace bound).
 struct AmPlan {
-    int w, n_split;
+    int w;
+    int chunk;    // position blocks per piece; 0: whole query blocks, no partial states
+    int stride;   // partial states per (query row, head)
     bool pair;
     unsigned nqb, groups;
 };
 
-static AmPlan attn_mfma_plan(size_t n_head, size_t n_head_kv, size_t q_len) {
+static AmPlan attn_mfma_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len) {
     AmPlan p{};
     const size_t grp = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
     p.w = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1;
     p.nqb = (unsigned)((q_len + 31) / 32);
     p.groups = (unsigned)(n_head / p.w);
-    const size_t cus = (size_t)cu_count_attn(), wgs = (size_t)p.nqb * p.groups;
+    const size_t cus = (size_t)cu_count_attn();
     p.pair = (size_t)(p.nqb / 2) * p.groups >= cus;
-    p.n_split = 1;
-    // measured on MI355X (Llama-3-8B heads, us per call for 1 / 2 / 4 / 8
-    // splits): 256 tokens 45.6 / 34.6 / 31.3 / 38.9, 512 tokens 85.0 / 60.1 /
-    // 68.4 / 83.9, 1024 tokens 164 / 174 / 190 / 224: about one workgroup per CU
-    if (!p.pair)
-        while (p.n_split < 8 && wgs * (size_t)p.n_split * 2 <= cus) p.n_split *= 2;
-    const int ovr = tuning_env(TUNE_ATTN_MFMA_SPLIT);
-    if (ovr > 0 && !p.pair) p.n_split = ovr < ATT_MAX_SPLIT ? ovr : ATT_MAX_SPLIT;
+    p.chunk = 0;
+    p.stride = 1;
+    // the merge writes whole Q8_K blocks (256 values: two heads of 128)
+    if (p.pair || (n_head * 128) % 256 != 0) return p;
+    const long long start = kv_len > q_len ? (long long)(kv_len - q_len) : 0;
+    size_t total = 0;
+    int longest = 0;
+    for (unsigned qb = 0; qb < p.nqb; qb++) {
+        const int nb = am_qblock_blocks((int)qb, (int)q_len, (int)kv_len, start);
+        total += (size_t)nb;
+        longest = nb > longest ? nb : longest;
+    }
+    (void)total;
+    // Choose the chunk by simulating the launch in units of one position
+    // block: the pieces in the kernel's order (each costing its blocks + 1.5
+    // for its fixed part: the query rows, the first copy, the partial state),
+    // every CU holding up to two workgroups that share it equally, each
+    // further piece going to the CU that frees a slot first.  Candidates cut
+    // the longest query block into k = 1 .. 64 pieces; ties keep fewer
+    // pieces.  The model picks the measured best at 512, 768 and 1024 tokens
+    // (Llama-3-8B heads, us per call, chunk: time): 512 tokens 6: 55.5, 3:
+    // 59.3, 8: 61.8, 4: 63.3; 768 tokens 6: 86.2, 12: 97, 4: 97.6, 5: 99.3,
+    // 8: 100, 16: 102.3, 24: 122; 1024 tokens 11: 132, 6: 138, 32 (whole
+    // query blocks): 157.4, 8: 157.6.  (With a fixed part of 1 block it chose
+    // 5 at 768 tokens.)
+    std::vector<int> nbs(p.nqb);
+    for (unsigned qb = 0; qb < p.nqb; qb++) nbs[qb] = am_qblock_blocks((int)qb, (int)q_len, (int)kv_len, start);
+    auto simulate = [&](int c) {
+        std::vector<double> jobs;   // the kernel's order: query blocks longest first, then the head groups
+        for (int qb = (int)p.nqb - 1; qb >= 0; qb--)
+            for (int b = 0; b < nbs[qb]; b += c) {
+                const double len = (nbs[qb] - b < c ? nbs[qb] - b : c) + 1.5;
+                for (unsigned g = 0; g < p.groups; g++) jobs.push_back(len);
+            }
+        struct Cu { double t, w[2]; int n; };
+        std::vector<Cu> cu(cus, Cu{0.0, {0.0, 0.0}, 0});
+        size_t next = 0;
+        for (int pass = 0; pass < 2; pass++)
+            for (size_t k = 0; k < cus && next < jobs.size(); k++) cu[k].w[cu[k].n++] = jobs[next++];
+        auto event = [](const Cu& u) {
+            return u.n == 2 ? u.t + 2.0 * (u.w[0] < u.w[1] ? u.w[0] : u.w[1]) : u.t + u.w[0];
+        };
+        typedef std::pair<double, size_t> Ev;
+        std::priority_queue<Ev, std::vector<Ev>, std::greater<Ev>> heap;
+        for (size_t k = 0; k < cus; k++)
+            if (cu[k].n) heap.push(Ev(event(cu[k]), k));
+        double end = 0.0;
+        while (!heap.empty()) {
+            const Ev ev = heap.top();
+            heap.pop();
+            Cu& u = cu[ev.second];
+            if (u.n == 2) {   // the shorter job ends; the other has done as much
+                const int done = u.w[0] < u.w[1] ? 0 : 1;
+                u.w[0] = u.w[1 - done] - u.w[done];
+                u.n = 1;
+            } else {
+                u.n = 0;
+            }
+            u.t = ev.first;
+            end = ev.first > end ? ev.first : end;
+            if (next < jobs.size()) u.w[u.n++] = jobs[next++];
+            if (u.n) heap.push(Ev(event(u), ev.second));
+        }
+        return end;
+    };
+    size_t chunk = (size_t)longest;
+    double best = simulate(longest);
+    for (int k = 2; k <= 64 && k <= longest; k++) {
+        const int c = (longest + k - 1) / k;
+        if ((size_t)c >= chunk) continue;
+        const double e = simulate(c);
+        if (e < best - 1e-9) {
+            best = e;
+            chunk = (size_t)c;
+        }
+    }
+    const int ovr = tuning_env(TUNE_ATTN_MFMA_SPLIT);   // pieces of the longest query block (tuning)
+    if (ovr > 0) chunk = ((size_t)longest + (size_t)ovr - 1) / (size_t)ovr;
+    if (chunk < 1) chunk = 1;
+    if (chunk >= (size_t)longest) return p;   // every query block in one piece
+    const size_t nbmax = (kv_len + 31) / 32;
+    p.chunk = (int)chunk;
+    p.stride = (int)((nbmax + chunk - 1) / chunk);
     return p;
 }
 
@@ -786,8 +905,8 @@ static int cu_count_attn() {
 
 size_t attention_workspace(size_t n_head, size_t head_dim, size_t q_len, size_t kv_len, size_t n_head_kv) {
     if (head_dim == 128 && q_len >= (size_t)attn_mfma_min_q() && kv_len < ((size_t)1 << 23)) {
-        const AmPlan p = attn_mfma_plan(n_head, n_head_kv, q_len);
-        return p.n_split > 1 ? (size_t)p.n_split * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
+        const AmPlan p = attn_mfma_plan(n_head, n_head_kv, q_len, kv_len);
+        return p.chunk > 0 ? (size_t)p.stride * n_head * q_len * (head_dim + 2) * sizeof(float) : 0;
     }
     int ns = 0, chunk = 0;
     attention_plan(n_head, n_head_kv, q_len, kv_len, &ns, &chunk);
@@ -832,7 +951,7 @@ void attention_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len
 // quantizes them.
 bool attention_q8_direct(const AttnArgs& a) {
     if ((a.n_head * a.head_dim) % 256 != 0) return false;
-    if (attn_mfma_path(a)) return attn_mfma_plan(a.n_head, a.n_head_kv, a.q_len).n_split > 1;
+    if (attn_mfma_path(a)) return attn_mfma_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len).chunk > 0;
     int ns = 0, chunk = 0;
     attention_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len, &ns, &chunk);
     return ns > 1;
@@ -872,32 +991,35 @@ hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
     if (a.q_len == 0 || a.n_head == 0) return hipSuccess;
     if (attn_mfma_path(a)) {
         const float scale = (1.0f / sqrtf(128.0f)) * LOG2E;
-        const AmPlan p = attn_mfma_plan(a.n_head, a.n_head_kv, a.q_len);
+        const AmPlan p = attn_mfma_plan(a.n_head, a.n_head_kv, a.q_len, a.kv_len);
         const int w = p.w;
         const bool pair = p.pair;
-        const dim3 grid(pair ? (p.nqb + 1) / 2 : p.nqb, p.groups, (unsigned)p.n_split);
+        unsigned nx = pair ? (p.nqb + 1) / 2 : p.nqb;
+        if (p.chunk > 0) {   // the pieces of every query block at the actual start position
+            nx = 0;
+            for (unsigned qb = 0; qb < p.nqb; qb++)
+                nx += (unsigned)((am_qblock_blocks((int)qb, (int)a.q_len, (int)a.kv_len, (long long)a.start_pos) +
+                                  p.chunk - 1) / p.chunk);
+        }
+        const dim3 grid = p.chunk > 0 ? dim3(nx * p.groups, 1, 1) : dim3(nx, p.groups, 1);
 #define BARQ_AM_LAUNCH(W_, P_)                                                                                    \
     hipLaunchKernelGGL((attn_mfma_kernel<W_, P_>), grid, dim3(64 * W_), 0, s, a.q, a.k, a.v, a.layer_off,           \
                        a.head_stride, (int)a.n_head, (int)a.n_head_kv, (int)a.q_len, (int)a.kv_len,               \
-                       (long long)a.start_pos, scale, a.out, a.part)
+                       (long long)a.start_pos, scale, a.out, a.part, p.chunk, p.stride)
         if (w == 4) { if (pair) BARQ_AM_LAUNCH(4, true); else BARQ_AM_LAUNCH(4, false); }
         else if (w == 2) { if (pair) BARQ_AM_LAUNCH(2, true); else BARQ_AM_LAUNCH(2, false); }
         else { if (pair) BARQ_AM_LAUNCH(1, true); else BARQ_AM_LAUNCH(1, false); }
 #undef BARQ_AM_LAUNCH
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess || p.n_split == 1) return e;
-        if ((a.n_head * 128) % 256 == 0) {
-            const dim3 cg((unsigned)(a.n_head * 128 / 256), (unsigned)a.q_len);
-            if (a.out_q8)
-                hipLaunchKernelGGL((attn_combine_few_kernel<128, true>), cg, dim3(256), 0, s, a.part, p.n_split,
-                                   (int)a.n_head, a.out, a.out_q8);
-            else
-                hipLaunchKernelGGL((attn_combine_few_kernel<128, false>), cg, dim3(256), 0, s, a.part, p.n_split,
-                                   (int)a.n_head, a.out, a.out_q8);
-        } else {
-            hipLaunchKernelGGL(attn_combine_kernel<128>, dim3((unsigned)a.n_head, (unsigned)a.q_len), dim3(1024), 0, s,
-                               a.part, p.n_split, (int)a.n_head, a.out);
-        }
+        if (e != hipSuccess || p.chunk == 0) return e;
+        // (the plan splits only when the rows are whole Q8_K blocks)
+        const dim3 cg((unsigned)(a.n_head * 128 / 256), (unsigned)a.q_len);
+        if (a.out_q8)
+            hipLaunchKernelGGL((attn_combine_few_kernel<128, true>), cg, dim3(256), 0, s, a.part, p.stride, p.chunk,
+                               (int)a.n_head, (int)a.q_len, (int)a.kv_len, (long long)a.start_pos, a.out, a.out_q8);
+        else
+            hipLaunchKernelGGL((attn_combine_few_kernel<128, false>), cg, dim3(256), 0, s, a.part, p.stride, p.chunk,
+                               (int)a.n_head, (int)a.q_len, (int)a.kv_len, (long long)a.start_pos, a.out, a.out_q8);
         return hipGetLastError();
     }
     switch (a.head_dim) {

@@ -143,6 +143,8 @@ ATTN_CASES = [
     (6, 4, 128, 33, 33, 0, 40),           # irregular grouping
     (8, 2, 128, 40, 100, 20, 100),        # start_pos + q_len < kv_len: masked tail
     (32, 8, 128, 512, 512, 0, 512),       # a Llama-3-8B prompt of 512 tokens
+    (32, 8, 128, 768, 768, 0, 768),       # pieces of 6 position blocks, two workgroups per CU
+    (32, 8, 128, 200, 1000, 800, 1000),   # a chunk after a long prefix: every query block in pieces
     (4, 2, 64, 48, 48, 0, 48),            # head_dim 64 stays on the split kernel
     (32, 32, 128, 512, 512, 0, 512),      # query blocks paired (long + short) per workgroup
     (64, 64, 128, 288, 300, 12, 300),     # paired, odd block count (the middle block alone)
