@@ -327,7 +327,7 @@ void b32_gemm_kernel(const uint8_t* __restrict__ W, uint32_t wrb, const int8_t* 
             #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (row < M) out[(size_t)row * N + col] = acc[t][r];
+                if (row < M) __builtin_nontemporal_store(acc[t][r], &out[(size_t)row * N + col]);
             }
     }
 }
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void slice_sum_kernel(const float* __restrict_
     if (i >= n) return;
     float a = P[i];
     for (int sl = 1; sl < ks; sl++) a += P[(size_t)sl * n + i];
-    Y[i] = a;
+    __builtin_nontemporal_store(a, &Y[i]);
 }
 
 // ---- launch ------------------------------------------------------------------

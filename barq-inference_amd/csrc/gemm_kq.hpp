@@ -552,7 +552,10 @@ __device__ __forceinline__ void kq_round(std::integer_sequence<int, S...>, uint8
     (kq_step<F, BM, NW, NS, KG, S>(stages, b + S, nst, xr, wr, off, kg, wave, l, acc), ...);
 }
 
-// Tile results to Y[row * N + col] for rows < count and columns < N.
+// Tile results to Y[row * N + col] for rows < count and columns < N, with
+// non-temporal stores: lines the next kernel reads from memory anyway are
+// not left dirty in L2 (measured: C4 25.6-26.8 against 27.2-28.1 us, the
+// prefill layer 452-454 against 461-463 us, C5 231 against 234-237 us).
 template <class F, int BM, int NW>
 __device__ __forceinline__ void kq_store(const float (&acc)[KQL<F, BM, NW>::MTW][16], float* Y, int count, int N,
                                          int m0, int n0, int wave, int l) {
@@ -565,7 +568,7 @@ __device__ __forceinline__ void kq_store(const float (&acc)[KQL<F, BM, NW>::MTW]
                 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = m0 + 4 * (l >> 4) + r;
-                    if (row < count) Y[(size_t)row * N + col] = acc[0][4 * cb + r];
+                    if (row < count) __builtin_nontemporal_store(acc[0][4 * cb + r], &Y[(size_t)row * N + col]);
                 }
             }
         }
@@ -578,7 +581,7 @@ __device__ __forceinline__ void kq_store(const float (&acc)[KQL<F, BM, NW>::MTW]
             #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + mb + 32 * t + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (row < count) Y[(size_t)row * N + col] = acc[t][r];
+                if (row < count) __builtin_nontemporal_store(acc[t][r], &Y[(size_t)row * N + col]);
             }
     }
 }

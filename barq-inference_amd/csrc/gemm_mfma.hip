@@ -372,7 +372,7 @@ void gemm_kq_kernel(const uint8_t* __restrict__ W, size_t w_row_bytes, const uin
             #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int row = m0 + 16 * i + 4 * g + r;
-                if (row < M) Y[(size_t)row * N + col] = acc[i][r];
+                if (row < M) __builtin_nontemporal_store(acc[i][r], &Y[(size_t)row * N + col]);
             }
         }
     }
