@@ -249,6 +249,35 @@ def test_attention_q8k_equals_quantized_attention(be, n_head, n_kv, hd, q_len, k
     c.close()
 
 
+def test_attention_prompt_pieces_random_shapes(be, orc):
+    """Prompt chunks of seeded random lengths after random cached prefixes
+    (some with a masked tail: start_pos + q_len < kv_len) on the MFMA prompt
+    kernel, whose pieces per query block follow the launch simulation's chunk:
+    the f32 rows against the oracle, and the Q8_K merge against quantizing
+    them."""
+    rng = np.random.default_rng(2024)
+    for case in range(10):
+        n_head, n_kv = [(8, 2), (12, 6), (16, 4), (32, 8)][case % 4]
+        hd = 128
+        q_len = int(rng.integers(32, 200))
+        prefix = int(rng.integers(0, 400))
+        kv_len = prefix + q_len
+        start = prefix if case % 3 else max(0, prefix - int(rng.integers(1, 40)))
+        print(f"prompt pieces case {case}: n_head={n_head} n_kv={n_kv} q_len={q_len} kv_len={kv_len} "
+              f"start={start}", flush=True)
+        c, k, v = fill_cache(be, n_kv, hd, kv_len, 900 + case)
+        q = rng_f32(950 + case, n_head, q_len, hd)
+        y = A.compute_attention(be, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start)
+        ref = orc.attention(q, k, v, n_head, q_len, kv_len, start)
+        err = np.max(np.abs(y.cpu().numpy() - ref))
+        assert err <= 2e-5 * np.max(np.abs(v)), (case, err)
+        if (n_head * hd) % 256 == 0:
+            q8 = A.compute_attention_q8k(be, dev(q), c, 1, n_head, n_kv, hd, q_len, kv_len, start)
+            want = be.quantize_act(B.Q8_K, y.reshape(q_len, n_head * hd)).cpu().numpy().reshape(-1)
+            assert np.array_equal(q8.cpu().numpy().reshape(-1), want), case
+        c.close()
+
+
 def test_attention_q8k_argument_errors(be):
     c, k, v = fill_cache(be, 2, 64, 20, 3)
     q = rng_f32(1, 3, 1, 64)
