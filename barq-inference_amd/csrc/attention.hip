@@ -797,7 +797,30 @@ struct AmPlan {
     unsigned nqb, groups;
 };
 
+static AmPlan attn_mfma_plan_uncached(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len);
+
+// The plan of the last (n_head, n_head_kv, q_len, kv_len, device) this
+// thread asked for: the workspace query and the launch ask in turn.
 static AmPlan attn_mfma_plan(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len) {
+    struct Entry {
+        size_t key[4];
+        int dev;
+        AmPlan plan;
+        bool valid;
+    };
+    thread_local Entry last = {{0, 0, 0, 0}, -1, AmPlan{}, false};
+    if (tuning_env(TUNE_ATTN_MFMA_SPLIT) > 0) return attn_mfma_plan_uncached(n_head, n_head_kv, q_len, kv_len);
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    if (last.valid && last.dev == dev && last.key[0] == n_head && last.key[1] == n_head_kv && last.key[2] == q_len &&
+        last.key[3] == kv_len)
+        return last.plan;
+    const AmPlan p = attn_mfma_plan_uncached(n_head, n_head_kv, q_len, kv_len);
+    last = Entry{{n_head, n_head_kv, q_len, kv_len}, dev, p, true};
+    return p;
+}
+
+static AmPlan attn_mfma_plan_uncached(size_t n_head, size_t n_head_kv, size_t q_len, size_t kv_len) {
     AmPlan p{};
     const size_t grp = (n_head_kv && n_head % n_head_kv == 0) ? n_head / n_head_kv : 1;
     p.w = grp % 4 == 0 ? 4 : grp % 2 == 0 ? 2 : 1;
@@ -875,6 +898,11 @@ static AmPlan attn_mfma_plan(size_t n_head, size_t n_head_kv, size_t q_len, size
     for (int k = 2; k <= 64 && k <= longest; k++) {
         const int c = (longest + k - 1) / k;
         if ((size_t)c >= chunk) continue;
+        // more than eight pieces per CU never measured faster; the bound
+        // also keeps the simulation to a few thousand pieces
+        size_t n = 0;
+        for (int nb : nbs) n += (size_t)((nb + c - 1) / c);
+        if (n * p.groups > 8 * cus) break;   // smaller chunks only add pieces
         const double e = simulate(c);
         if (e < best - 1e-9) {
             best = e;
