@@ -232,7 +232,7 @@ def test_append_rope_q_equals_separate_steps(be, layout, n_head, n_kv, hd, n):
     (32, 8, 128, 40, 100, 60, 100),       # a prompt chunk on the MFMA kernel
     (8, 2, 64, 1, 1000, 999, 1000),       # head_dim 64: four heads per block
     (4, 2, 256, 1, 517, 516, 517),        # head_dim 256: one head per block
-    (8, 1, 64, 1, 20000, 19999, 20000),   # 313 splits: more than the 256 threads a head gets in the Q8_K merge
+    (8, 1, 64, 1, 20000, 19999, 20000),   # 157 splits (test_attention_q8k_many_splits: more than the merge's threads)
 ])
 def test_attention_q8k_equals_quantized_attention(be, n_head, n_kv, hd, q_len, kv_len, start, pos):
     """attention_q8k writes the bytes quantize_act(Q8_K) writes for the f32
@@ -320,12 +320,15 @@ def test_attention_mfma_kernel_small_chunks(be, orc, n_head, n_kv, q_len, kv_len
     c.close()
 
 
-def test_attention_q8k_many_splits_head_dim_128(be):
-    """More splits than the Q8_K merge's 512 threads per head at head_dim 128
-    (625 splits with BARQ_ATTN_WG=2048, read at handle creation): the merge
-    still writes the bytes the f32 merge's rows quantize to."""
+@pytest.mark.parametrize("hd,kv_len", [(128, 40000), (64, 20000)])
+def test_attention_q8k_many_splits(be, hd, kv_len):
+    """More splits than the Q8_K merge's threads per head (512 at head_dim
+    128, 256 at 64; 625 and 313 splits with BARQ_ATTN_WG=2048, read at handle
+    creation): the merge still writes the bytes the f32 merge's rows quantize
+    to."""
     import os
-    n_head, n_kv, hd, kv_len = 8, 1, 128, 40000
+    n_head, n_kv = 8, 1
+    print(f"attention_q8k many splits hd={hd} kv_len={kv_len}", flush=True)
     c, k, v = fill_cache(be, n_kv, hd, kv_len, 77)
     q = rng_f32(78, n_head, 1, hd)
     old = os.environ.get("BARQ_ATTN_WG")
