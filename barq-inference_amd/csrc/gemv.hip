@@ -201,7 +201,7 @@ __device__ __forceinline__ void gemv_q4k_rows_issue(const uint8_t* __restrict__ 
 // still be in flight), so only the last row's is left after the last byte.
 template <int R>
 __device__ __forceinline__ float gemv_q4k_rows_finish(int nblk, int l, const uint8_t* buf, Q4KXRaw& xr) {
-    static_assert(R == 2 || R == 4, "two or four rows per wave");
+    static_assert(R == 1 || R == 2 || R == 4, "one, two or four rows per wave");
     using F = FmtQ4K;
     const F::Lane c = F::lane(l);
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES;
@@ -995,9 +995,19 @@ hipError_t gemv_q8_launch(int w_type, const void* W, size_t n_rows, size_t k, co
         if (q4k_lds_supported(W, n_rows, k) && tuning_env(TUNE_GEMV_LDS, 1) && !env_cfg().r) {
             constexpr int WAVES = 4;
             const uint32_t bytes = (uint32_t)(n_rows * (k / 256 * Q4_K_BYTES));
-            if (tuning_env(TUNE_GEMV_LDS, 1) == 4) {
+            // rows per wave: one up to 4096 rows, two above (measured in one
+            // process, us per call, one row against two, k = 4096: 1024 rows
+            // 2.50-2.52 / 2.95-2.99, 4096 rows 3.77-3.79 / 3.90, 6144 rows
+            // 4.59 / 4.55, 14336 rows 7.95 / 7.19; outputs bit-identical).
+            // BARQ_GEMV_LDS = 2 / 3 / 4 force two / one / four.
+            const int mode = tuning_env(TUNE_GEMV_LDS, 1);
+            if (mode == 4) {
                 const unsigned grid = (unsigned)((n_rows + 4 * WAVES - 1) / (4 * WAVES));
                 hipLaunchKernelGGL((gemv_q4k_lds_kernel<WAVES, 4>), dim3(grid), dim3(WAVES * 64), 0, s, w, bytes, x,
+                                   y, n, (int)(k / 256));
+            } else if (mode == 3 || (mode == 1 && n_rows <= 4096)) {
+                const unsigned grid = (unsigned)((n_rows + WAVES - 1) / WAVES);
+                hipLaunchKernelGGL((gemv_q4k_lds_kernel<WAVES, 1>), dim3(grid), dim3(WAVES * 64), 0, s, w, bytes, x,
                                    y, n, (int)(k / 256));
             } else {
                 const unsigned grid = (unsigned)((n_rows + 2 * WAVES - 1) / (2 * WAVES));

@@ -343,8 +343,8 @@ void gemv_dma_kernel(const uint8_t* __restrict__ Wq, uint32_t rb, const uint8_t*
 // copies have landed.  No workgroup barrier.  The lane slicing, arithmetic
 // and reduction are gemv_dma_kernel<P, W, 1, 1>'s: the outputs are
 // bit-identical.
-template <class P>
-constexpr int pair32_buf = (2 * 128 * P::F::ROW_BLOCK_BYTES + 1023) / 1024 * 1024;
+template <class P, int R = 2>
+constexpr int pair32_buf = (R * 128 * P::F::ROW_BLOCK_BYTES + 1023) / 1024 * 1024;
 
 struct Q80XRaw {
     i32x4v v[4];
@@ -374,24 +374,26 @@ __device__ __forceinline__ void wait_vmcnt_upto4(uint32_t n) {
 // NX = 2-4 activation rows (x_row_bytes apart; y is [NX x n_rows]): every
 // row's block pair is loaded ahead of the copies and each (token, row)
 // product computed the same way, so y[j] equals the one-token GEMV of
-// activation row j bit for bit.
-template <class P, int WAVES, int NX = 1>
+// activation row j bit for bit.  R = 1: one weight row per wave (row 0's
+// arithmetic and reduction unchanged, so the same bits).
+template <class P, int WAVES, int NX = 1, int R = 2>
 __global__ __launch_bounds__(WAVES * 64)
 void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const uint8_t* __restrict__ xq,
                         float* __restrict__ y, int n_rows, int nblk, uint32_t x_row_bytes) {
     using F = typename P::F;
-    constexpr int BUF = pair32_buf<P>;
+    static_assert(R == 1 || R == 2, "one or two rows per wave");
+    constexpr int BUF = pair32_buf<P, R>;
     __shared__ __align__(16) uint8_t lds[WAVES][BUF];
     const int l = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * WAVES + wave) * 2;
+    const int row0 = (blockIdx.x * WAVES + wave) * R;
     if (row0 >= n_rows) return;
     uint8_t* buf = lds[wave];
     // every lane loads (lanes past the last pair re-read it and ignore it)
     Q80XRaw xr[NX];
     #pragma unroll
     for (int j = 0; j < NX; j++) q80_x_issue(xr[j], xq + (size_t)j * x_row_bytes, min(l, nblk / 2 - 1));
-    const uint32_t rb = (uint32_t)nblk * F::ROW_BLOCK_BYTES, span = 2 * rb;
+    const uint32_t rb = (uint32_t)nblk * F::ROW_BLOCK_BYTES, span = R * rb;
     const i32x4v rs = make_rsrc4(W, w_bytes);
     const uint32_t base = (uint32_t)row0 * rb;
     // every copy instruction is issued (a constant count; lanes past the
@@ -433,19 +435,21 @@ void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const u
         #pragma unroll
         for (int j = 0; j < NX; j++) acc[2 * j] = F::dot(w, x[j], c);
     }
-    wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    if (act) {
-        typename F::Wt w;
-        P::load_w(w, buf + rb, c);
-        #pragma unroll
-        for (int j = 0; j < NX; j++) acc[2 * j + 1] = F::dot(w, x[j], c);
+    if constexpr (R == 2) {
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        if (act) {
+            typename F::Wt w;
+            P::load_w(w, buf + rb, c);
+            #pragma unroll
+            for (int j = 0; j < NX; j++) acc[2 * j + 1] = F::dot(w, x[j], c);
+        }
     }
     if constexpr (NX == 1) {
         const float v = reduce4(acc[0], acc[1], 0.0f, 0.0f);
         if ((l & 31) == 0) {
             const int rr = l >> 5;
-            if (row0 + rr < n_rows) y[row0 + rr] = v;
+            if (rr < R && row0 + rr < n_rows) y[row0 + rr] = v;
         }
     } else {
         constexpr int NA = 2 * NX;
@@ -455,7 +459,7 @@ void gemv_pair32_kernel(const uint8_t* __restrict__ W, uint32_t w_bytes, const u
             if ((l & 15) == 0) {
                 const int f = g + (l == 0 ? 0 : l == 32 ? 1 : l == 16 ? 2 : 3);
                 const int j = f >> 1, rr = f & 1;
-                if (f < NA && row0 + rr < n_rows) y[(size_t)j * n_rows + row0 + rr] = v;
+                if (f < NA && rr < R && row0 + rr < n_rows) y[(size_t)j * n_rows + row0 + rr] = v;
             }
         }
     }
@@ -606,6 +610,17 @@ static hipError_t pair32_launch(const void* W, size_t n_rows, size_t k, const vo
     const uint8_t* x8 = static_cast<const uint8_t*>(xq);
     const uint32_t wb = (uint32_t)(n_rows * (k / 32 * P::F::ROW_BLOCK_BYTES)), xrb = (uint32_t)(k / 32 * Q8_0_BYTES);
     const int n = (int)n_rows, nb = (int)(k / 32);
+    // one token: one weight row per wave up to 1024 rows (measured in one
+    // process, us per call, one row against two: Q4_0 1024 x 4096 2.56 /
+    // 2.68, 4096 x 4096 3.76 / 3.66, 6144 x 4096 4.62 / 4.30; Q8_0 and the
+    // reference's Q4_0 at 4096 x 4096 4.77 / 4.53 and 3.92 / 3.84; outputs
+    // bit-identical).  BARQ_GEMV_LDS = 2 / 3 force two / one.
+    const int mode = tuning_env(TUNE_GEMV_LDS, 1);
+    if (m == 1 && (mode == 3 || (mode == 1 && n_rows <= 1024))) {
+        const dim3 grid1((unsigned)((n_rows + WAVES - 1) / WAVES));
+        hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 1, 1>), grid1, block, 0, s, w8, wb, x8, y, n, nb, xrb);
+        return hipGetLastError();
+    }
     switch (m) {
     case 1: hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 1>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;
     case 2: hipLaunchKernelGGL((gemv_pair32_kernel<P, WAVES, 2>), grid, block, 0, s, w8, wb, x8, y, n, nb, xrb); break;

@@ -179,25 +179,31 @@ def test_gemv_variants(be, orc, w_type):
 
 
 def test_gemv_q4k_lds_equals_register_gemv(be, orc):
-    """The LDS-staged Q4_K GEMV (k <= 4096, the default there) against the
-    register GEMV (BARQ_GEMV_LDS=0), with two and four rows per wave
-    (BARQ_GEMV_LDS=4): bit-identical outputs (same lane slices, arithmetic
-    and reduction), all within the bar of the oracle.  Row counts that are
-    not a multiple of the rows per wave leave the last wave short; short k
-    leaves lanes idle and changes how many copies each row's wait skips."""
+    """The LDS-staged Q4_K GEMV (k <= 4096, the default there: one row per
+    wave up to 4096 rows, two above) against the register GEMV
+    (BARQ_GEMV_LDS=0), with one, two and four rows per wave forced
+    (BARQ_GEMV_LDS=3, 2, 4): bit-identical outputs (same lane slices,
+    arithmetic and reduction), all within the bar of the oracle.  Row counts
+    that are not a multiple of the rows per wave leave the last wave short;
+    short k leaves lanes idle and changes how many copies each row's wait
+    skips; 4096 and 4097 rows sit either side of the default's switch."""
     from conftest import assert_bits_equal
-    for n, k in [(1, 256), (5, 512), (67, 4096), (129, 3840), (1023, 768), (14336, 4096), (3, 4096), (30, 2304)]:
+    for n, k in [(1, 256), (5, 512), (67, 4096), (129, 3840), (1023, 768), (14336, 4096), (3, 4096), (30, 2304),
+                 (4096, 4096), (4097, 4096)]:
         print("q4k lds gemv", n, k, flush=True)
         w, xq, ref = matmul_case(orc, B.Q4_K, n, k, 1, 1300 + n + k)
         wd, xd = dev(w), dev(xq)
         got = be.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
         with env(BARQ_GEMV_LDS=0) as b:
             reg = b.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
-        # four rows per wave: the same per-row arithmetic and reduction
-        with env(BARQ_GEMV_LDS=4) as b:
-            quad = b.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
+        # one, two and four rows per wave: the same per-row arithmetic and reduction
+        forced = {}
+        for mode in (3, 2, 4):
+            with env(BARQ_GEMV_LDS=mode) as b:
+                forced[mode] = b.matvec(B.Q4_K, wd, n, k, B.Q8_K, xd).cpu().numpy()
         assert_bits_equal(got, reg)
-        assert_bits_equal(quad, reg)
+        for mode, y in forced.items():
+            assert_bits_equal(y, reg)
         assert_close_1e3(got, ref.ravel())
 
 
@@ -292,14 +298,17 @@ def test_gemv_32_element_pairs_multi_equal_one_token_gemv(be, orc, name):
 
 @pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_0_BARQ"])
 def test_gemv_32_element_pairs_equal_dma_gemv(be, orc, name):
-    """The two-row LDS-staged GEMV of the 32-element formats (the default for
-    k <= 4096) against the LDS-streamed one-row-per-wave GEMV
+    """The LDS-staged GEMV of the 32-element formats (the default for k <=
+    4096: one weight row per wave up to 1024 rows, two above; BARQ_GEMV_LDS
+    = 3 / 2 force one / two) against the LDS-streamed one-row-per-wave GEMV
     (BARQ_GEMV_LDS=0): bit-identical outputs (same lane slicing, arithmetic
-    and reduction), both within the bar of the oracle; odd row counts leave
-    the last wave one row, short k leaves lanes idle."""
+    and reduction), all within the bar of the oracle; odd row counts leave
+    the last wave one row, short k leaves lanes idle; 1024 and 1025 rows sit
+    either side of the default's switch."""
     from conftest import assert_bits_equal
     t = getattr(B, name)
-    for n, k in [(1, 256), (7, 512), (300, 4096), (4096, 4096), (129, 1280), (64, 3840)]:
+    for n, k in [(1, 256), (7, 512), (300, 4096), (4096, 4096), (129, 1280), (64, 3840), (1024, 4096),
+                 (1025, 2048)]:
         print(f"{name} pair gemv", n, k, flush=True)
         w, xq, ref = matmul_case(orc, t, n, k, 1, 1900 + n + k)
         wd, xd = dev(w), dev(xq)
@@ -307,6 +316,9 @@ def test_gemv_32_element_pairs_equal_dma_gemv(be, orc, name):
         with env(BARQ_GEMV_LDS=0) as b:
             base = b.matvec(t, wd, n, k, B.Q8_PARTNER[t], xd).cpu().numpy()
         assert_bits_equal(got, base)
+        for mode in (3, 2):
+            with env(BARQ_GEMV_LDS=mode) as b:
+                assert_bits_equal(b.matvec(t, wd, n, k, B.Q8_PARTNER[t], xd).cpu().numpy(), base)
         assert_close_1e3(got, ref.ravel())
 
 
