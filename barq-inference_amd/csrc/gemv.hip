@@ -547,12 +547,13 @@ void gemv_q8_glu_kernel(const uint8_t* __restrict__ G, const uint8_t* __restrict
 
 // The fused gate/up GEMV for k <= 4096 staged through LDS (the Q4_K rows'
 // scheme above): a wave copies gate row i and up row i (2304 bytes each at
-// k = 4096) into its own LDS buffer, 3 KB apart, with whole-line
-// non-temporal buffer->LDS loads, its activation slice loaded ahead of the
-// copies by inline asm; the gate row's dot product runs once its three
-// copies have landed.  The arithmetic and reduction are
+// k = 4096) into its own 4.5 KB LDS buffer, the up row right after the gate
+// row, with whole-line non-temporal buffer->LDS loads, its activation slice
+// loaded ahead of the copies by inline asm; the gate row's dot product runs
+// once its three copies have landed.  The arithmetic and reduction are
 // gemv_q8_glu_kernel<FmtQ4K, 1, ...>'s, so h is bit-identical.
-constexpr int GLU_LDS_BUF = 6 * 1024;
+constexpr int GLU_ROW = 2304;                 // a Q4_K row of 4096 elements
+constexpr int GLU_LDS_BUF = 2 * GLU_ROW;      // gate row, then up row
 
 //
 // NX = 2-4 activation rows (x_row_bytes apart; h is [NX x n_rows]): the wave
@@ -576,15 +577,19 @@ void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restric
     for (int j = 0; j < NX; j++) q4k_x_issue(xr[j], xq + (size_t)j * x_row_bytes, min(l >> 2, nblk - 1), l & 3);
     const uint32_t rb = (uint32_t)nblk * Q4_K_BYTES, base = (uint32_t)row * rb;
     const i32x4v gs = make_rsrc4(G, m_bytes), us = make_rsrc4(U, m_bytes);
+    // per row two 1 KB copies and one 256-byte copy (64 lanes x 4 bytes):
+    // the up row right after the gate row, 4.5 KB per wave
     #pragma unroll
-    for (int q = 0; q < 3; q++) {
-        const uint32_t off = 1024u * q + 16u * (uint32_t)l;
-        lds_load16_nt(gs, buf + 1024 * q, off < rb ? base + off : 0x80000000u, 0);
-    }
-    #pragma unroll
-    for (int q = 0; q < 3; q++) {
-        const uint32_t off = 1024u * q + 16u * (uint32_t)l;
-        lds_load16_nt(us, buf + 3072 + 1024 * q, off < rb ? base + off : 0x80000000u, 0);
+    for (int m = 0; m < 2; m++) {
+        const i32x4v rs = m ? us : gs;
+        uint8_t* dst = buf + m * GLU_ROW;
+        #pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint32_t off = 1024u * q + 16u * (uint32_t)l;
+            lds_load16_nt(rs, dst + 1024 * q, off < rb ? base + off : 0x80000000u, 0);
+        }
+        const uint32_t off = 2048u + 4u * (uint32_t)l;
+        lds_load4_nt(rs, dst + 2048, off < rb ? base + off : 0x80000000u, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     const F::Lane c = F::lane(l);
@@ -610,9 +615,9 @@ void gemv_glu_lds_kernel(const uint8_t* __restrict__ G, const uint8_t* __restric
     asm volatile("" ::: "memory");
     if (act) {
         F::Wt w;
-        w.hdr = *reinterpret_cast<const uint4*>(b + 3072);
-        w.q0 = *reinterpret_cast<const uint4*>(b + 3072 + 16 + 32 * c.p);
-        w.q1 = *reinterpret_cast<const uint4*>(b + 3072 + 32 + 32 * c.p);
+        w.hdr = *reinterpret_cast<const uint4*>(b + GLU_ROW);
+        w.q0 = *reinterpret_cast<const uint4*>(b + GLU_ROW + 16 + 32 * c.p);
+        w.q1 = *reinterpret_cast<const uint4*>(b + GLU_ROW + 32 + 32 * c.p);
         #pragma unroll
         for (int j = 0; j < NX; j++) acc[2 * j + 1] = F::dot(w, xs[j], c);
     }

@@ -57,6 +57,11 @@ __device__ __forceinline__ void lds_load4(i32x4v r, void* lds_wave_base, uint32_
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
                  :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
+__device__ __forceinline__ void lds_load4_nt(i32x4v r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen nt lds"
+                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding)
